@@ -1,0 +1,571 @@
+// ehip.hip — the C-ABI device layer (include/ehip.h): weight upload and
+// repacking, per-state device buffers, and the decode / prefill schedules.
+//
+// Decode step (replaces ember_forward, src/model.c:362-414), 5 kernels per
+// layer plus one for the head, all on the state's stream:
+//   qkv   : matvec  RMSNorm(attn_norm) + Q8_0 prologue, [wq;wk;wv] rows,
+//           bias epilogue          (layer 0 also gathers the embedding row)
+//   attn  : fused QK-norm + RoPE + KV store + split-K GQA attention
+//   wo    : matvec  Q8_0 prologue, residual epilogue
+//   w13   : matvec  RMSNorm(ffn_norm) + Q8_0 prologue, [w1;w3] rows, SwiGLU
+//   w2    : matvec  Q8_0 prologue, residual epilogue
+//   head  : matvec  RMSNorm(final_norm) + Q8_0 prologue -> logits
+// The token and position live in device memory, copied from pinned host
+// memory by the first node, so one captured hipGraph replays every step.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../../../include/ehip.h"
+#include "kernels.h"
+
+using namespace ehip;
+
+static thread_local char g_err[512];
+
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+#define HCHK(call, ret)                                                                  \
+    do {                                                                                 \
+        hipError_t e_ = (call);                                                          \
+        if (e_ != hipSuccess) {                                                          \
+            set_err("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return ret;                                                                  \
+        }                                                                                \
+    } while (0)
+
+extern "C" const char *ehip_last_error(void) { return g_err; }
+
+extern "C" int ehip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+// ---------------------------------------------------------------- model ----
+struct DevLayer {
+    DMat qkv, wo, w13, w2;
+    float *attn_norm, *ffn_norm, *q_norm, *k_norm, *bias_qkv;
+};
+
+struct EhipModel {
+    EhipConfig cfg;
+    std::vector<DevLayer> layers;
+    DMat emb, head;
+    float *final_norm, *inv_freq;
+    std::vector<void *> allocs;
+    uint64_t bytes;
+    bool any_f32;
+};
+
+static void *dev_alloc(EhipModel *m, size_t n) {
+    void *p = nullptr;
+    if (hipMalloc(&p, n ? n : 1) != hipSuccess) return nullptr;
+    m->allocs.push_back(p);
+    m->bytes += n;
+    return p;
+}
+
+static size_t file_row_bytes(int dt, int cols) {
+    return dt == DT_F32 ? (size_t)cols * 4 : (size_t)(cols / QB) * (dt == DT_Q8 ? 34 : 18);
+}
+
+// Repack row-concatenated matrices (all of one dtype and width) from the
+// file encoding into the device layout described in dev_common.h.
+static bool upload_mat(EhipModel *m, DMat *out, const EhipWeight *parts, const int *rows, int nparts,
+                       int cols, const char *what) {
+    const int dt = parts[0].dtype;
+    int R = 0;
+    for (int i = 0; i < nparts; i++) {
+        if (!parts[i].data) { set_err("missing tensor for %s", what); return false; }
+        if (parts[i].dtype != dt) { set_err("%s: mixed weight encodings are not supported", what); return false; }
+        R += rows[i];
+    }
+    if (dt != DT_F32 && dt != DT_Q8 && dt != DT_Q4) { set_err("%s: unsupported dtype %d", what, dt); return false; }
+    if (dt != DT_F32 && cols % QB) { set_err("%s: row length %d not a multiple of 32", what, cols); return false; }
+    const int nb = cols / QB;
+    const size_t qrow = dt == DT_F32 ? (size_t)cols * 4 : (dt == DT_Q8 ? (size_t)cols : (size_t)cols / 2);
+    const size_t qbytes = qrow * R, dbytes = dt == DT_F32 ? 0 : (size_t)R * nb * 2;
+    const size_t qpad = (qbytes + 255) & ~(size_t)255;
+    std::vector<uint8_t> host(qpad + dbytes);
+    uint8_t *hq = host.data();
+    uint16_t *hd = reinterpret_cast<uint16_t *>(host.data() + qpad);
+    size_t r0 = 0;
+    for (int p = 0; p < nparts; p++) {
+        const uint8_t *src = static_cast<const uint8_t *>(parts[p].data);
+        const size_t frb = file_row_bytes(dt, cols);
+        for (int r = 0; r < rows[p]; r++, r0++) {
+            const uint8_t *row = src + (size_t)r * frb;
+            if (dt == DT_F32) {
+                memcpy(hq + r0 * qrow, row, qrow);
+                continue;
+            }
+            const size_t bs = dt == DT_Q8 ? 34 : 18, pay = bs - 2;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *blk = row + (size_t)b * bs;
+                uint16_t d;
+                memcpy(&d, blk, 2);
+                hd[r0 * nb + b] = d;
+                memcpy(hq + r0 * qrow + (size_t)b * pay, blk + 2, pay);
+            }
+        }
+    }
+    uint8_t *dev = static_cast<uint8_t *>(dev_alloc(m, host.size()));
+    if (!dev) { set_err("hipMalloc of %zu bytes for %s failed", host.size(), what); return false; }
+    HCHK(hipMemcpy(dev, host.data(), host.size(), hipMemcpyHostToDevice), false);
+    out->dtype = dt; out->rows = R; out->cols = cols;
+    out->q = dev;
+    out->d = dt == DT_F32 ? nullptr : reinterpret_cast<const uint16_t *>(dev + qpad);
+    if (dt == DT_F32) m->any_f32 = true;
+    return true;
+}
+
+static float *upload_f32(EhipModel *m, const float *const *parts, const int *lens, int nparts) {
+    size_t n = 0;
+    for (int i = 0; i < nparts; i++) n += lens[i];
+    std::vector<float> host(n, 0.0f);
+    size_t o = 0;
+    for (int i = 0; i < nparts; i++) {
+        if (parts[i]) memcpy(host.data() + o, parts[i], lens[i] * sizeof(float));
+        o += lens[i];
+    }
+    float *dev = static_cast<float *>(dev_alloc(m, n * 4));
+    if (!dev) { set_err("hipMalloc of %zu bytes failed", n * 4); return nullptr; }
+    if (hipMemcpy(dev, host.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        set_err("hipMemcpy of a vector failed");
+        return nullptr;
+    }
+    return dev;
+}
+
+extern "C" void ehip_model_free(EhipModel *m) {
+    if (!m) return;
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+extern "C" uint64_t ehip_model_bytes(const EhipModel *m) { return m ? m->bytes : 0; }
+
+extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *layers, EhipWeight tok_emb,
+                                        EhipWeight lm_head, const float *final_norm,
+                                        const float *rope_inv_freq) {
+    const EhipConfig &c = *cfg;
+    const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) { set_err("n_heads must be a multiple of n_kv_heads"); return nullptr; }
+    if (hd != 48 && hd != 64 && hd != 128) { set_err("head_dim %d not supported by the attention kernel", hd); return nullptr; }
+    if (c.n_heads / c.n_kv_heads > 8) { set_err("more than 8 query heads per kv head"); return nullptr; }
+    if (tok_emb.dtype != DT_F32 && tok_emb.dtype != DT_Q8) { set_err("embedding must be F32 or Q8_0"); return nullptr; }
+    EhipModel *m = new EhipModel();
+    m->cfg = c;
+    m->bytes = 0;
+    m->any_f32 = false;
+    int hiprc = hipSetDevice(0);
+    if (hiprc != hipSuccess) { set_err("hipSetDevice(0) failed: no usable GPU"); delete m; return nullptr; }
+    m->layers.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        const EhipLayer &y = layers[l];
+        DevLayer &d = m->layers[l];
+        char what[64];
+        snprintf(what, sizeof what, "layer %d qkv", l);
+        EhipWeight qkv[3] = { y.wq, y.wk, y.wv };
+        int qkv_rows[3] = { qd, kvd, kvd };
+        if (!upload_mat(m, &d.qkv, qkv, qkv_rows, 3, c.dim, what)) goto fail;
+        snprintf(what, sizeof what, "layer %d wo", l);
+        if (!upload_mat(m, &d.wo, &y.wo, &c.dim, 1, qd, what)) goto fail;
+        {
+            EhipWeight w13[2] = { y.w1, y.w3 };
+            int rows13[2] = { c.hidden_dim, c.hidden_dim };
+            snprintf(what, sizeof what, "layer %d w1|w3", l);
+            if (!upload_mat(m, &d.w13, w13, rows13, 2, c.dim, what)) goto fail;
+        }
+        snprintf(what, sizeof what, "layer %d w2", l);
+        if (!upload_mat(m, &d.w2, &y.w2, &c.dim, 1, c.hidden_dim, what)) goto fail;
+        {
+            const float *an = y.attn_norm, *fn = y.ffn_norm;
+            if (!(d.attn_norm = upload_f32(m, &an, &c.dim, 1))) goto fail;
+            if (!(d.ffn_norm = upload_f32(m, &fn, &c.dim, 1))) goto fail;
+            d.q_norm = d.k_norm = nullptr;
+            if (c.qk_norm && y.q_norm) {
+                if (!y.k_norm) { set_err("layer %d has q_norm but no k_norm", l); goto fail; }
+                if (!(d.q_norm = upload_f32(m, &y.q_norm, &hd, 1))) goto fail;
+                if (!(d.k_norm = upload_f32(m, &y.k_norm, &hd, 1))) goto fail;
+            }
+            d.bias_qkv = nullptr;
+            if (y.bq || y.bk || y.bv) {
+                const float *bp[3] = { y.bq, y.bk, y.bv };
+                int bl[3] = { qd, kvd, kvd };
+                if (!(d.bias_qkv = upload_f32(m, bp, bl, 3))) goto fail;
+            }
+        }
+    }
+    {
+        if (!upload_mat(m, &m->emb, &tok_emb, &c.vocab_size, 1, c.dim, "tok_embeddings")) goto fail;
+        if (lm_head.data == tok_emb.data) m->head = m->emb;
+        else if (!upload_mat(m, &m->head, &lm_head, &c.vocab_size, 1, c.dim, "lm_head")) goto fail;
+        if (!(m->final_norm = upload_f32(m, &final_norm, &c.dim, 1))) goto fail;
+        int half = hd / 2;
+        if (!(m->inv_freq = upload_f32(m, &rope_inv_freq, &half, 1))) goto fail;
+    }
+    return m;
+fail:
+    ehip_model_free(m);
+    return nullptr;
+}
+
+// ---------------------------------------------------------------- state ----
+constexpr int PF_CHUNK = 256;  // prefill tokens per pass through the layers
+
+struct EhipState {
+    EhipModel *m;
+    int ctx, f16kv, esize, graph_mode;
+    hipStream_t st;
+    void *kc, *vc;
+    int *tokpos_d, *tokpos_h;
+    float *x, *qkv, *o, *h, *logits_d, *logits_h;
+    float *part; unsigned *ctr;
+    int mc_dec, min_chunk_dec;
+    // prefill scratch
+    float *X, *QKV, *O, *H, *xf, *dxp, *part_pf;
+    int8_t *qx; int *xsum, *ids_d; unsigned *ctr_pf;
+    int mc_pf;
+    hipGraph_t graph; hipGraphExec_t gexec;
+    hipEvent_t ev0, ev1;
+    std::vector<void *> allocs;
+};
+
+static void *salloc(EhipState *s, size_t n, bool zero = false) {
+    void *p = nullptr;
+    if (hipMalloc(&p, n ? n : 1) != hipSuccess) return nullptr;
+    if (zero && hipMemset(p, 0, n ? n : 1) != hipSuccess) { (void)hipFree(p); return nullptr; }
+    s->allocs.push_back(p);
+    return p;
+}
+
+extern "C" void ehip_state_destroy(EhipState *s) {
+    if (!s) return;
+    (void)hipStreamSynchronize(s->st);
+    if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    for (void *p : s->allocs) (void)hipFree(p);
+    if (s->tokpos_h) (void)hipHostFree(s->tokpos_h);
+    if (s->logits_h) (void)hipHostFree(s->logits_h);
+    if (s->ev0) (void)hipEventDestroy(s->ev0);
+    if (s->ev1) (void)hipEventDestroy(s->ev1);
+    (void)hipStreamDestroy(s->st);
+    delete s;
+}
+
+static int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
+    const EhipConfig &c = m->cfg;
+    const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    EhipState *s = new EhipState();  // value-initialised: every pointer starts null
+    s->m = m; s->ctx = ctx; s->f16kv = kv_fp16 ? 1 : 0; s->esize = kv_fp16 ? 2 : 4;
+    s->graph_mode = env_int("EHIP_GRAPH", 1);
+    if (hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking) != hipSuccess) {
+        set_err("hipStreamCreate failed");
+        delete s;
+        return nullptr;
+    }
+    const size_t kvb = (size_t)c.n_layers * ctx * kvd * s->esize;
+    const int need = (ctx + ATT_CHUNK_MAX - 1) / ATT_CHUNK_MAX;
+    const int target_wg = env_int("EHIP_ATT_WGS", 512);
+    s->mc_dec = std::max(need, (target_wg + c.n_kv_heads - 1) / c.n_kv_heads);
+    s->min_chunk_dec = env_int("EHIP_ATT_MIN_CHUNK", 32);
+    s->mc_pf = need;
+    const int wide = std::max(std::max(c.dim, c.hidden_dim), qd);
+    bool ok = (s->kc = salloc(s, kvb, true)) && (s->vc = salloc(s, kvb, true)) &&
+              (s->tokpos_d = (int *)salloc(s, 8, true)) &&
+              (s->x = (float *)salloc(s, 4 * (size_t)c.dim)) &&
+              (s->qkv = (float *)salloc(s, 4 * (size_t)(qd + 2 * kvd))) &&
+              (s->o = (float *)salloc(s, 4 * (size_t)qd)) &&
+              (s->h = (float *)salloc(s, 4 * (size_t)c.hidden_dim)) &&
+              (s->logits_d = (float *)salloc(s, 4 * (size_t)c.vocab_size, true)) &&
+              (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * s->mc_dec * (hd + 2))) &&
+              (s->ctr = (unsigned *)salloc(s, 4 * (size_t)c.n_kv_heads, true)) &&
+              (s->X = (float *)salloc(s, 4 * (size_t)PF_CHUNK * c.dim)) &&
+              (s->QKV = (float *)salloc(s, 4 * (size_t)PF_CHUNK * (qd + 2 * kvd))) &&
+              (s->O = (float *)salloc(s, 4 * (size_t)PF_CHUNK * qd)) &&
+              (s->H = (float *)salloc(s, 4 * (size_t)PF_CHUNK * 2 * c.hidden_dim)) &&
+              (s->qx = (int8_t *)salloc(s, (size_t)PF_CHUNK * wide)) &&
+              (s->dxp = (float *)salloc(s, 4 * (size_t)PF_CHUNK * (wide / QB + 1))) &&
+              (s->xsum = (int *)salloc(s, 4 * (size_t)PF_CHUNK * (wide / QB + 1))) &&
+              (s->ids_d = (int *)salloc(s, 4 * (size_t)PF_CHUNK)) &&
+              (s->part_pf = (float *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_heads * s->mc_pf * (hd + 2))) &&
+              (s->ctr_pf = (unsigned *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_kv_heads, true));
+    if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * (size_t)PF_CHUNK * wide)) != nullptr;
+    if (!ok) {
+        set_err("device allocation for a state with ctx %d failed (KV %zu bytes)", ctx, 2 * kvb);
+        ehip_state_destroy(s);
+        return nullptr;
+    }
+    if (hipHostMalloc(&s->tokpos_h, 8, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(&s->logits_h, 4 * (size_t)c.vocab_size, hipHostMallocDefault) != hipSuccess ||
+        hipEventCreate(&s->ev0) != hipSuccess || hipEventCreate(&s->ev1) != hipSuccess) {
+        set_err("pinned host allocation failed");
+        ehip_state_destroy(s);
+        return nullptr;
+    }
+    memset(s->logits_h, 0, 4 * (size_t)c.vocab_size);
+    return s;
+}
+
+// ------------------------------------------------------------ schedules ----
+static AttnArgs attn_args(EhipState *s, int l) {
+    const EhipConfig &c = s->m->cfg;
+    const DevLayer &y = s->m->layers[l];
+    const int kvd = c.n_kv_heads * c.head_dim;
+    AttnArgs a{};
+    a.q_norm = y.q_norm; a.k_norm = y.k_norm; a.inv_freq = s->m->inv_freq;
+    a.eps = c.norm_eps; a.inv_sqrt = 1.0f / sqrtf((float)c.head_dim);
+    a.rope_style = c.rope_style;
+    const size_t loff = (size_t)l * s->ctx * kvd * s->esize;
+    a.kc = static_cast<uint8_t *>(s->kc) + loff;
+    a.vc = static_cast<uint8_t *>(s->vc) + loff;
+    a.kv_dim = kvd; a.hd = c.head_dim; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.ctx = s->ctx;
+    return a;
+}
+
+static int enq_attn_decode(EhipState *s, int l) {
+    AttnArgs a = attn_args(s, l);
+    a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
+    a.part = s->part; a.counters = s->ctr; a.max_chunks = s->mc_dec; a.min_chunk = s->min_chunk_dec;
+    a.out = s->o;
+    return launch_attention(s->st, true, s->f16kv, a);
+}
+
+static int enq_head(EhipState *s, const float *xin) {
+    const EhipModel *m = s->m;
+    MatvecArgs a{};
+    a.W = m->head; a.units = m->cfg.vocab_size; a.in = xin; a.norm_w = m->final_norm;
+    a.eps = m->cfg.norm_eps; a.out = s->logits_d;
+    return launch_matvec(s->st, PRO_NORM, EPI_STORE, a);
+}
+
+static int enq_w13(EhipState *s, int l) {
+    const EhipModel *m = s->m;
+    const DevLayer &y = m->layers[l];
+    MatvecArgs a{};
+    a.W = y.w13; a.units = m->cfg.hidden_dim; a.pair_off = m->cfg.hidden_dim;
+    a.in = s->x; a.norm_w = y.ffn_norm; a.eps = m->cfg.norm_eps; a.out = s->h;
+    return launch_matvec(s->st, PRO_NORM, EPI_SWIGLU, a);
+}
+
+// All launches of one decode step (the tokpos copy is the caller's).
+static int enq_decode(EhipState *s) {
+    const EhipModel *m = s->m;
+    const EhipConfig &c = m->cfg;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    for (int l = 0; l < c.n_layers; l++) {
+        const DevLayer &y = m->layers[l];
+        MatvecArgs a{};
+        a.W = y.qkv; a.units = qd + 2 * kvd; a.in = s->x; a.norm_w = y.attn_norm; a.eps = c.norm_eps;
+        a.tokpos = s->tokpos_d; a.emb = m->emb; a.x_out = s->x; a.out = s->qkv; a.bias = y.bias_qkv;
+        if (launch_matvec(s->st, l == 0 ? PRO_EMBED_NORM : PRO_NORM, EPI_STORE, a)) return -1;
+        if (enq_attn_decode(s, l)) return -1;
+        MatvecArgs b{};
+        b.W = y.wo; b.units = c.dim; b.in = s->o; b.out = s->x;
+        if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, b)) return -1;
+        if (enq_w13(s, l)) return -1;
+        MatvecArgs d{};
+        d.W = y.w2; d.units = c.dim; d.in = s->h; d.out = s->x;
+        if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, d)) return -1;
+    }
+    return enq_head(s, s->x);
+}
+
+static int enq_step(EhipState *s) {
+    const int V = s->m->cfg.vocab_size;
+    HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 8, hipMemcpyHostToDevice, s->st), -1);
+    if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
+    HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * (size_t)V, hipMemcpyDeviceToHost, s->st), -1);
+    return 0;
+}
+
+static int run_step(EhipState *s) {
+    if (s->graph_mode) {
+        if (!s->gexec) {
+            HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), -1);
+            int rc = enq_step(s);
+            hipGraph_t g = nullptr;
+            hipError_t e = hipStreamEndCapture(s->st, &g);
+            if (rc) { if (g) (void)hipGraphDestroy(g); return -1; }
+            if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return -1; }
+            s->graph = g;
+            HCHK(hipGraphInstantiate(&s->gexec, g, nullptr, nullptr, 0), -1);
+        }
+        HCHK(hipGraphLaunch(s->gexec, s->st), -1);
+    } else if (enq_step(s)) {
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" float *ehip_forward(EhipState *s, int tok, int pos) {
+    s->tokpos_h[0] = tok;
+    s->tokpos_h[1] = pos;
+    if (run_step(s)) return nullptr;
+    HCHK(hipStreamSynchronize(s->st), nullptr);
+    return s->logits_h;
+}
+
+extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
+    const EhipModel *m = s->m;
+    const EhipConfig &c = m->cfg;
+    const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd, hid = c.hidden_dim;
+    const int stride = qd + 2 * kvd;
+    for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {
+        const int mt = std::min(PF_CHUNK, n - c0);
+        HCHK(hipMemcpyAsync(s->ids_d, ids + c0, 4 * (size_t)mt, hipMemcpyHostToDevice, s->st), nullptr);
+        for (int l = 0; l < c.n_layers; l++) {
+            const DevLayer &y = m->layers[l];
+            QuantRowsArgs q{};
+            q.x = s->X; q.x_stride = c.dim; q.cols = c.dim; q.n = mt;
+            q.norm_w = y.attn_norm; q.eps = c.norm_eps;
+            if (l == 0) { q.ids = s->ids_d; q.emb = m->emb; q.x_out = s->X; }
+            q.xf = m->any_f32 ? s->xf : nullptr; q.qx = s->qx; q.dx = s->dxp; q.xs = s->xsum;
+            int rc = launch_quant_rows(s->st, q);
+            GemmArgs g{};
+            g.W = y.qkv; g.units = stride; g.n = mt; g.qx = s->qx; g.dx = s->dxp; g.xs = s->xsum; g.xf = q.xf;
+            g.out = s->QKV; g.out_stride = stride; g.bias = y.bias_qkv;
+            rc |= launch_gemm(s->st, EPI_STORE, g);
+            QkPostArgs p{};
+            p.qkv = s->QKV; p.stride = stride; p.q_norm = y.q_norm; p.k_norm = y.k_norm;
+            p.inv_freq = m->inv_freq; p.eps = c.norm_eps; p.rope_style = c.rope_style;
+            AttnArgs at = attn_args(s, l);
+            p.kc = at.kc; p.vc = at.vc; p.kv_dim = kvd; p.hd = hd; p.n_heads = c.n_heads;
+            p.n_kv = c.n_kv_heads; p.pos_base = start + c0; p.n_tok = mt;
+            rc |= launch_qkpost(s->st, s->f16kv, p);
+            at.q = s->QKV; at.q_stride = stride; at.pos_base = start + c0; at.n_tok = mt;
+            at.part = s->part_pf; at.counters = s->ctr_pf; at.max_chunks = s->mc_pf;
+            at.min_chunk = ATT_CHUNK_MAX; at.out = s->O;
+            rc |= launch_attention(s->st, false, s->f16kv, at);
+            QuantRowsArgs q2{};
+            q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;
+            q2.xf = q.xf; q2.qx = s->qx; q2.dx = s->dxp; q2.xs = s->xsum;
+            rc |= launch_quant_rows(s->st, q2);
+            GemmArgs g2{};
+            g2.W = y.wo; g2.units = c.dim; g2.n = mt; g2.qx = s->qx; g2.dx = s->dxp; g2.xs = s->xsum;
+            g2.xf = q.xf; g2.out = s->X; g2.out_stride = c.dim;
+            rc |= launch_gemm(s->st, EPI_RESID, g2);
+            QuantRowsArgs q3 = q;
+            q3.ids = nullptr; q3.norm_w = y.ffn_norm;
+            rc |= launch_quant_rows(s->st, q3);
+            GemmArgs g3{};
+            g3.W = y.w13; g3.units = 2 * hid; g3.n = mt; g3.qx = s->qx; g3.dx = s->dxp; g3.xs = s->xsum;
+            g3.xf = q.xf; g3.out = s->H; g3.out_stride = 2 * hid;
+            rc |= launch_gemm(s->st, EPI_STORE, g3);
+            QuantRowsArgs q4{};
+            q4.x = s->H; q4.x_stride = 2 * hid; q4.cols = hid; q4.n = mt; q4.swiglu = 1;
+            q4.xf = q.xf; q4.qx = s->qx; q4.dx = s->dxp; q4.xs = s->xsum;
+            rc |= launch_quant_rows(s->st, q4);
+            GemmArgs g4{};
+            g4.W = y.w2; g4.units = c.dim; g4.n = mt; g4.qx = s->qx; g4.dx = s->dxp; g4.xs = s->xsum;
+            g4.xf = q.xf; g4.out = s->X; g4.out_stride = c.dim;
+            rc |= launch_gemm(s->st, EPI_RESID, g4);
+            if (rc) { set_err("a prefill kernel could not be launched for this shape"); return nullptr; }
+        }
+        if (c0 + mt == n) {
+            if (enq_head(s, s->X + (size_t)(mt - 1) * c.dim)) { set_err("head launch failed"); return nullptr; }
+            HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * (size_t)c.vocab_size, hipMemcpyDeviceToHost, s->st), nullptr);
+        }
+    }
+    HCHK(hipStreamSynchronize(s->st), nullptr);
+    return s->logits_h;
+}
+
+// ------------------------------------------------------- inspection ----
+extern "C" int ehip_kv_read(EhipState *s, int which, int layer, int n_pos, void *host) {
+    const EhipConfig &c = s->m->cfg;
+    const size_t row = (size_t)c.n_kv_heads * c.head_dim * s->esize;
+    if (layer < 0 || layer >= c.n_layers || n_pos < 0 || n_pos > s->ctx) { set_err("kv_read out of range"); return -1; }
+    const uint8_t *base = static_cast<const uint8_t *>(which ? s->vc : s->kc) + (size_t)layer * s->ctx * row;
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipMemcpy(host, base, row * n_pos, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
+extern "C" int ehip_kv_write(EhipState *s, int which, int layer, int n_pos, const void *host) {
+    const EhipConfig &c = s->m->cfg;
+    const size_t row = (size_t)c.n_kv_heads * c.head_dim * s->esize;
+    if (layer < 0 || layer >= c.n_layers || n_pos < 0 || n_pos > s->ctx) { set_err("kv_write out of range"); return -1; }
+    uint8_t *base = static_cast<uint8_t *>(which ? s->vc : s->kc) + (size_t)layer * s->ctx * row;
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipMemcpy(base, host, row * n_pos, hipMemcpyHostToDevice), -1);
+    return 0;
+}
+
+extern "C" int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t bytes) {
+    const EhipConfig &c = s->m->cfg;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const void *src[5] = { s->x, s->qkv, s->o, s->h, s->logits_d };
+    const uint64_t len[5] = { 4ull * c.dim, 4ull * (qd + 2 * kvd), 4ull * qd, 4ull * c.hidden_dim,
+                              4ull * c.vocab_size };
+    if (which < 0 || which > 4 || bytes > len[which]) { set_err("debug_buffer: bad request"); return -1; }
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipMemcpy(host, src[which], bytes, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
+extern "C" int ehip_set_graph_mode(EhipState *s, int mode) {
+    s->graph_mode = mode ? 1 : 0;
+    return 0;
+}
+
+extern "C" int ehip_time_decode(EhipState *s, int pos0, int steps, float *ms) {
+    const int V = s->m->cfg.vocab_size;
+    if (pos0 < 0 || pos0 + steps > s->ctx || steps <= 0) { set_err("time_decode: positions out of range"); return -1; }
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipEventRecord(s->ev0, s->st), -1);
+    for (int i = 0; i < steps; i++) {
+        const int pos = pos0 + i;
+        s->tokpos_h[0] = (int)(((long)pos * 131 + 7) % V);
+        s->tokpos_h[1] = pos;
+        if (run_step(s)) return -1;
+        HCHK(hipStreamSynchronize(s->st), -1);
+    }
+    HCHK(hipEventRecord(s->ev1, s->st), -1);
+    HCHK(hipEventSynchronize(s->ev1), -1);
+    float t = 0.0f;
+    HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
+    *ms = t / steps;
+    return 0;
+}
+
+extern "C" int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms) {
+    if (pos < 0 || pos >= s->ctx || reps <= 0) { set_err("time_kernel: bad arguments"); return -1; }
+    s->tokpos_h[0] = 0;
+    s->tokpos_h[1] = pos;
+    HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 8, hipMemcpyHostToDevice, s->st), -1);
+    auto one = [&]() -> int {
+        if (kernel == 0) return enq_attn_decode(s, 0);
+        if (kernel == 1) return enq_head(s, s->x);
+        if (kernel == 2) return enq_w13(s, 0);
+        return -1;
+    };
+    if (one()) { set_err("time_kernel: unknown kernel %d", kernel); return -1; }  // warm-up
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipEventRecord(s->ev0, s->st), -1);
+    for (int i = 0; i < reps; i++) if (one()) return -1;
+    HCHK(hipEventRecord(s->ev1, s->st), -1);
+    HCHK(hipEventSynchronize(s->ev1), -1);
+    float t = 0.0f;
+    HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
+    *ms = t / reps;
+    return 0;
+}

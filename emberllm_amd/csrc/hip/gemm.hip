@@ -1,0 +1,211 @@
+// gemm.hip — batched prefill products for gfx950.
+//
+// Replaces ember_matmul_batch -> mmb_rows (src/kernels.c:223-264) and the
+// per-token RMSNorm / SwiGLU / embedding loops of ember_prefill
+// (src/model.c:305-351).
+//
+// k_quant_rows: one workgroup per token row builds the Q8_0 activation codes
+// (optionally after the embedding lookup, an RMSNorm or the SwiGLU gate).
+// k_gemm: a 64 (units) x 64 (tokens) output tile per workgroup, walking K one
+// 32-weight quant block at a time.  Each thread owns a 4 x 4 micro-tile and
+// accumulates the block products in block order, (acc * dw) * dx, the same
+// order as vecdot_q8 / vecdot_q4 (kernels.c:151-183).
+#include "kernels.h"
+
+namespace ehip {
+
+__global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *xs = reinterpret_cast<float *>(smem);
+    __shared__ float red[NWAVE];
+    const int K = a.cols, nb = K / QB, b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.0f;
+    if (a.ids) {
+        const int tok = a.ids[b];
+        for (int i = tid; i < K; i += WG) {
+            float v;
+            if (a.emb.dtype == DT_F32) v = reinterpret_cast<const float *>(a.emb.q)[(size_t)tok * K + i];
+            else v = (float)reinterpret_cast<const int8_t *>(a.emb.q)[(size_t)tok * K + i] *
+                     h2f(a.emb.d[(size_t)tok * nb + i / QB]);
+            xs[i] = v; ss += v * v;
+            a.x_out[(size_t)b * K + i] = v;
+        }
+    } else if (a.swiglu) {
+        const float *row = a.x + (size_t)b * a.x_stride;
+        for (int i = tid; i < K; i += WG) {
+            const float g = row[i];
+            const float v = g / (1.0f + expf(-g)) * row[K + i];
+            xs[i] = v; ss += v * v;
+        }
+    } else {
+        const float *row = a.x + (size_t)b * a.x_stride;
+        for (int i = tid; i < K; i += WG) { const float v = row[i]; xs[i] = v; ss += v * v; }
+    }
+    if (a.norm_w) {
+        const float tot = block_sum(ss, red);
+        const float scale = 1.0f / sqrtf(tot / (float)K + a.eps);
+        for (int i = tid; i < K; i += WG) xs[i] = xs[i] * scale * a.norm_w[i];
+    }
+    __syncthreads();
+    if (a.xf)
+        for (int i = tid; i < K; i += WG) a.xf[(size_t)b * K + i] = xs[i];
+    if (a.qx) {
+        for (int blk = wave * 2 + (lane >> 5); blk < nb; blk += NWAVE * 2) {
+            float dq;
+            const int q = quant_q8_lane(xs[blk * QB + (lane & 31)], &dq);
+            a.qx[(size_t)b * K + blk * QB + (lane & 31)] = (int8_t)q;
+            int s = q;
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off);
+            if ((lane & 31) == 0) {
+                a.dx[(size_t)b * nb + blk] = dq;
+                a.xs[(size_t)b * nb + blk] = s;
+            }
+        }
+    }
+}
+
+int launch_quant_rows(hipStream_t st, const QuantRowsArgs &a) {
+    if (a.cols % QB != 0 || (size_t)a.cols * 4 > 64 * 1024 || a.n <= 0) return -1;
+    hipLaunchKernelGGL(k_quant_rows, dim3(a.n), dim3(WG), (size_t)a.cols * 4, st, a);
+    return 0;
+}
+
+// --------------------------------------------------------------------------
+constexpr int TM = 64, TN = 64;
+
+template <int DT, int EPI>
+__global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
+    // one K-block of the tile: weights, activations, their scales
+    __shared__ __align__(16) uint8_t ws[TM * (DT == DT_F32 ? 128 : 32)];
+    __shared__ __align__(16) uint8_t xsm[TN * (DT == DT_F32 ? 128 : 32)];
+    __shared__ float dws[TM], dxs[TN];
+    __shared__ int sums[TN];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int u0 = blockIdx.x * TM, b0 = blockIdx.y * TN;
+    const int K = a.W.cols, nb = K / QB;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+
+    for (int blk = 0; blk < nb; blk++) {
+        if (DT == DT_F32) {
+            // 64 rows x 32 floats each for W and X: 512 float4 apiece
+            for (int i = tid; i < TM * 8; i += WG) {
+                const int r = i >> 3, p = i & 7;
+                const int u = u0 + r;
+                float4 w = make_float4(0, 0, 0, 0);
+                if (u < a.units)
+                    w = reinterpret_cast<const float4 *>(a.W.q)[((size_t)u * K + blk * QB) / 4 + p];
+                reinterpret_cast<float4 *>(ws)[i] = w;
+                const int t = b0 + r;
+                float4 x = make_float4(0, 0, 0, 0);
+                if (t < a.n) x = reinterpret_cast<const float4 *>(a.xf)[((size_t)t * K + blk * QB) / 4 + p];
+                reinterpret_cast<float4 *>(xsm)[i] = x;
+            }
+        } else {
+            if (tid < 128) {
+                const int r = tid >> 1, h = tid & 1;
+                const int u = u0 + r, t = b0 + r;
+                int4 w = make_int4(0, 0, 0, 0), x = make_int4(0, 0, 0, 0);
+                if (DT == DT_Q8) {
+                    if (u < a.units) w = *reinterpret_cast<const int4 *>(a.W.q + (size_t)u * K + blk * QB + h * 16);
+                    reinterpret_cast<int4 *>(ws)[tid] = w;
+                } else if (h == 0) {
+                    if (u < a.units) w = *reinterpret_cast<const int4 *>(a.W.q + (size_t)u * (K / 2) + blk * 16);
+                    reinterpret_cast<int4 *>(ws)[r] = w;
+                }
+                if (t < a.n) x = *reinterpret_cast<const int4 *>(a.qx + (size_t)t * K + blk * QB + h * 16);
+                reinterpret_cast<int4 *>(xsm)[tid] = x;
+            } else if (tid < 192) {
+                const int u = u0 + tid - 128;
+                dws[tid - 128] = u < a.units ? h2f(a.W.d[(size_t)u * nb + blk]) : 0.0f;
+            } else {
+                const int t = b0 + tid - 192;
+                dxs[tid - 192] = t < a.n ? a.dx[(size_t)t * nb + blk] : 0.0f;
+                sums[tid - 192] = (DT == DT_Q4 && t < a.n) ? a.xs[(size_t)t * nb + blk] : 0;
+            }
+        }
+        __syncthreads();
+        if (DT == DT_F32) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float *w = reinterpret_cast<const float *>(ws) + (tx * 4 + i) * QB;
+                    const float *x = reinterpret_cast<const float *>(xsm) + (ty * 4 + j) * QB;
+                    float s = acc[i][j];
+                    for (int k = 0; k < QB; k++) s += w[k] * x[k];  // dot_f32 order
+                    acc[i][j] = s;
+                }
+        } else {
+            int xv[4][8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int4 *xp = reinterpret_cast<const int4 *>(xsm) + (ty * 4 + j) * 2;
+                const int4 lo = xp[0], hi = xp[1];
+                xv[j][0] = lo.x; xv[j][1] = lo.y; xv[j][2] = lo.z; xv[j][3] = lo.w;
+                xv[j][4] = hi.x; xv[j][5] = hi.y; xv[j][6] = hi.z; xv[j][7] = hi.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = tx * 4 + i;
+                int wv[8];
+                if (DT == DT_Q8) {
+                    const int4 *wp = reinterpret_cast<const int4 *>(ws) + r * 2;
+                    const int4 lo = wp[0], hi = wp[1];
+                    wv[0] = lo.x; wv[1] = lo.y; wv[2] = lo.z; wv[3] = lo.w;
+                    wv[4] = hi.x; wv[5] = hi.y; wv[6] = hi.z; wv[7] = hi.w;
+                } else {
+                    const int4 p = reinterpret_cast<const int4 *>(ws)[r];
+                    const int m = 0x0f0f0f0f;
+                    wv[0] = p.x & m; wv[1] = p.y & m; wv[2] = p.z & m; wv[3] = p.w & m;
+                    wv[4] = (p.x >> 4) & m; wv[5] = (p.y >> 4) & m; wv[6] = (p.z >> 4) & m; wv[7] = (p.w >> 4) & m;
+                }
+                const float dw = dws[r];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    int d = 0;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) d = sdot4(wv[k], xv[j][k], d);
+                    if (DT == DT_Q4) d -= 8 * sums[ty * 4 + j];
+                    acc[i][j] += ((float)d * dw) * dxs[ty * 4 + j];
+                }
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int u = u0 + tx * 4 + i;
+        if (u >= a.units) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int t = b0 + ty * 4 + j;
+            if (t >= a.n) continue;
+            float *o = a.out + (size_t)t * a.out_stride + u;
+            if (EPI == EPI_STORE) *o = a.bias ? acc[i][j] + a.bias[u] : acc[i][j];
+            else *o += acc[i][j];
+        }
+    }
+}
+
+int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
+    if (a.W.cols % QB != 0 || a.n <= 0) return -1;
+    dim3 grid((a.units + TM - 1) / TM, (a.n + TN - 1) / TN);
+#define G(DT)                                                                              \
+    if (a.W.dtype == DT) {                                                                 \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm<DT, EPI_STORE>), grid, dim3(WG), 0, st, a); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm<DT, EPI_RESID>), grid, dim3(WG), 0, st, a); \
+        else return -1;                                                                    \
+        return 0;                                                                          \
+    }
+    G(DT_Q8) G(DT_Q4) G(DT_F32)
+#undef G
+    return -1;
+}
+
+}  // namespace ehip

@@ -1,0 +1,97 @@
+// kernels.h — launch interface of the gfx950 kernels (host side, C++).
+#pragma once
+#include "dev_common.h"
+
+namespace ehip {
+
+// ---------------------------------------------------------------- matvec --
+// One decode-step matrix-vector product with a fused prologue and epilogue:
+//   prologue  PRO_NORM        x' = rmsnorm(in) then Q8_0-quantize x'
+//             PRO_PLAIN       Q8_0-quantize in
+//             PRO_EMBED_NORM  in = embedding row of the device token, written
+//                             to x_out, then as PRO_NORM
+//   epilogue  EPI_STORE   out[r] = W[r].x' (+ bias[r])
+//             EPI_RESID   out[r] += W[r].x'
+//             EPI_SWIGLU  out[u] = silu(W[u].x') * W[u+pair_off].x'
+enum { PRO_NORM = 0, PRO_PLAIN = 1, PRO_EMBED_NORM = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+
+struct MatvecArgs {
+    DMat W;
+    int units;            // number of outputs
+    int pair_off;         // EPI_SWIGLU: row offset of the second matrix
+    const float *in;      // [W.cols]
+    const float *norm_w;  // [W.cols]
+    float eps;
+    const int *tokpos;    // device {tok, pos}
+    DMat emb;             // embedding table (PRO_EMBED_NORM)
+    float *x_out;
+    float *out;
+    const float *bias;
+};
+int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
+
+// ------------------------------------------------------------- attention --
+// GQA attention of n_tok query tokens against the cache, split over chunks
+// of positions (flash-decoding); the last workgroup of each (token, kv head)
+// combines the chunk partials.  With `fused`, the single token's raw q/k/v
+// (straight out of the QKV matvec) is QK-normed and rotated in the prologue
+// and its k/v are written to the cache at `pos` by the chunk that owns it.
+struct AttnArgs {
+    const float *q;        // fused: raw q|k|v row; else rotated Q rows
+    int q_stride;          // floats between consecutive tokens' q
+    const float *q_norm, *k_norm;  // [hd] or nullptr
+    const float *inv_freq;         // [hd/2]
+    float eps, inv_sqrt;
+    int rope_style;
+    void *kc, *vc;         // layer cache base, [ctx][kv_dim]
+    int kv_dim, hd, n_heads, n_kv, ctx;
+    const int *tokpos;     // fused (decode): device {tok, pos}
+    int pos_base;          // unfused (prefill): token b sits at pos_base + b
+    int n_tok;
+    float *part;           // [n_tok][n_heads][max_chunks][hd + 2]
+    unsigned *counters;    // [n_tok][n_kv], zero between launches
+    int max_chunks, min_chunk;
+    float *out;            // [n_tok][n_heads*hd]
+};
+int launch_attention(hipStream_t st, bool fused, bool f16kv, const AttnArgs &a);
+constexpr int ATT_CHUNK_MAX = 256;  // positions held in LDS per workgroup
+
+// QK-norm + RoPE of n_tok tokens' q (in place) and k, and the k/v cache
+// store, for prefill.  qkv rows are [q | k | v] with row stride `stride`.
+struct QkPostArgs {
+    float *qkv; int stride;
+    const float *q_norm, *k_norm, *inv_freq;
+    float eps; int rope_style;
+    void *kc, *vc;
+    int kv_dim, hd, n_heads, n_kv, pos_base, n_tok;
+};
+int launch_qkpost(hipStream_t st, bool f16kv, const QkPostArgs &a);
+
+// ------------------------------------------------------------ prefill GEMM --
+// Q8_0-quantize n rows of activations (optionally RMSNorm-ed first):
+//   qx[n][cols] int8, dx[n][cols/32] fp32 (the fp16-rounded block scales),
+//   xs[n][cols/32] int32 block sums of the codes (Q4_0 weights need them).
+struct QuantRowsArgs {
+    const float *x; int x_stride, cols, n;
+    int swiglu;                           // row value i = silu(x[i]) * x[cols + i]
+    const float *norm_w; float eps;       // nullptr: no norm
+    const int *ids; DMat emb; float *x_out;  // ids != nullptr: embed rows first
+    float *xf;                            // fp32 copy of the (normed) rows, F32 weights
+    int8_t *qx; float *dx; int *xs;
+};
+int launch_quant_rows(hipStream_t st, const QuantRowsArgs &a);
+
+// Y = X . W^T over n tokens, fused epilogues as in matvec (EPI_*), with the
+// activations already quantized by launch_quant_rows.
+struct GemmArgs {
+    DMat W;
+    int units, pair_off, n;
+    const int8_t *qx; const float *dx; const int *xs;  // quantized X
+    const float *xf;                                     // fp32 X (F32 weights)
+    float *out; int out_stride;
+    const float *bias;
+};
+int launch_gemm(hipStream_t st, int epi, const GemmArgs &a);
+
+}  // namespace ehip

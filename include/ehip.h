@@ -1,0 +1,93 @@
+/* ehip.h — the thin C-ABI device layer beneath ember.h.
+ *
+ * The host library (C11) resolves tensors from the mmap'd .ember file and
+ * hands plain host pointers to this layer, which repacks and uploads them to
+ * one MI355X (gfx950) and runs the forward pass there.  No C++ or HIP type
+ * crosses this boundary: only pointers, sizes and the structs below.
+ *
+ * Each entry point replaces the work of a reference function:
+ *   ehip_model_upload   <- weight resolution in ember_state_new_ex (src/model.c:120-171)
+ *   ehip_state_create   <- activation/KV allocation (src/model.c:173-193)
+ *   ehip_state_destroy  <- ember_state_free (src/model.c:195-205)
+ *   ehip_forward        <- ember_forward (src/model.c:362-414)
+ *   ehip_prefill        <- ember_prefill (src/model.c:283-360)
+ * Errors: functions returning a pointer return NULL, functions returning int
+ * return nonzero; ehip_last_error() then names the failing call.
+ */
+#ifndef EMBER_EHIP_H
+#define EMBER_EHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct EhipModel EhipModel;  /* weights resident in HBM         */
+typedef struct EhipState EhipState;  /* KV cache, activations, stream   */
+
+typedef struct {
+    int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size;
+    float   rope_theta, norm_eps;
+    int32_t rope_style;   /* EMBER_ROPE_*                                       */
+    int32_t qk_norm;      /* nonzero: per-head RMSNorm of q and k before RoPE   */
+} EhipConfig;
+
+/* A weight matrix in its file encoding: `data` points at rows*in_len weights
+ * stored as EMBER_DT_F32, EMBER_DT_Q8_0 (34-byte blocks) or EMBER_DT_Q4_0
+ * (18-byte blocks), row-major [rows][in_len]. */
+typedef struct { const void *data; int32_t dtype; } EhipWeight;
+
+typedef struct {
+    EhipWeight wq, wk, wv, wo, w1, w2, w3;
+    const float *attn_norm, *ffn_norm;   /* [dim]                      */
+    const float *q_norm, *k_norm;        /* [head_dim] or NULL          */
+    const float *bq, *bk, *bv;           /* [n_heads*hd], [kv_dim] or NULL */
+} EhipLayer;
+
+const char *ehip_last_error(void);
+/* Number of visible devices (0 when no GPU); initialises the runtime. */
+int ehip_device_count(void);
+
+/* Repack and upload all weights.  `rope_inv_freq` holds head_dim/2 values
+ * 1/theta^(2i/head_dim) computed on the host, so device and host RoPE angles
+ * agree bit for bit. */
+EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *layers,
+                             EhipWeight tok_emb, EhipWeight lm_head,
+                             const float *final_norm, const float *rope_inv_freq);
+void       ehip_model_free(EhipModel *m);
+/* Device bytes held by the uploaded weights. */
+uint64_t   ehip_model_bytes(const EhipModel *m);
+
+EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16);
+void       ehip_state_destroy(EhipState *s);
+
+/* Decode one token; returns host-readable logits owned by the state (pinned). */
+float *ehip_forward(EhipState *s, int tok, int pos);
+/* Prefill ids[0..n) at positions start..; returns last-token logits. */
+float *ehip_prefill(EhipState *s, const int *ids, int n, int start);
+
+/* ---- inspection and measurement (tests and bench) ----------------------- */
+/* Copy the KV cache of the given layers to/from host memory in the cache's
+ * own element type; which = 0 keys, 1 values; rows [0, n_pos). */
+int ehip_kv_read(EhipState *s, int which, int layer, int n_pos, void *host);
+int ehip_kv_write(EhipState *s, int which, int layer, int n_pos, const void *host);
+/* Copy a per-step device buffer to the host after a call: which = 0 the
+ * residual stream x [dim], 1 the last layer's raw q|k|v, 2 its attention
+ * output [n_heads*hd], 3 its SwiGLU output [hidden], 4 logits [vocab]. */
+int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t bytes);
+/* 0: eager launches, 1: one hipGraph per decode step (default). */
+int ehip_set_graph_mode(EhipState *s, int mode);
+/* Time `steps` decode steps at positions pos0.. with HIP events recorded on
+ * the state's stream; writes the average step time in ms.  Tokens follow the
+ * reference bench stream (pos*131+7) % vocab. */
+int ehip_time_decode(EhipState *s, int pos0, int steps, float *ms_per_step);
+/* Time `reps` launches of one decode-step kernel in isolation on the
+ * state's stream (kernel: 0 = attention of layer 0, 1 = lm_head matvec,
+ * 2 = fused w1|w3 matvec of layer 0) at position pos; writes average ms. */
+int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms_per_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,26 @@
+# Builds the reference C library from its own sources where they lie under
+# /root/reference/src (every file except the CLI's main.c, as its Makefile's
+# `lib` target does: Makefile:27-46), into oracle/_ref/.  Test
+# infrastructure only: it validates the restatement in oracle.c and serves
+# as the "reference" CPU baseline.  Nothing is copied into this repository.
+#   _ref/libember_ref_debug.so  flags of `make debug` (Makefile:57-59)
+#   _ref/libember_ref.so        flags of the optimized build (Makefile:23),
+#                               -march=x86-64-v3 in place of -march=native
+# -Wl,-Bsymbolic keeps the library's internal calls inside itself, since its
+# exported ember_* names equal the product library's.
+REF ?= /root/reference
+CC  ?= gcc
+SRC := $(filter-out $(REF)/src/main.c,$(wildcard $(REF)/src/*.c))
+COMMON = -std=c11 -D_DEFAULT_SOURCE -fPIC -shared -pthread -Wl,-Bsymbolic -w
+
+.PHONY: all
+all: _ref/libember_ref_debug.so _ref/libember_ref.so
+
+_ref:
+	mkdir -p _ref
+
+_ref/libember_ref_debug.so: $(SRC) | _ref
+	$(CC) $(COMMON) -O2 -fno-fast-math -ffp-contract=off -o $@ $(SRC) -lm
+
+_ref/libember_ref.so: $(SRC) | _ref
+	$(CC) $(COMMON) -O3 -ffast-math -march=x86-64-v3 -funroll-loops -o $@ $(SRC) -lm

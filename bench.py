@@ -1,0 +1,298 @@
+#!/usr/bin/env python3
+"""Single-stream decode benchmark of the token loop on one MI355X.
+
+Workload (the headline configuration): a Qwen3-0.6B-shape model, Q8_0
+(dim 1024, 28 layers, 16 query / 8 KV heads of 128, QK-norm, FFN 3072,
+vocab 151936, tied embeddings, RoPE theta 1e6), weights drawn N(0, 0.02)
+from the package's seeded generator, norms 1.0, quantized by its bit-exact
+Q8_0 quantizer.  The KV cache (fp32) is filled by a batched prefill of 4096
+seeded random ids; then greedy decode runs at positions 4096.. .
+
+A step is one decode token.  `value` is the device-resident greedy loop
+(ehip_generate_greedy: decode graph + on-device argmax, no host round trip)
+over exactly --steps tokens after --warmup untimed ones, timed with HIP
+events on the state's stream between two stream synchronisations.  Also
+reported, never as `value`:
+  api_decode_tok_s      ember_forward per token through the C API, host
+                        logits over PCIe each step (the reference bench's
+                        loop, src/main.c:258-263)
+  decode_tok_s_depth128 the same device loop at depth 128
+  prefill_tok_s_pp128 / _pp4096   ember_prefill at position 0 (mean of 5
+                        after 1 warmup, src/main.c:251-266)
+  roofline              the dominant kernel (split-K attention of one layer
+                        at depth 4096): algorithmic bytes per launch over
+                        its average duration (HIP events, isolated launches
+                        on the state's stream)
+  cpu_baseline          the reference's own C code, compiled from its
+                        sources into oracle/_ref/ (or, absent that, the
+                        oracle's port), decoding at the same depth on the
+                        host cores; best of a thread sweep on a bounded
+                        sample
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+METRIC = "single-stream decode tok/s (Qwen3-0.6B-shape Q8_0) + %HBM roofline; prefill tok/s"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def weight_bytes(c):
+    """Bytes of every quantized matrix, norm and bias read by one decode step."""
+    blk = {1: 34, 2: 18}[c["dtype"]] if c["dtype"] else None
+    hd, L, dim, hid, V = c["head_dim"], c["n_layers"], c["dim"], c["hidden_dim"], c["vocab_size"]
+    qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+
+    def mat(rows, cols, b=blk):
+        return rows * cols * 4 if b is None else rows * (cols // 32) * b
+
+    per_layer = (mat(qd, dim) + 2 * mat(kvd, dim) + mat(dim, qd) + 2 * mat(hid, dim) + mat(dim, hid)
+                 + 4 * 2 * dim + (4 * 2 * hd if c["qk_norm"] else 0)
+                 + (4 * (qd + 2 * kvd) if c["qkv_bias"] else 0))
+    head_blk = 34 if c["dtype"] in (1, 2) else None   # lm_head / embedding stay Q8_0 in Q4 files
+    return L * per_layer + mat(V, dim, head_blk) + 4 * dim + mat(1, dim, head_blk)
+
+
+def step_bytes(c, pos, e_kv):
+    """Algorithmic HBM bytes of the decode step at position `pos`."""
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    L, V = c["n_layers"], c["vocab_size"]
+    return weight_bytes(c) + 2 * L * (pos + 1) * kvd * e_kv + 2 * L * kvd * e_kv + 4 * V
+
+
+def attn_launch_bytes(c, pos, e_kv):
+    """Algorithmic bytes of one layer's attention launch at `pos`: K and V rows
+    [0, pos] read once, the new row written, q|k|v in, output out."""
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    qd = c["n_heads"] * c["head_dim"]
+    return 2 * (pos + 1) * kvd * e_kv + 2 * kvd * e_kv + 4 * (qd + 2 * kvd) + 4 * qd
+
+
+def profiled_traffic(kernel, model, depth, kv):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs, scaled against a copy kernel of
+    known size), when one exists for this exact workload; else None."""
+    path = os.path.join(ROOT, "profiles", f"decode_qwen3_q8_depth{depth}_traffic.md")
+    if model != "qwen3_06b" or kv != "f32" or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            cells = [x.strip() for x in line.strip().strip("|").split("|")]
+            if len(cells) == 5 and cells[0].strip("`").startswith(kernel):
+                return int(float(cells[4]) * 1e6)
+    return None
+
+
+def cpu_baseline(path, c, depth, budget_s):
+    """The reference's CPU decode at `depth` on this host: best of a thread
+    sweep, each point 1 warmup + timed steps within the time budget."""
+    if os.path.join(ROOT, "oracle") not in sys.path:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    ncpu = min(16, len(os.sched_getaffinity(0)))
+    V = c["vocab_size"]
+    kind, debug_note = "reference", "oracle/_ref/libember_ref.so (reference sources, -O3 -ffast-math -march=x86-64-v3)"
+    try:
+        libr = oracle.reference_lib(debug=False)
+
+        def make(ctx):
+            return oracle.Reference(path, ctx=ctx, debug=False)
+
+        def set_threads(n):
+            libr.ember_threads_shutdown()
+            libr.ember_threads_init(n)
+    except (FileNotFoundError, OSError):
+        kind, debug_note = "port", "oracle/liboracle_fast.so (restatement, optimized flags)"
+        libo = oracle.oracle_lib(fast=True)
+
+        def make(ctx):
+            return oracle.Oracle(path, ctx=ctx, fast=True)
+
+        def set_threads(n):
+            libo.orc_threads_shutdown()
+            libo.orc_threads_init(n)
+    sweep = [t for t in (1, 2, 4, 8, 16) if t <= ncpu]
+    if ncpu not in sweep:
+        sweep.append(ncpu)
+    per_point = budget_s / len(sweep)
+    eng = make(depth + 64)
+    best = (0.0, 1, 0)
+    t_start = time.time()
+    pos = depth
+    for nt in sweep:
+        set_threads(nt)
+        eng.forward((pos * 131 + 7) % V, pos)       # warmup (first touch of pages)
+        pos += 1
+        n, t0 = 0, time.perf_counter()
+        while n < 2 or (time.perf_counter() - t0 < per_point * 0.6 and n < 32):
+            eng.forward((pos * 131 + 7) % V, pos)
+            pos += 1
+            n += 1
+            if pos >= depth + 60:
+                pos = depth
+        rate = n / (time.perf_counter() - t0)
+        log(f"cpu baseline ({kind}) {nt} threads: {rate:.2f} tok/s over {n} steps")
+        if rate > best[0]:
+            best = (rate, nt, n)
+    eng.close()
+    set_threads(1)
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(best[0], 3), "unit": "tok/s", "cores": best[1], "kind": kind,
+            "sample": (f"{best[2]} greedy-shaped decode steps (token stream (pos*131+7)%V) at positions "
+                       f"{depth}.. of the same model via {debug_note}; best of threads {sweep} "
+                       f"({time.time() - t_start:.0f} s total) on '{cpu}', {ncpu} cores available")}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--model", default="qwen3_06b")
+    ap.add_argument("--depth", type=int, default=4096)
+    ap.add_argument("--kv", choices=("f32", "f16"), default="f32")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-only", action="store_true", help="skip the prefill and kernel timings")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the token loop is "
+              "single-stream on one MI355X; multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+
+    from emberllm_amd import _native, configs, emberllm
+
+    lib = _native.lib()
+    if lib.ehip_device_count() <= 0:
+        print("bench.py: no GPU visible to the HIP runtime", file=sys.stderr)
+        sys.exit(1)
+    c = configs.ALL[args.model]
+    K, W, depth = args.steps, args.warmup, args.depth
+    e_kv = 2 if args.kv == "f16" else 4
+    t0 = time.time()
+    path = configs.model_path(args.model, threads=16)
+    log(f"model {path} ready in {time.time() - t0:.1f} s")
+    ctx = depth + max(K, W) + 2
+    eng = emberllm.Engine(path, ctx=ctx, kv_fp16=args.kv == "f16")
+    rng = np.random.default_rng(4096)
+    V = c["vocab_size"]
+    out = {}
+
+    # ---- prefill --------------------------------------------------------
+    def prefill_rate(n, reps=5, warm=1):
+        ids = rng.integers(0, V, n).astype(np.int32)
+        rates = []
+        for r in range(warm + reps):
+            t = time.perf_counter()
+            eng.prefill(ids)
+            dt = time.perf_counter() - t
+            if r >= warm:
+                rates.append(n / dt)
+        return float(np.mean(rates)), float(np.std(rates, ddof=1) if len(rates) > 1 else 0.0)
+
+    if not args.decode_only:
+        out["prefill_tok_s_pp128"], out["prefill_tok_s_pp128_sd"] = prefill_rate(128)
+        log(f"prefill pp128 {out['prefill_tok_s_pp128']:.1f} tok/s")
+    # fill the cache to `depth` (also timed: pp<depth>)
+    ids = rng.integers(0, V, depth).astype(np.int32)
+    reps = 1 if args.decode_only else 3
+    rates = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        lg = eng.prefill(ids)
+        rates.append(depth / (time.perf_counter() - t))
+    out[f"prefill_tok_s_pp{depth}"] = float(np.max(rates[1:] if len(rates) > 1 else rates))
+    log(f"prefill pp{depth} {out[f'prefill_tok_s_pp{depth}']:.1f} tok/s")
+    tok0 = int(np.argmax(lg))
+
+    # ---- decode at depth: device-resident greedy loop --------------------
+    eng.generate_greedy(tok0, depth, W)             # warmup (also builds the graph)
+    wall = time.perf_counter()
+    toks, ms = eng.generate_greedy(tok0, depth, K)  # synchronises before and after
+    wall = time.perf_counter() - wall
+    tok_s = K / (ms / 1e3)
+    ms_step = ms / K
+    mean_bytes = float(np.mean([step_bytes(c, depth + i, e_kv) for i in range(K)]))
+    log(f"decode @{depth}: {tok_s:.1f} tok/s ({ms_step * 1e3:.1f} us/step, wall {K / wall:.1f} tok/s), "
+        f"{mean_bytes / 1e6:.1f} MB/step -> {tok_s * mean_bytes / HBM_PEAK:.3f} of HBM roofline")
+
+    # ---- the same decode through the C API (host logits every step) -------
+    pos, t = depth, time.perf_counter()
+    for i in range(K):
+        eng.forward((pos * 131 + 7) % V, pos)
+        pos += 1
+    out["api_decode_tok_s"] = K / (time.perf_counter() - t)
+    log(f"api decode @{depth}: {out['api_decode_tok_s']:.1f} tok/s (ember_forward, PCIe logits)")
+
+    roof = None
+    if not args.decode_only:
+        # ---- dominant kernel: attention of one layer at this depth ---------
+        reps_k = 200
+        ms_att = eng.time_kernel(0, depth, reps_k)
+        ab = attn_launch_bytes(c, depth, e_kv)
+        ms_head = eng.time_kernel(1, depth, reps_k)
+        hb = c["vocab_size"] * (c["dim"] // 32) * 34 + 4 * c["vocab_size"]
+        ms_w13 = eng.time_kernel(2, depth, reps_k)
+        wb = 2 * c["hidden_dim"] * (c["dim"] // 32) * 34 + 4 * c["hidden_dim"]
+        out["kernels"] = {
+            "attention_layer": {"us": ms_att * 1e3, "GB_s": ab / (ms_att / 1e3) / 1e9, "bytes": ab},
+            "lm_head": {"us": ms_head * 1e3, "GB_s": hb / (ms_head / 1e3) / 1e9, "bytes": hb},
+            "w1w3_swiglu": {"us": ms_w13 * 1e3, "GB_s": wb / (ms_w13 / 1e3) / 1e9, "bytes": wb},
+        }
+        log(f"kernels: {json.dumps(out['kernels'])}")
+        achieved = ab / (ms_att / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(achieved / (HBM_PEAK / 1e9), 4),
+                "traffic": profiled_traffic("ehip::k_attn_dec", args.model, depth, args.kv),
+                "kernel": f"k_attn (split-K GQA attention, one layer) at position {depth}, "
+                          f"{ab} algorithmic bytes per launch, mean of {reps_k} launches"}
+
+        # ---- depth 128 ------------------------------------------------------
+        eng.generate_greedy(tok0, 128, W)
+        _, ms128 = eng.generate_greedy(tok0, 128, K)
+        out["decode_tok_s_depth128"] = K / (ms128 / 1e3)
+        log(f"decode @128: {out['decode_tok_s_depth128']:.1f} tok/s")
+    eng.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(path, c, depth, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 dot / f32 accumulate (Q8_0 weights and activations), f32 KV" if e_kv == 4 else
+                 "int8 dot / f32 accumulate (Q8_0 weights and activations), f16 KV",
+        "data": "synthetic: seeded N(0,0.02) weights quantized to Q8_0, seeded uniform random prompt ids",
+        "config": {"workload": f"{args.model}-shape greedy decode of {K} tokens at depth {depth} after a "
+                               f"{depth}-token batched prefill; {args.kv} KV cache",
+                   "depth": depth, "kv": args.kv, "parallelism": "single GPU, single stream"},
+        "hbm_roofline_frac_step": round(tok_s * mean_bytes / HBM_PEAK, 4),
+        "bytes_per_step": int(mean_bytes),
+        "wall_tok_s": round(K / wall, 2),
+    }
+    line.update({k: (round(v, 2) if isinstance(v, float) else v) for k, v in out.items()})
+    line["roofline"] = roof
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -126,6 +126,7 @@ PROTOTYPES = {
     "ehip_set_graph_mode": (ctypes.c_int, [_P, ctypes.c_int]),
     "ehip_debug_buffer": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_uint64]),
     "ehip_time_decode": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _FP]),
+    "ehip_generate_greedy": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _IP, _FP]),
     "ehip_time_kernel": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP]),
     # ember_synth.h
     "ember_synth_write": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(EmberSynthConfig)]),

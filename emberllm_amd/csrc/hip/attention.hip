@@ -1,8 +1,9 @@
-// attention.hip — GQA attention over the HBM-resident KV cache (gfx950).
+// attention.hip — prefill GQA attention over the HBM-resident KV cache (gfx950).
 //
-// Replaces attention -> attn_heads + softmax (src/model.c:57-64, 207-278)
-// and, in the fused decode form, the QK-norm / RoPE / kv_store steps of
-// ember_forward (src/model.c:386-393).
+// Replaces the per-token attention calls of ember_prefill (src/model.c:335-337
+// -> attention -> attn_heads + softmax, model.c:57-64, 207-278) and its
+// QK-norm / RoPE / kv_store loop (model.c:323-333, k_qkpost).  The decode
+// form lives in attn_decode.hip.
 //
 // Roofline: HBM-bound.  Algorithmic bytes per decode step and layer =
 // 2 * (pos+1) * kv_dim * esize (K and V read once) + 2 * kv_dim * esize (the
@@ -47,23 +48,21 @@ __device__ __forceinline__ void head_norm(float *v, const float *w, float eps, i
     for (int d = lane; d < HD; d += 64) v[d] = v[d] * scale * w[d];
 }
 
-// rotate the pairs of one head vector (model.c:66-80); the inverse
-// frequencies come from the host so the angle pos*freq is bit-identical.
-__device__ __forceinline__ void rope_pair(float *v, int i, int hd, int pos, const float *inv_freq, int style) {
-    const float ang = (float)pos * inv_freq[i];
-    const float c = cosf(ang), s = sinf(ang);
+// rotate pair i of one head vector (model.c:66-80) by the tabulated
+// (cos, sin) of pos * freq_i, computed on the host with the reference's
+// expression and libm
+__device__ __forceinline__ void rope_pair(float *v, int i, int hd, float2 cs, int style) {
     const int ia = style == ROPE_NEOX ? i : 2 * i;
     const int ib = style == ROPE_NEOX ? i + hd / 2 : 2 * i + 1;
     const float v0 = v[ia], v1 = v[ib];
-    v[ia] = v0 * c - v1 * s;
-    v[ib] = v0 * s + v1 * c;
+    v[ia] = v0 * cs.x - v1 * cs.y;
+    v[ib] = v0 * cs.y + v1 * cs.x;
 }
 
-template <int HD, int GM, bool F16, bool FUSED>
+template <int HD, int GM, bool F16>
 __global__ __launch_bounds__(WG) void k_attn(AttnArgs a) {
     using L = Lay<HD>;
     __shared__ __align__(16) float qs[GM][HD];
-    __shared__ __align__(16) float kn[HD], vn[HD];
     __shared__ float sc[GM][ATT_CHUNK_MAX];
     __shared__ __align__(16) float vacc[NWAVE][GM][HD];
     __shared__ float ml[GM][2];
@@ -72,7 +71,7 @@ __global__ __launch_bounds__(WG) void k_attn(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int G = a.n_heads / a.n_kv;
-    const int pos = FUSED ? a.tokpos[1] : a.pos_base + b;
+    const int pos = a.pos_base + b;
     const int npos = pos + 1;
 
     // chunking, identical in every workgroup of this (token, kv head)
@@ -86,42 +85,8 @@ __global__ __launch_bounds__(WG) void k_attn(AttnArgs a) {
     const int t0 = c * clen, t1 = min(npos, t0 + clen), len = t1 - t0;
     const size_t hoff = (size_t)g * HD;
 
-    // ---- prologue: q for the group (and, fused, this position's k/v) -----
-    if (FUSED) {
-        const int qd = a.n_heads * HD;
-        for (int i = tid; i < G * HD; i += WG) qs[i / HD][i % HD] = a.q[(size_t)g * G * HD + i];
-        for (int d = tid; d < HD; d += WG) {
-            kn[d] = a.q[qd + hoff + d];
-            vn[d] = a.q[qd + a.kv_dim + hoff + d];
-        }
-        __syncthreads();
-        if (a.q_norm) {
-            for (int h = wave; h <= G; h += NWAVE)
-                head_norm<HD>(h < G ? qs[h] : kn, h < G ? a.q_norm : a.k_norm, a.eps, lane);
-            __syncthreads();
-        }
-        for (int i = tid; i < (G + 1) * (HD / 2); i += WG) {
-            const int h = i / (HD / 2), p = i % (HD / 2);
-            rope_pair(h < G ? qs[h] : kn, p, HD, pos, a.inv_freq, a.rope_style);
-        }
-        __syncthreads();
-        if (F16) {
-            for (int d = tid; d < HD; d += WG) { kn[d] = h2f(f2h(kn[d])); vn[d] = h2f(f2h(vn[d])); }
-        }
-        if (c == nc - 1) {  // the chunk holding `pos` stores it (model.c:39-48)
-            const size_t off = (size_t)pos * a.kv_dim + hoff;
-            for (int d = tid; d < HD; d += WG) {
-                if (F16) {
-                    reinterpret_cast<uint16_t *>(a.kc)[off + d] = f2h(kn[d]);
-                    reinterpret_cast<uint16_t *>(a.vc)[off + d] = f2h(vn[d]);
-                } else {
-                    reinterpret_cast<float *>(a.kc)[off + d] = kn[d];
-                    reinterpret_cast<float *>(a.vc)[off + d] = vn[d];
-                }
-            }
-        }
-        __syncthreads();
-    } else {
+    // ---- prologue: q rows of the group --------------------------------------
+    {
         const float *qrow = a.q + (size_t)b * a.q_stride + (size_t)g * G * HD;
         for (int i = tid; i < G * HD; i += WG) qs[i / HD][i % HD] = qrow[i];
         __syncthreads();
@@ -137,10 +102,7 @@ __global__ __launch_bounds__(WG) void k_attn(AttnArgs a) {
     // ---- scores --------------------------------------------------------
     for (int t = t0 + wave * L::RPL + rw; t < t1; t += NWAVE * L::RPL) {
         float4 k4 = make_float4(0, 0, 0, 0);
-        if (pj) {
-            if (FUSED && t == pos) k4 = *reinterpret_cast<const float4 *>(&kn[4 * j]);
-            else k4 = load4<F16>(a.kc, (size_t)t * a.kv_dim + hoff + 4 * j);
-        }
+        if (pj) k4 = load4<F16>(a.kc, (size_t)t * a.kv_dim + hoff + 4 * j);
         float p[GM];
 #pragma unroll
         for (int h = 0; h < GM; h++) {
@@ -178,10 +140,7 @@ __global__ __launch_bounds__(WG) void k_attn(AttnArgs a) {
     for (int h = 0; h < GM; h++) acc[h] = make_float4(0, 0, 0, 0);
     for (int t = t0 + wave * L::RPL + rw; t < t1; t += NWAVE * L::RPL) {
         float4 v4 = make_float4(0, 0, 0, 0);
-        if (pj) {
-            if (FUSED && t == pos) v4 = *reinterpret_cast<const float4 *>(&vn[4 * j]);
-            else v4 = load4<F16>(a.vc, (size_t)t * a.kv_dim + hoff + 4 * j);
-        }
+        if (pj) v4 = load4<F16>(a.vc, (size_t)t * a.kv_dim + hoff + 4 * j);
 #pragma unroll
         for (int h = 0; h < GM; h++) {
             if (h < G) {
@@ -265,7 +224,7 @@ __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
     for (int d = lane; d < HD; d += 64) v[d] = row[d];
     __syncthreads();
     if (a.q_norm) { head_norm<HD>(v, isq ? a.q_norm : a.k_norm, a.eps, lane); __syncthreads(); }
-    for (int i = lane; i < HD / 2; i += 64) rope_pair(v, i, HD, pos, a.inv_freq, a.rope_style);
+    for (int i = lane; i < HD / 2; i += 64) rope_pair(v, i, HD, a.rope[(size_t)pos * (HD / 2) + i], a.rope_style);
     __syncthreads();
     if (isq) {
         for (int d = lane; d < HD; d += 64) row[d] = v[d];
@@ -286,30 +245,29 @@ __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
 
 // --------------------------------------------------------------------------
 template <int HD, int GM, bool F16>
-static void go_attn(hipStream_t st, bool fused, const AttnArgs &a) {
+static void go_attn(hipStream_t st, const AttnArgs &a) {
     dim3 grid(a.max_chunks, a.n_kv, a.n_tok);
-    if (fused) hipLaunchKernelGGL((k_attn<HD, GM, F16, true>), grid, dim3(WG), 0, st, a);
-    else hipLaunchKernelGGL((k_attn<HD, GM, F16, false>), grid, dim3(WG), 0, st, a);
+    hipLaunchKernelGGL((k_attn<HD, GM, F16>), grid, dim3(WG), 0, st, a);
 }
 
 template <int HD, bool F16>
-static int pick_g(hipStream_t st, bool fused, const AttnArgs &a) {
+static int pick_g(hipStream_t st, const AttnArgs &a) {
     const int G = a.n_heads / a.n_kv;
-    if (G <= 1) go_attn<HD, 1, F16>(st, fused, a);
-    else if (G <= 2) go_attn<HD, 2, F16>(st, fused, a);
-    else if (G <= 4) go_attn<HD, 4, F16>(st, fused, a);
-    else if (G <= 8) go_attn<HD, 8, F16>(st, fused, a);
+    if (G <= 1) go_attn<HD, 1, F16>(st, a);
+    else if (G <= 2) go_attn<HD, 2, F16>(st, a);
+    else if (G <= 4) go_attn<HD, 4, F16>(st, a);
+    else if (G <= 8) go_attn<HD, 8, F16>(st, a);
     else return -1;
     return 0;
 }
 
-int launch_attention(hipStream_t st, bool fused, bool f16kv, const AttnArgs &a) {
+int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a) {
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0) return -1;
     if ((a.ctx + ATT_CHUNK_MAX - 1) / ATT_CHUNK_MAX > a.max_chunks) return -1;
     switch (a.hd) {
-        case 48: return f16kv ? pick_g<48, true>(st, fused, a) : pick_g<48, false>(st, fused, a);
-        case 64: return f16kv ? pick_g<64, true>(st, fused, a) : pick_g<64, false>(st, fused, a);
-        case 128: return f16kv ? pick_g<128, true>(st, fused, a) : pick_g<128, false>(st, fused, a);
+        case 48: return f16kv ? pick_g<48, true>(st, a) : pick_g<48, false>(st, a);
+        case 64: return f16kv ? pick_g<64, true>(st, a) : pick_g<64, false>(st, a);
+        case 128: return f16kv ? pick_g<128, true>(st, a) : pick_g<128, false>(st, a);
     }
     return -1;
 }

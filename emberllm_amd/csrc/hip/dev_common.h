@@ -35,14 +35,64 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+// Sum over the 64 lanes with DPP lane moves (no LDS round trips); the total
+// is returned to every lane from lane 63.  The association order is fixed:
+// pairs, quads, eighths, rows of 16, then rows combined.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add<0xb1, 0xf>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);   // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);   // row_mirror: every lane of a row holds its row sum
+    v = dpp_add<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_dpp(v); }
+
+// v[i] + v[i ^ 16] and v[i] + v[i ^ 32] in every lane (gfx950 lane swaps)
+__device__ __forceinline__ float xor16_add(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v[i] + v[i ^ 8] within each row of 16 (row_ror:8)
+__device__ __forceinline__ float xor8_add(float v) { return dpp_add<0x128, 0xf>(v); }
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL,
+                                                               ROW_MASK, 0xf, false)));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    v = dpp_max<0xb1, 0xf>(v);
+    v = dpp_max<0x4e, 0xf>(v);
+    v = dpp_max<0x141, 0xf>(v);
+    v = dpp_max<0x140, 0xf>(v);
+    v = dpp_max<0x142, 0xa>(v);
+    v = dpp_max<0x143, 0xc>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Maximum / integer sum over aligned groups of 8 lanes; every lane of the
+// group receives the result.
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false)));
+    return v;
+}
+__device__ __forceinline__ int sum8(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, false);
     return v;
 }
 

@@ -63,7 +63,8 @@ struct EhipModel {
     EhipConfig cfg;
     std::vector<DevLayer> layers;
     DMat emb, head;
-    float *final_norm, *inv_freq;
+    float *final_norm;
+    std::vector<float> inv_freq;   // host copy: 1/theta^(2i/hd), the reference's expression
     std::vector<void *> allocs;
     uint64_t bytes;
     bool any_f32;
@@ -214,8 +215,7 @@ extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *
         if (lm_head.data == tok_emb.data) m->head = m->emb;
         else if (!upload_mat(m, &m->head, &lm_head, &c.vocab_size, 1, c.dim, "lm_head")) goto fail;
         if (!(m->final_norm = upload_f32(m, &final_norm, &c.dim, 1))) goto fail;
-        int half = hd / 2;
-        if (!(m->inv_freq = upload_f32(m, &rope_inv_freq, &half, 1))) goto fail;
+        m->inv_freq.assign(rope_inv_freq, rope_inv_freq + hd / 2);
     }
     return m;
 fail:
@@ -233,13 +233,17 @@ struct EhipState {
     void *kc, *vc;
     int *tokpos_d, *tokpos_h;
     float *x, *qkv, *o, *h, *logits_d, *logits_h;
-    float *part; unsigned *ctr;
-    int mc_dec, min_chunk_dec;
+    float *part;
+    float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
+    int mc_dec;
     // prefill scratch
     float *X, *QKV, *O, *H, *xf, *dxp, *part_pf;
     int8_t *qx; int *xsum, *ids_d; unsigned *ctr_pf;
     int mc_pf;
+    // device greedy loop: argmax partials, counter, generated tokens [ctx]
+    float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
+    hipGraph_t graph_gen; hipGraphExec_t gexec_gen;
     hipEvent_t ev0, ev1;
     std::vector<void *> allocs;
 };
@@ -257,6 +261,8 @@ extern "C" void ehip_state_destroy(EhipState *s) {
     (void)hipStreamSynchronize(s->st);
     if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
     if (s->graph) (void)hipGraphDestroy(s->graph);
+    if (s->gexec_gen) (void)hipGraphExecDestroy(s->gexec_gen);
+    if (s->graph_gen) (void)hipGraphDestroy(s->graph_gen);
     for (void *p : s->allocs) (void)hipFree(p);
     if (s->tokpos_h) (void)hipHostFree(s->tokpos_h);
     if (s->logits_h) (void)hipHostFree(s->logits_h);
@@ -284,20 +290,23 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     }
     const size_t kvb = (size_t)c.n_layers * ctx * kvd * s->esize;
     const int need = (ctx + ATT_CHUNK_MAX - 1) / ATT_CHUNK_MAX;
-    const int target_wg = env_int("EHIP_ATT_WGS", 512);
-    s->mc_dec = std::max(need, (target_wg + c.n_kv_heads - 1) / c.n_kv_heads);
-    s->min_chunk_dec = env_int("EHIP_ATT_MIN_CHUNK", 32);
+    const int dch = attn_decode_chunk(hd, s->f16kv != 0);
+    if (dch <= 0) {
+        set_err("head_dim %d not supported by the attention kernel", hd);
+        ehip_state_destroy(s);
+        return nullptr;
+    }
+    s->mc_dec = (ctx + dch - 1) / dch;
     s->mc_pf = need;
     const int wide = std::max(std::max(c.dim, c.hidden_dim), qd);
     bool ok = (s->kc = salloc(s, kvb, true)) && (s->vc = salloc(s, kvb, true)) &&
-              (s->tokpos_d = (int *)salloc(s, 8, true)) &&
+              (s->tokpos_d = (int *)salloc(s, 16, true)) &&
               (s->x = (float *)salloc(s, 4 * (size_t)c.dim)) &&
               (s->qkv = (float *)salloc(s, 4 * (size_t)(qd + 2 * kvd))) &&
               (s->o = (float *)salloc(s, 4 * (size_t)qd)) &&
               (s->h = (float *)salloc(s, 4 * (size_t)c.hidden_dim)) &&
               (s->logits_d = (float *)salloc(s, 4 * (size_t)c.vocab_size, true)) &&
               (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * s->mc_dec * (hd + 2))) &&
-              (s->ctr = (unsigned *)salloc(s, 4 * (size_t)c.n_kv_heads, true)) &&
               (s->X = (float *)salloc(s, 4 * (size_t)PF_CHUNK * c.dim)) &&
               (s->QKV = (float *)salloc(s, 4 * (size_t)PF_CHUNK * (qd + 2 * kvd))) &&
               (s->O = (float *)salloc(s, 4 * (size_t)PF_CHUNK * qd)) &&
@@ -307,14 +316,30 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->xsum = (int *)salloc(s, 4 * (size_t)PF_CHUNK * (wide / QB + 1))) &&
               (s->ids_d = (int *)salloc(s, 4 * (size_t)PF_CHUNK)) &&
               (s->part_pf = (float *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_heads * s->mc_pf * (hd + 2))) &&
-              (s->ctr_pf = (unsigned *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_kv_heads, true));
+              (s->ctr_pf = (unsigned *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_kv_heads, true)) &&
+              (s->am_val = (float *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
+              (s->am_idx = (int *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
+              (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * (size_t)PF_CHUNK * wide)) != nullptr;
+    if (ok) {
+        // RoPE table with the reference's arithmetic (model.c:69-71): the
+        // angle pos * freq in fp32, then the host libm cosf / sinf
+        const int half = hd / 2;
+        std::vector<float2> tab((size_t)ctx * half);
+        for (int p = 0; p < ctx; p++)
+            for (int i = 0; i < half; i++) {
+                const float ang = (float)p * m->inv_freq[i];
+                tab[(size_t)p * half + i] = make_float2(cosf(ang), sinf(ang));
+            }
+        ok = (s->rope = (float2 *)salloc(s, sizeof(float2) * tab.size())) != nullptr &&
+             hipMemcpy(s->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice) == hipSuccess;
+    }
     if (!ok) {
         set_err("device allocation for a state with ctx %d failed (KV %zu bytes)", ctx, 2 * kvb);
         ehip_state_destroy(s);
         return nullptr;
     }
-    if (hipHostMalloc(&s->tokpos_h, 8, hipHostMallocDefault) != hipSuccess ||
+    if (hipHostMalloc(&s->tokpos_h, 16, hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(&s->logits_h, 4 * (size_t)c.vocab_size, hipHostMallocDefault) != hipSuccess ||
         hipEventCreate(&s->ev0) != hipSuccess || hipEventCreate(&s->ev1) != hipSuccess) {
         set_err("pinned host allocation failed");
@@ -331,7 +356,7 @@ static AttnArgs attn_args(EhipState *s, int l) {
     const DevLayer &y = s->m->layers[l];
     const int kvd = c.n_kv_heads * c.head_dim;
     AttnArgs a{};
-    a.q_norm = y.q_norm; a.k_norm = y.k_norm; a.inv_freq = s->m->inv_freq;
+    a.q_norm = y.q_norm; a.k_norm = y.k_norm; a.rope = s->rope;
     a.eps = c.norm_eps; a.inv_sqrt = 1.0f / sqrtf((float)c.head_dim);
     a.rope_style = c.rope_style;
     const size_t loff = (size_t)l * s->ctx * kvd * s->esize;
@@ -344,17 +369,21 @@ static AttnArgs attn_args(EhipState *s, int l) {
 static int enq_attn_decode(EhipState *s, int l) {
     AttnArgs a = attn_args(s, l);
     a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
-    a.part = s->part; a.counters = s->ctr; a.max_chunks = s->mc_dec; a.min_chunk = s->min_chunk_dec;
+    a.part = s->part; a.max_chunks = s->mc_dec;
     a.out = s->o;
-    return launch_attention(s->st, true, s->f16kv, a);
+    return launch_attn_decode(s->st, s->f16kv, a);
 }
 
-static int enq_head(EhipState *s, const float *xin) {
+static MatvecArgs head_args(EhipState *s, const float *xin) {
     const EhipModel *m = s->m;
     MatvecArgs a{};
     a.W = m->head; a.units = m->cfg.vocab_size; a.in = xin; a.norm_w = m->final_norm;
     a.eps = m->cfg.norm_eps; a.out = s->logits_d;
-    return launch_matvec(s->st, PRO_NORM, EPI_STORE, a);
+    return a;
+}
+
+static int enq_head(EhipState *s, const float *xin) {
+    return launch_matvec(s->st, PRO_NORM, EPI_STORE, head_args(s, xin));
 }
 
 static int enq_w13(EhipState *s, int l) {
@@ -366,8 +395,8 @@ static int enq_w13(EhipState *s, int l) {
     return launch_matvec(s->st, PRO_NORM, EPI_SWIGLU, a);
 }
 
-// All launches of one decode step (the tokpos copy is the caller's).
-static int enq_decode(EhipState *s) {
+// The layer launches of one decode step (the tokpos copy is the caller's).
+static int enq_layers(EhipState *s) {
     const EhipModel *m = s->m;
     const EhipConfig &c = m->cfg;
     const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
@@ -386,6 +415,11 @@ static int enq_decode(EhipState *s) {
         d.W = y.w2; d.units = c.dim; d.in = s->h; d.out = s->x;
         if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, d)) return -1;
     }
+    return 0;
+}
+
+static int enq_decode(EhipState *s) {
+    if (enq_layers(s)) return -1;
     return enq_head(s, s->x);
 }
 
@@ -424,6 +458,66 @@ extern "C" float *ehip_forward(EhipState *s, int tok, int pos) {
     return s->logits_h;
 }
 
+// One step of the device-resident greedy loop: the decode launches, then the
+// argmax that feeds the chosen token back into tokpos.
+static int enq_gen_step(EhipState *s) {
+    if (s->m->head.dtype != DT_F32) {   // argmax fused into the lm_head matvec
+        if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
+        MatvecArgs a = head_args(s, s->x);
+        a.am_val = s->am_val; a.am_idx = s->am_idx;
+        a.am_tokpos = s->tokpos_d; a.am_out = s->gen_tok; a.am_cap = s->ctx;
+        if (launch_matvec(s->st, PRO_NORM, EPI_STORE, a)) { set_err("lm_head launch failed"); return -1; }
+        return 0;
+    }
+    if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
+    ArgmaxArgs g{};
+    g.logits = s->logits_d; g.n = s->m->cfg.vocab_size;
+    g.pval = s->am_val; g.pidx = s->am_idx;
+    g.tokpos = s->tokpos_d; g.out = s->gen_tok; g.cap = s->ctx;
+    if (launch_argmax(s->st, g)) { set_err("argmax launch failed"); return -1; }
+    return 0;
+}
+
+static int run_gen_step(EhipState *s) {
+    if (!s->graph_mode) return enq_gen_step(s);
+    if (!s->gexec_gen) {
+        HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), -1);
+        int rc = enq_gen_step(s);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(s->st, &g);
+        if (rc) { if (g) (void)hipGraphDestroy(g); return -1; }
+        if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return -1; }
+        s->graph_gen = g;
+        HCHK(hipGraphInstantiate(&s->gexec_gen, g, nullptr, nullptr, 0), -1);
+    }
+    HCHK(hipGraphLaunch(s->gexec_gen, s->st), -1);
+    return 0;
+}
+
+extern "C" int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *out_tokens, float *ms) {
+    const int V = s->m->cfg.vocab_size;
+    if (n <= 0 || pos < 0 || (long)pos + n > s->ctx) { set_err("generate: positions %d..%d exceed the context of %d", pos, pos + n - 1, s->ctx); return -1; }
+    if (tok < 0 || tok >= V) { set_err("generate: token id %d out of range [0,%d)", tok, V); return -1; }
+    s->tokpos_h[0] = tok;
+    s->tokpos_h[1] = pos;
+    s->tokpos_h[2] = 0;
+    s->tokpos_h[3] = 0;
+    HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipEventRecord(s->ev0, s->st), -1);
+    for (int i = 0; i < n; i++)
+        if (run_gen_step(s)) return -1;
+    HCHK(hipEventRecord(s->ev1, s->st), -1);
+    HCHK(hipEventSynchronize(s->ev1), -1);
+    if (ms) {
+        float t = 0.0f;
+        HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
+        *ms = t;
+    }
+    if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
 extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
     const EhipModel *m = s->m;
     const EhipConfig &c = m->cfg;
@@ -446,7 +540,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             rc |= launch_gemm(s->st, EPI_STORE, g);
             QkPostArgs p{};
             p.qkv = s->QKV; p.stride = stride; p.q_norm = y.q_norm; p.k_norm = y.k_norm;
-            p.inv_freq = m->inv_freq; p.eps = c.norm_eps; p.rope_style = c.rope_style;
+            p.rope = s->rope; p.eps = c.norm_eps; p.rope_style = c.rope_style;
             AttnArgs at = attn_args(s, l);
             p.kc = at.kc; p.vc = at.vc; p.kv_dim = kvd; p.hd = hd; p.n_heads = c.n_heads;
             p.n_kv = c.n_kv_heads; p.pos_base = start + c0; p.n_tok = mt;
@@ -454,7 +548,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             at.q = s->QKV; at.q_stride = stride; at.pos_base = start + c0; at.n_tok = mt;
             at.part = s->part_pf; at.counters = s->ctr_pf; at.max_chunks = s->mc_pf;
             at.min_chunk = ATT_CHUNK_MAX; at.out = s->O;
-            rc |= launch_attention(s->st, false, s->f16kv, at);
+            rc |= launch_attention(s->st, s->f16kv, at);
             QuantRowsArgs q2{};
             q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;
             q2.xf = q.xf; q2.qx = s->qx; q2.dx = s->dxp; q2.xs = s->xsum;

@@ -28,20 +28,28 @@ struct MatvecArgs {
     float *x_out;
     float *out;
     const float *bias;
+    // EPI_STORE only, optional: greedy selection over the outputs (first
+    // maximum).  Per-workgroup winners go to am_val/am_idx (MATVEC_MAX_GRID
+    // entries); a merge kernel then writes am_tokpos = {token, pos + 1, n + 1}
+    // and am_out[n] = token (when n < am_cap).
+    float *am_val; int *am_idx;
+    int *am_tokpos; int *am_out; int am_cap;
 };
+constexpr int MATVEC_MAX_GRID = 2048;
 int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
 
 // ------------------------------------------------------------- attention --
 // GQA attention of n_tok query tokens against the cache, split over chunks
 // of positions (flash-decoding); the last workgroup of each (token, kv head)
-// combines the chunk partials.  With `fused`, the single token's raw q/k/v
-// (straight out of the QKV matvec) is QK-normed and rotated in the prologue
-// and its k/v are written to the cache at `pos` by the chunk that owns it.
+// combines the chunk partials.  In the decode form the single token's raw
+// q/k/v (straight out of the QKV matvec) is QK-normed and rotated in the
+// prologue and its k/v are written to the cache at `pos` by the chunk that
+// owns it.
 struct AttnArgs {
     const float *q;        // fused: raw q|k|v row; else rotated Q rows
     int q_stride;          // floats between consecutive tokens' q
     const float *q_norm, *k_norm;  // [hd] or nullptr
-    const float *inv_freq;         // [hd/2]
+    const float2 *rope;            // [ctx][hd/2] (cos, sin) of pos * freq_i
     float eps, inv_sqrt;
     int rope_style;
     void *kc, *vc;         // layer cache base, [ctx][kv_dim]
@@ -54,14 +62,20 @@ struct AttnArgs {
     int max_chunks, min_chunk;
     float *out;            // [n_tok][n_heads*hd]
 };
-int launch_attention(hipStream_t st, bool fused, bool f16kv, const AttnArgs &a);
+// prefill: q rows already normed and rotated, k/v already in the cache
+int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
 constexpr int ATT_CHUNK_MAX = 256;  // positions held in LDS per workgroup
+// decode (one token, fused QK-norm / RoPE / KV store); max_chunks must be at
+// least ceil(ctx / attn_decode_chunk(hd, f16kv))
+int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a);
+int attn_decode_chunk(int hd, bool f16kv);
 
 // QK-norm + RoPE of n_tok tokens' q (in place) and k, and the k/v cache
 // store, for prefill.  qkv rows are [q | k | v] with row stride `stride`.
 struct QkPostArgs {
     float *qkv; int stride;
-    const float *q_norm, *k_norm, *inv_freq;
+    const float *q_norm, *k_norm;
+    const float2 *rope;            // [ctx][hd/2] (cos, sin)
     float eps; int rope_style;
     void *kc, *vc;
     int kv_dim, hd, n_heads, n_kv, pos_base, n_tok;
@@ -93,5 +107,21 @@ struct GemmArgs {
     const float *bias;
 };
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a);
+
+// ---------------------------------------------------------------- sample --
+// Greedy selection (first maximum) over n logits; writes tokpos[0] = token,
+// tokpos[1] += 1 and appends the token to out[tokpos[2]++] (when < cap).
+struct ArgmaxArgs {
+    const float *logits; int n;
+    float *pval; int *pidx;     // [ARGMAX_MAX_BLOCKS] per-workgroup winners
+    int *tokpos;                // device {tok, pos, n_generated}
+    int *out; int cap;
+};
+constexpr int ARGMAX_MAX_BLOCKS = 256;
+int launch_argmax(hipStream_t st, const ArgmaxArgs &a);
+// The merge step alone: first maximum over `nparts` (value, index) winners,
+// n = the number of logits they cover (for the out-of-range guard).
+int launch_argmax_merge(hipStream_t st, const float *pval, const int *pidx, int nparts, int n,
+                        int *tokpos, int *out, int cap);
 
 }  // namespace ehip

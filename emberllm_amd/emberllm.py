@@ -72,6 +72,17 @@ class Engine:
             raise RuntimeError(_native.last_error())
         return ms.value
 
+    def generate_greedy(self, tok, pos, n):
+        """Greedy decode of n tokens held on the device; returns (tokens, ms)."""
+        out = np.zeros(n, dtype=np.int32)
+        ms = ctypes.c_float()
+        rc = self.lib.ehip_generate_greedy(self.dev, int(tok), int(pos), int(n),
+                                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                                           ctypes.byref(ms))
+        if rc != 0:
+            raise RuntimeError(_native.last_error())
+        return out, ms.value
+
     def time_kernel(self, kernel, pos, reps):
         ms = ctypes.c_float()
         if self.lib.ehip_time_kernel(self.dev, int(kernel), int(pos), int(reps), ctypes.byref(ms)) != 0:

@@ -50,8 +50,9 @@ const char *ehip_last_error(void);
 int ehip_device_count(void);
 
 /* Repack and upload all weights.  `rope_inv_freq` holds head_dim/2 values
- * 1/theta^(2i/head_dim) computed on the host, so device and host RoPE angles
- * agree bit for bit. */
+ * 1/theta^(2i/head_dim) computed on the host; each state tabulates
+ * cosf/sinf of pos * freq_i for its positions with the host libm, as the
+ * reference computes them per call (src/model.c:66-71). */
 EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *layers,
                              EhipWeight tok_emb, EhipWeight lm_head,
                              const float *final_norm, const float *rope_inv_freq);
@@ -66,6 +67,19 @@ void       ehip_state_destroy(EhipState *s);
 float *ehip_forward(EhipState *s, int tok, int pos);
 /* Prefill ids[0..n) at positions start..; returns last-token logits. */
 float *ehip_prefill(EhipState *s, const int *ids, int n, int start);
+
+/* Greedy decode held entirely on the device, replacing the caller's loop of
+ * ember_sample (temperature <= 0: the first maximum, src/sample.c:114-127)
+ * followed by ember_forward (the generate loop of src/main.c:197-206).
+ * Starting from token `tok` at position `pos`, run n decode steps; after
+ * each, the argmax of the logits becomes the next input token on the device,
+ * with no host round trip (one hipGraph replayed n times).  The n chosen
+ * tokens are copied to out_tokens (if non-NULL); the last step's logits stay
+ * in device memory (ehip_debug_buffer 4).  *ms (if non-NULL) receives the
+ * device time of the n steps, from HIP events on the state's stream.  No
+ * stop-token handling: exactly n tokens are generated.  Returns 0, or
+ * nonzero with ehip_last_error() set. */
+int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *out_tokens, float *ms);
 
 /* ---- inspection and measurement (tests and bench) ----------------------- */
 /* Copy the KV cache of the given layers to/from host memory in the cache's

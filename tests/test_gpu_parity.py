@@ -216,3 +216,77 @@ def test_qwen3_decode_at_depth_4096(oracle_threads):
     orc.close()
     # same bar as the depth-16 Qwen3 case
     say(check_run(res, "qwen3_06b-p16-d32-s11"))
+
+
+def _greedy_case(name, n_prompt, n_gen, seed, ctx=0, kv16=False):
+    """Device greedy loop vs the C-API loop (ember_forward + first-max argmax
+    on the host, src/sample.c:114-127) and vs the oracle, teacher forced on
+    the GPU's own token sequence."""
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, V, n_prompt)
+    say(f"device greedy {name} prompt={n_prompt} gen={n_gen} kv16={kv16}")
+    a = emberllm.Engine(path, ctx=ctx, kv_fp16=kv16)
+    first = a.prefill(ids)
+    tok0 = int(np.argmax(first))
+    toks, ms = a.generate_greedy(tok0, n_prompt, n_gen)
+    assert ms > 0
+    last = a.debug_buffer(4, V)
+    a.close()
+    b = emberllm.Engine(path, ctx=ctx, kv_fp16=kv16)
+    b.prefill(ids)
+    orc = oracle.Oracle(path, ctx=ctx, kv_fp16=kv16)
+    orc.prefill(ids)
+    t, res = tok0, []
+    for i in range(n_gen):
+        lg = b.forward(t, n_prompt + i)
+        ref = orc.forward(t, n_prompt + i)
+        assert int(np.argmax(lg)) == int(toks[i]), f"step {i}: device loop chose {toks[i]}, API loop {np.argmax(lg)}"
+        res.append(compare(lg, ref))
+        t = int(toks[i])
+    np.testing.assert_array_equal(last, lg)   # bit-identical last logits
+    b.close()
+    orc.close()
+    return res
+
+
+def test_device_greedy_loop(oracle_threads):
+    res = _greedy_case("t_qwen3", 9, 40, 5)
+    for r in res:
+        assert r["agree"] or r["margin"] < 2 * r["max_abs"], r
+    res = _greedy_case("t_g7", 300, 12, 6, kv16=True)
+    for r in res:
+        assert r["agree"] or r["margin"] < 2 * r["max_abs"], r
+
+
+def test_device_argmax_first_maximum(tmp_path):
+    """Ties resolve to the first index, as the reference's strict `>` scan
+    (src/sample.c:114-118): with final_norm zeroed every logit is exactly 0,
+    so each greedy step must choose token 0."""
+    import shutil
+    src = configs.model_path("t_llama")
+    path = str(tmp_path / "tied_logits.ember")
+    shutil.copy(src, path)
+    lib = emberllm._native.lib()
+    m = lib.ember_model_load(path.encode())
+    t = lib.ember_model_tensor(m, b"final_norm").contents
+    off, nbytes = int(t.offset), int(t.nbytes)
+    lib.ember_model_free(m)
+    with open(path, "r+b") as f:
+        f.seek(off)
+        f.write(bytes(nbytes))
+    say("device argmax tie rule")
+    e = emberllm.Engine(path)
+    lg = e.prefill([1, 2, 3])
+    assert np.all(lg == 0.0)
+    toks, _ = e.generate_greedy(5, 3, 4)
+    np.testing.assert_array_equal(toks, 0)
+    e.close()
+
+
+@pytest.mark.slow
+def test_device_greedy_qwen3_shape(oracle_threads):
+    res = _greedy_case("qwen3_06b", 16, 24, 12, ctx=48)
+    ok = [r["agree"] or r["margin"] < 2 * r["max_abs"] for r in res]
+    assert np.mean(ok) >= 0.99, res

@@ -8,23 +8,31 @@
 // 2 * (pos+1) * kv_dim * esize (K and V rows read once) + 2 * kv_dim * esize
 // (the new row written) + the q|k|v input and the output (a few KB).
 //
-// Grid = (chunks, kv heads).  A workgroup owns CR consecutive positions of
-// one kv head and serves all kv_mul query heads of that group from the same
-// K/V rows, so each cache row is read once per step.  CR is sized so that
-// each thread holds exactly NL = 8 sixteen-byte pieces of K and 8 of V:
-//   1. every K/V load of the chunk is issued first, into registers (the rows
-//      before `pos` are already in the cache);
-//   2. while they are in flight, the token's q heads and k/v are read from the
-//      QKV matvec output, QK-normed and rotated, and the chunk that owns
+// Grid = (kv heads, chunks), kv heads varying fastest so that neighbouring
+// workgroups read whole cache rows.  A workgroup owns CR = IT * NL * RPB
+// consecutive positions of one kv head and serves all kv_mul query heads of
+// that group from the same K/V rows, so each cache row is read once per step.
+// Lane (rw, j) of a wave holds 16-byte piece j of row rw of each wave load:
+//   1. loads: the token's q heads / k / v pieces (straight out of the QKV
+//      matvec), the QK-norm weights and the RoPE (cos, sin) of its piece, then
+//      the first batch of NL K pieces and NL V pieces per thread;
+//   2. QK-norm and RoPE in registers: a head's sum of squares is a reduction
+//      over the LPR lanes of its row, a NEOX partner element sits P/2 lanes
+//      away, an interleaved partner in the same lane; the chunk holding
 //      `pos` stores the new k/v row;
-//   3. scores (LPR lanes per row, cross-lane sums), the chunk's softmax
-//      statistics, then p.V, reduced over rows in registers and over waves in
-//      LDS.
-// With one chunk the normalised output is written directly (model.c:57-64
-// order: max, exp, 1/sum).  Otherwise each chunk publishes (o, m, l) and
-// k_attn_merge (one workgroup per query head, the next kernel on the stream)
-// rescales and sums them.  A kernel boundary orders the two; a per-workgroup
-// release fence and counter would cost more than the extra launch here.
+//   3. IT batches, each issuing the next batch's loads before its own scores
+//      (cross-lane sums over the row's lanes), with a running softmax
+//      (max, sum of exp, sum of exp * V) per wave;
+//   4. the four waves' partials combine in LDS.  With one chunk that is the
+//      output (model.c:57-64: max, exp, 1/sum); otherwise the chunk's
+//      (o, m, l) is stored and k_attn_merge, the next kernel, combines them.
+// Measured on the MI355X, the kernel boundary is the cheapest way to order
+// the partials before the merge: a last-arriver merge inside this kernel
+// needs device-scope stores, a wait for their completion and an atomic,
+// three memory round trips on the critical path while the HBM queues are
+// full, and cost more than the extra launch.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace ehip {
@@ -32,13 +40,14 @@ namespace ehip {
 template <int HD, bool F16> struct DecLay {
     static constexpr int PE = F16 ? 8 : 4;                 // elements per 16-byte piece
     static constexpr int P = HD / PE;                      // pieces per row
-    static constexpr int LPR = P <= 4 ? 4 : (P <= 8 ? 8 : (P <= 16 ? 16 : (P <= 32 ? 32 : 64)));
+    static constexpr int LPR = P <= 8 ? 8 : (P <= 16 ? 16 : (P <= 32 ? 32 : 64));
     static constexpr int RPL = 64 / LPR;                   // rows per wave load
     static constexpr int RPB = NWAVE * RPL;                // rows per workgroup load
-    static constexpr int NL = 8;                           // loads per thread, K and V each
-    static constexpr int CR = NL * RPB;                    // positions per chunk
-    static_assert(HD % PE == 0, "head_dim must be a multiple of the piece size");
+    static_assert(HD % PE == 0 && P % 2 == 0, "head_dim must split into an even number of pieces");
 };
+
+template <int HD, bool F16, int NL, int IT>
+constexpr int dec_chunk() { return NL * DecLay<HD, F16>::RPB * IT; }
 
 // Sum over aligned groups of N lanes (N = 8 .. 64), every lane of the group
 // receiving it: DPP moves within rows of 16, lane swaps across rows.
@@ -53,12 +62,26 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// Sum over the lanes i, i + N, i + 2N, ... of the wave (N = 8 .. 64)
+// Sum / maximum over the lanes i, i + N, i + 2N, ... of the wave (N = 8 .. 64)
 template <int N>
 __device__ __forceinline__ float stride_sum(float v) {
     if constexpr (N <= 8) v = xor8_add(v);
     if constexpr (N <= 16) v = xor16_add(v);
     if constexpr (N <= 32) v = xor32_add(v);
+    return v;
+}
+template <int N>
+__device__ __forceinline__ float stride_max(float v) {
+    if constexpr (N <= 8)
+        v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false)));
+    if constexpr (N <= 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    if constexpr (N <= 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
     return v;
 }
 
@@ -77,308 +100,322 @@ __device__ __forceinline__ void piece_to_float(const uint4 &u, float *f) {
     }
 }
 
-// RMSNorm of one head vector held in LDS by one wave (model.c:50-55)
-template <int HD>
-__device__ __forceinline__ void dec_head_norm(float *v, const float *w, float eps, int lane) {
-    float ss = 0.0f;
-    for (int d = lane; d < HD; d += 64) ss += v[d] * v[d];
-    ss = wave_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
-    for (int d = lane; d < HD; d += 64) v[d] = v[d] * scale * w[d];
+template <int PE>
+__device__ __forceinline__ void load_floats(float (&v)[PE], const float *p) {
+#pragma unroll
+    for (int e = 0; e < PE; e += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(p + e);
+        v[e] = f.x; v[e + 1] = f.y; v[e + 2] = f.z; v[e + 3] = f.w;
+    }
 }
 
-template <int HD, int GM, bool F16>
+template <int HD, int GM, bool F16, int NL, int IT>
 __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     using L = DecLay<HD, F16>;
-    constexpr int PE = L::PE, CR = L::CR, NL = L::NL;
-    __shared__ __align__(16) float qs[GM][HD];
-    __shared__ __align__(16) float kn[HD], vn[HD];
-    __shared__ float cs[HD / 2], sn[HD / 2];
-    __shared__ float sc[GM][CR];
-    __shared__ __align__(16) float vacc[NWAVE][GM][HD];
-    __shared__ float ml[GM][2];
+    constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL, RPB = L::RPB;
+    constexpr int BR = NL * RPB;      // rows per batch
+    constexpr int CR = BR * IT;       // rows per chunk
+    __shared__ float sm_m[NWAVE][GM], sm_l[NWAVE][GM];
+    __shared__ __align__(16) float sm_o[NWAVE][GM][HD];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = blockIdx.x, g = blockIdx.y;
+    const int g = blockIdx.x, c = blockIdx.y;   // kv heads vary fastest: neighbours read whole cache rows
     const int G = a.n_heads / a.n_kv;
     const int pos = a.tokpos[1];
-    const int npos = pos + 1;
-    const int nc = (npos + CR - 1) / CR;
+    const int nc = (pos + 1 + CR - 1) / CR;
     if (c >= nc) return;
-    const int t0 = c * CR, t1 = min(npos, t0 + CR);
-    const size_t hoff = (size_t)g * HD;
-    const int j = lane % L::LPR, rw = lane / L::LPR;
-    const bool pj = j < L::P;
-
-    // ---- 1. loads: this token's q heads, k, v and (cos, sin) first, then
-    // every cached K/V row of the chunk (rows before `pos`), all in flight --
-    constexpr int QPT = (GM * HD + WG - 1) / WG;
+    const int t0 = c * CR, t1 = min(pos + 1, t0 + CR);
+    const int j = lane % LPR, rw = lane / LPR;
+    const bool pj = j < P;
+    const int jc = pj ? j : P - 1;   // clamped piece index for loads
     const int qd = a.n_heads * HD;
-    float qv[QPT];
+    const size_t hoff = (size_t)g * HD;
+    const bool neox = a.rope_style == ROPE_NEOX;
+
+    // ---- 1. loads --------------------------------------------------------
+    float qv[GM][PE], kn[PE], vn[PE], qw[PE], kw[PE];
+    float2 cs[PE];
 #pragma unroll
-    for (int r = 0; r < QPT; r++) qv[r] = a.q[(size_t)g * G * HD + min(tid + r * WG, G * HD - 1)];
-    const int dt = min(tid, HD - 1);
-    const float kv0 = a.q[qd + hoff + dt];
-    const float vv0 = a.q[qd + a.kv_dim + hoff + dt];
-    const float2 rp = a.rope[(size_t)pos * (HD / 2) + min(tid, HD / 2 - 1)];
-    uint4 kr[NL], vr[NL];
+    for (int h = 0; h < GM; h++)
+        load_floats<PE>(qv[h], a.q + ((size_t)g * G + min(h, G - 1)) * HD + jc * PE);
+    load_floats<PE>(kn, a.q + qd + hoff + jc * PE);
+    load_floats<PE>(vn, a.q + qd + a.kv_dim + hoff + jc * PE);
+    if (a.q_norm) {
+        load_floats<PE>(qw, a.q_norm + jc * PE);
+        load_floats<PE>(kw, a.k_norm + jc * PE);
+    }
+    {
+        const float2 *rp = a.rope + (size_t)pos * (HD / 2);
+        const int i0 = neox ? (jc % (P / 2)) * PE : jc * (PE / 2);
 #pragma unroll
-    for (int i = 0; i < NL; i++) {
-        const int t = t0 + i * L::RPB + wave * L::RPL + rw;
-        const size_t off = (size_t)min(t, pos) * a.kv_dim + hoff + (size_t)min(j, L::P - 1) * PE;
-        if (F16) {
-            kr[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
-            vr[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
-        } else {
-            kr[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.kc) + off);
-            vr[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.vc) + off);
+        for (int e = 0; e < PE; e += 2) {
+            const float4 f = *reinterpret_cast<const float4 *>(rp + i0 + min(e, neox ? PE - 2 : PE / 2 - 2));
+            cs[e] = make_float2(f.x, f.y);
+            cs[e + 1] = make_float2(f.z, f.w);
         }
     }
-
-    // ---- 2. QK-norm, RoPE and the cache store of this token ----------------
-    {
+    uint4 kr[NL], vr[NL];
+    auto load_batch = [&](int tb) {   // K rows first, then V rows
 #pragma unroll
-        for (int r = 0; r < QPT; r++) {
-            const int i = tid + r * WG;
-            if (i < G * HD) qs[i / HD][i % HD] = qv[r];
+        for (int i = 0; i < NL; i++) {
+            const int t = min(tb + i * RPB + wave * RPL + rw, pos);
+            const size_t off = (size_t)t * a.kv_dim + hoff + (size_t)jc * PE;
+            kr[i] = F16 ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.kc) + off)
+                        : *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.kc) + off);
         }
-        if (tid < HD) { kn[tid] = kv0; vn[tid] = vv0; }
-        if (tid < HD / 2) { cs[tid] = rp.x; sn[tid] = rp.y; }
-        __syncthreads();
-        if (a.q_norm) {   // model.c:386-389, after bias, before RoPE
-            for (int h = wave; h <= G; h += NWAVE)
-                dec_head_norm<HD>(h < G ? qs[h] : kn, h < G ? a.q_norm : a.k_norm, a.eps, lane);
-            __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int t = min(tb + i * RPB + wave * RPL + rw, pos);
+            const size_t off = (size_t)t * a.kv_dim + hoff + (size_t)jc * PE;
+            vr[i] = F16 ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.vc) + off)
+                        : *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.vc) + off);
         }
-        for (int i = tid; i < (G + 1) * (HD / 2); i += WG) {   // model.c:66-80
-            const int h = i / (HD / 2), p = i % (HD / 2);
-            float *v = h < G ? qs[h] : kn;
-            const int ia = a.rope_style == ROPE_NEOX ? p : 2 * p;
-            const int ib = a.rope_style == ROPE_NEOX ? p + HD / 2 : 2 * p + 1;
-            const float v0 = v[ia], v1 = v[ib];
-            v[ia] = v0 * cs[p] - v1 * sn[p];
-            v[ib] = v0 * sn[p] + v1 * cs[p];
-        }
-        __syncthreads();
-        if (F16) {   // the cache holds fp16 (model.c:39-48): attend to the rounded values
-            for (int d = tid; d < HD; d += WG) { kn[d] = h2f(f2h(kn[d])); vn[d] = h2f(f2h(vn[d])); }
-        }
-        if (c == nc - 1) {   // the chunk holding `pos` stores its row
-            const size_t off = (size_t)pos * a.kv_dim + hoff;
-            for (int d = tid; d < HD; d += WG) {
-                if (F16) {
-                    reinterpret_cast<uint16_t *>(a.kc)[off + d] = f2h(kn[d]);
-                    reinterpret_cast<uint16_t *>(a.vc)[off + d] = f2h(vn[d]);
-                } else {
-                    reinterpret_cast<float *>(a.kc)[off + d] = kn[d];
-                    reinterpret_cast<float *>(a.vc)[off + d] = vn[d];
-                }
+    };
+    load_batch(t0);
+
+    // ---- 2. QK-norm (model.c:386-389, after bias, before RoPE) and RoPE
+    // (model.c:66-80) of the group's q heads and of k, in registers --------
+    auto head_norm = [&](float (&v)[PE], const float (&w)[PE]) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PE; e++) ss += v[e] * v[e];
+        ss = group_sum<LPR>(pj ? ss : 0.0f);
+        const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+        for (int e = 0; e < PE; e++) v[e] = v[e] * scale * w[e];
+    };
+    const int partner = lane - j + (jc + P / 2) % P;
+    const bool low = j < P / 2;
+    auto rope = [&](float (&v)[PE]) {
+        if (neox) {   // pairs (i, i + hd/2): the partner piece is P/2 lanes away
+#pragma unroll
+            for (int e = 0; e < PE; e++) {
+                const float pv = __shfl(v[e], partner);
+                v[e] = low ? v[e] * cs[e].x - pv * cs[e].y : pv * cs[e].y + v[e] * cs[e].x;
+            }
+        } else {      // pairs (2i, 2i + 1) inside the piece
+#pragma unroll
+            for (int e = 0; e < PE; e += 2) {
+                const float v0 = v[e], v1 = v[e + 1];
+                const float2 r = cs[e / 2];
+                v[e] = v0 * r.x - v1 * r.y;
+                v[e + 1] = v0 * r.y + v1 * r.x;
             }
         }
-        __syncthreads();
+    };
+    if (a.q_norm) {
+#pragma unroll
+        for (int h = 0; h < GM; h++) head_norm(qv[h], qw);
+        head_norm(kn, kw);
+    }
+#pragma unroll
+    for (int h = 0; h < GM; h++) rope(qv[h]);
+    rope(kn);
+    if (F16) {   // the cache holds fp16 (model.c:39-48): attend to the rounded values
+#pragma unroll
+        for (int e = 0; e < PE; e++) { kn[e] = h2f(f2h(kn[e])); vn[e] = h2f(f2h(vn[e])); }
+    }
+    if (c == nc - 1 && wave == 0 && rw == 0 && pj) {   // the chunk holding `pos` stores its row
+        const size_t off = (size_t)pos * a.kv_dim + hoff + (size_t)j * PE;
+        if constexpr (F16) {
+            uint32_t pk[PE / 2], pv[PE / 2];
+#pragma unroll
+            for (int e = 0; e < PE / 2; e++) {
+                pk[e] = (uint32_t)f2h(kn[2 * e]) | ((uint32_t)f2h(kn[2 * e + 1]) << 16);
+                pv[e] = (uint32_t)f2h(vn[2 * e]) | ((uint32_t)f2h(vn[2 * e + 1]) << 16);
+            }
+            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.kc) + off) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.vc) + off) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
+        } else {
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(a.kc) + off) = make_float4(kn[0], kn[1], kn[2], kn[3]);
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(a.vc) + off) = make_float4(vn[0], vn[1], vn[2], vn[3]);
+        }
     }
 
-    // ---- 3. scores -----------------------------------------------------------
-    float qr[GM][PE];
+    // ---- 3. batches of BR rows: the next batch's loads are issued before the
+    // current batch's scores; a running (max, sum, output) per wave --------
+    float m[GM], l[GM], o[GM][PE];
 #pragma unroll
-    for (int h = 0; h < GM; h++)
+    for (int h = 0; h < GM; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < PE; e++) qr[h][e] = (h < G && pj) ? qs[h][j * PE + e] : 0.0f;
+        for (int e = 0; e < PE; e++) o[h][e] = 0.0f;
+    }
+    for (int it = 0; it < IT; it++) {
+        const int tb = t0 + it * BR;
+        if (tb >= t1) break;
+        uint4 kc[NL], vc[NL];
 #pragma unroll
-    for (int i = 0; i < NL; i++) {
-        const int t = t0 + i * L::RPB + wave * L::RPL + rw;
-        float kf[PE];
-        if (t == pos) {
+        for (int i = 0; i < NL; i++) { kc[i] = kr[i]; vc[i] = vr[i]; }
+        if (it + 1 < IT && tb + BR < t1) load_batch(tb + BR);
+        float sc[NL][GM];
 #pragma unroll
-            for (int e = 0; e < PE; e++) kf[e] = pj ? kn[j * PE + e] : 0.0f;
-        } else {
-            piece_to_float<F16>(kr[i], kf);
+        for (int i = 0; i < NL; i++) {
+            const int t = tb + i * RPB + wave * RPL + rw;
+            float kf[PE];
+            if (t == pos) {
+#pragma unroll
+                for (int e = 0; e < PE; e++) kf[e] = kn[e];
+            } else {
+                piece_to_float<F16>(kc[i], kf);
+            }
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                float sv = 0.0f;
+#pragma unroll
+                for (int e = 0; e < PE; e++) sv += qv[h][e] * kf[e];
+                sc[i][h] = group_sum<LPR>(pj ? sv : 0.0f) * a.inv_sqrt;
+            }
         }
-        float p[GM];
+        float mn[GM];
 #pragma unroll
         for (int h = 0; h < GM; h++) {
-            float s = 0.0f;
+            float mx = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < PE; e++) s += qr[h][e] * kf[e];
-            p[h] = group_sum<L::LPR>(s);
-        }
-        if (j == L::LPR - 1 && t < t1) {
+            for (int i = 0; i < NL; i++)
+                if (tb + i * RPB + wave * RPL + rw < t1) mx = fmaxf(mx, sc[i][h]);
+            mn[h] = fmaxf(m[h], stride_max<LPR>(mx));
+            const float r = m[h] == -INFINITY ? 0.0f : expf(m[h] - mn[h]);
+            l[h] *= r;
 #pragma unroll
-            for (int h = 0; h < GM; h++)
-                if (h < G) sc[h][t - t0] = p[h] * a.inv_sqrt;
-        }
-    }
-    __syncthreads();
-
-    // ---- 4. softmax statistics of the chunk --------------------------------
-    const int len = t1 - t0;
-    for (int h = wave; h < G; h += NWAVE) {
-        float m = -INFINITY;
-        for (int i = lane; i < len; i += 64) m = fmaxf(m, sc[h][i]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int i = lane; i < len; i += 64) { const float e = expf(sc[h][i] - m); sc[h][i] = e; l += e; }
-        l = wave_sum(l);
-        if (nc == 1) {   // whole row here: normalise the weights, as model.c:62-63
-            const float inv = 1.0f / l;
-            for (int i = lane; i < len; i += 64) sc[h][i] *= inv;
-        }
-        if (lane == 0) { ml[h][0] = m; ml[h][1] = l; }
-    }
-    __syncthreads();
-
-    // ---- 5. p . V -------------------------------------------------------------
-    float acc[GM][PE];
-#pragma unroll
-    for (int h = 0; h < GM; h++)
-#pragma unroll
-        for (int e = 0; e < PE; e++) acc[h][e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NL; i++) {
-        const int t = t0 + i * L::RPB + wave * L::RPL + rw;
-        if (t >= t1) continue;
-        float vf[PE];
-        if (t == pos) {
-#pragma unroll
-            for (int e = 0; e < PE; e++) vf[e] = pj ? vn[j * PE + e] : 0.0f;
-        } else {
-            piece_to_float<F16>(vr[i], vf);
+            for (int e = 0; e < PE; e++) o[h][e] *= r;
+            m[h] = mn[h];
         }
 #pragma unroll
-        for (int h = 0; h < GM; h++) {
-            if (h < G) {
-                const float pr = sc[h][t - t0];
+        for (int i = 0; i < NL; i++) {
+            const int t = tb + i * RPB + wave * RPL + rw;
+            if (t >= t1) continue;
+            float vf[PE];
+            if (t == pos) {
 #pragma unroll
-                for (int e = 0; e < PE; e++) acc[h][e] += pr * vf[e];
+                for (int e = 0; e < PE; e++) vf[e] = vn[e];
+            } else {
+                piece_to_float<F16>(vc[i], vf);
+            }
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                const float p = expf(sc[i][h] - m[h]);
+                l[h] += p;
+#pragma unroll
+                for (int e = 0; e < PE; e++) o[h][e] += p * vf[e];
             }
         }
     }
 #pragma unroll
     for (int h = 0; h < GM; h++) {
+        l[h] = stride_sum<LPR>(l[h]);
 #pragma unroll
-        for (int e = 0; e < PE; e++) acc[h][e] = stride_sum<L::LPR>(acc[h][e]);
+        for (int e = 0; e < PE; e++) o[h][e] = stride_sum<LPR>(o[h][e]);
         if (rw == 0 && pj && h < G)
 #pragma unroll
-            for (int e = 0; e < PE; e++) vacc[wave][h][j * PE + e] = acc[h][e];
+            for (int e = 0; e < PE; e++) sm_o[wave][h][j * PE + e] = o[h][e];
+        if (lane == 0 && h < G) { sm_m[wave][h] = m[h]; sm_l[wave][h] = l[h]; }
     }
     __syncthreads();
 
+    // ---- 4. combine the waves; publish or write ----------------------------
+    // Partials: o at part[head][chunk][HD], (m, l) at part_ml[head][chunk][2].
     const size_t head0 = (size_t)g * G;   // first query head of the group
-    if (nc == 1) {
-        for (int i = tid; i < G * HD; i += WG) {
-            const int h = i / HD, d = i % HD;
-            float o = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NWAVE; w++) o += vacc[w][h][d];
-            a.out[(head0 + h) * HD + d] = o;
-        }
-        return;
-    }
-
-    // ---- 6. split: publish (o, m, l) for k_attn_merge ------------------------
-    const int stride = HD + 2;
+    float *part_ml = a.part + (size_t)a.n_heads * a.max_chunks * HD;
     for (int i = tid; i < G * HD; i += WG) {
         const int h = i / HD, d = i % HD;
-        float o = 0.0f;
+        float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NWAVE; w++) o += vacc[w][h][d];
-        a.part[((head0 + h) * a.max_chunks + c) * stride + d] = o;
-    }
-    if (tid < G) {
-        float *pm = a.part + ((head0 + tid) * a.max_chunks + c) * stride + HD;
-        pm[0] = ml[tid][0];
-        pm[1] = ml[tid][1];
+        for (int w = 0; w < NWAVE; w++) M = fmaxf(M, sm_m[w][h]);
+        float O = 0.0f, S = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) {
+            const float mw = sm_m[w][h];
+            const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
+            O += f * sm_o[w][h][d];
+            S += f * sm_l[w][h];
+        }
+        if (nc == 1) {
+            a.out[(head0 + h) * HD + d] = O * (1.0f / S);
+        } else {
+            const size_t slot = (head0 + h) * a.max_chunks + c;
+            a.part[slot * HD + d] = O;
+            if (d == 0) { part_ml[2 * slot] = M; part_ml[2 * slot + 1] = S; }
+        }
     }
 }
 
-// One workgroup per query head: o = sum_k o_k exp(m_k - M) / sum_k l_k exp(m_k - M)
-// over the chunk partials.  Thread (s, d) owns output dim d and the chunks
-// k = s, s + S, ...; its partial loads are issued before the statistics are
-// reduced.  With a single chunk the attention kernel wrote the output.
-constexpr int MERGE_MAX_CHUNKS = 2048;
-constexpr int MERGE_BATCH = 64;
-
+// Split-K merge, one workgroup per query head (the next kernel on the
+// stream, so the partials written above are visible without fences):
+//   o = sum_k o_k e^(m_k - M) / sum_k l_k e^(m_k - M),  M = max_k m_k.
+// Thread (s, q) owns float4 quad q of the head row and chunks k = s, s + NS,
+// ...; every partial it needs is loaded in one batch, issued together with
+// the chunk statistics, before any reduction.
 template <int HD>
 __global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a, int chunk) {
-    constexpr int S = WG / HD;                 // chunk slices
-    __shared__ float fs[MERGE_MAX_CHUNKS];
+    constexpr int QPR = HD / 4, NS = WG / QPR, KB = 16;
+    extern __shared__ __align__(16) float dyn[];   // [max_chunks] float2, then [NS][HD]
     __shared__ float red[NWAVE];
-    __shared__ float osum[S][HD];
-    const int tid = threadIdx.x, h = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
     const int pos = a.tokpos[1];
     const int nc = (pos + 1 + chunk - 1) / chunk;
-    if (nc == 1) return;
-    const int stride = HD + 2;
-    const float *ph = a.part + (size_t)h * a.max_chunks * stride;
-    const int d = tid % HD, sl = tid / HD;
-    const bool act = sl < S;
-    // loads first: this thread's chunk statistics, then its first batch of
-    // partial outputs
-    const int k0s = min(tid, nc - 1);
-    const float m0 = ph[(size_t)k0s * stride + HD], l0 = ph[(size_t)k0s * stride + HD + 1];
-    float po[MERGE_BATCH];
+    if (nc == 1) return;   // the attention kernel wrote the output
+    float2 *sml = reinterpret_cast<float2 *>(dyn);
+    float *slice = dyn + 2 * a.max_chunks;
+    const float *po = a.part + (size_t)h * a.max_chunks * HD;
+    const float2 *pml = reinterpret_cast<const float2 *>(a.part + (size_t)a.n_heads * a.max_chunks * HD) +
+                        (size_t)h * a.max_chunks;
+    const int q = tid % QPR, sl = tid / QPR;
+    const bool act = sl < NS;
+    float4 ov[KB];
+    auto load_round = [&](int r) {
 #pragma unroll
-    for (int b = 0; b < MERGE_BATCH; b++) {
-        const int k = min(sl + b * S, nc - 1);
-        po[b] = act ? ph[(size_t)k * stride + d] : 0.0f;
+        for (int b = 0; b < KB; b++)
+            ov[b] = *reinterpret_cast<const float4 *>(po + (size_t)min(sl + NS * (r * KB + b), nc - 1) * HD + 4 * q);
+    };
+    load_round(0);
+    float mx = -INFINITY;
+    for (int k = tid; k < nc; k += WG) {
+        const float2 v = pml[k];
+        sml[k] = v;
+        mx = fmaxf(mx, v.x);
     }
-    // statistics: chunk maxima, then weights f_k and the denominator
-    float mloc = tid < nc ? m0 : -INFINITY;
-    for (int k = tid + WG; k < nc; k += WG) mloc = fmaxf(mloc, ph[(size_t)k * stride + HD]);
-    mloc = wave_max(mloc);
-    if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
     __syncthreads();
     float M = red[0];
 #pragma unroll
     for (int w = 1; w < NWAVE; w++) M = fmaxf(M, red[w]);
-    __syncthreads();
-    float lloc = 0.0f;
-    if (tid < nc) {
-        const float f = expf(m0 - M);
-        fs[tid] = f;
-        lloc = l0 * f;
+    float sp = 0.0f;
+    for (int k = tid; k < nc; k += WG) {
+        const float f = expf(sml[k].x - M);
+        sml[k].x = f;
+        sp += sml[k].y * f;
     }
-    for (int k = tid + WG; k < nc; k += WG) {
-        const float f = expf(ph[(size_t)k * stride + HD] - M);
-        fs[k] = f;
-        lloc += ph[(size_t)k * stride + HD + 1] * f;
-    }
-    const float L = block_sum(lloc, red);
-    __syncthreads();
-    float o = 0.0f;
+    const float S = block_sum(sp, red);   // its barriers also publish the weights f_k
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int rounds = (nc + NS * KB - 1) / (NS * KB);
+    for (int r = 0; r < rounds; r++) {
+        if (r > 0) load_round(r);
 #pragma unroll
-    for (int b = 0; b < MERGE_BATCH; b++) {
-        const int k = sl + b * S;
-        if (act && k < nc) o += po[b] * fs[k];
-    }
-    for (int k0 = MERGE_BATCH * S; k0 < nc; k0 += MERGE_BATCH * S) {   // beyond the first batch
-#pragma unroll
-        for (int b = 0; b < MERGE_BATCH; b++) {
-            const int k = min(k0 + sl + b * S, nc - 1);
-            po[b] = act ? ph[(size_t)k * stride + d] : 0.0f;
-        }
-#pragma unroll
-        for (int b = 0; b < MERGE_BATCH; b++) {
-            const int k = k0 + sl + b * S;
-            if (act && k < nc) o += po[b] * fs[k];
+        for (int b = 0; b < KB; b++) {
+            const int k = sl + NS * (r * KB + b);
+            const float f = (act && k < nc) ? sml[k].x : 0.0f;
+            acc.x += f * ov[b].x; acc.y += f * ov[b].y; acc.z += f * ov[b].z; acc.w += f * ov[b].w;
         }
     }
-    if (act) osum[sl][d] = o;
+    if (act) *reinterpret_cast<float4 *>(slice + (size_t)sl * HD + 4 * q) = acc;
     __syncthreads();
-    if (tid < HD) {
-        float t = 0.0f;
+    for (int d = tid; d < HD; d += WG) {
+        float O = 0.0f;
 #pragma unroll
-        for (int s2 = 0; s2 < S; s2++) t += osum[s2][tid];
-        a.out[(size_t)h * HD + tid] = t * (1.0f / L);
+        for (int s2 = 0; s2 < NS; s2++) O += slice[(size_t)s2 * HD + d];
+        a.out[(size_t)h * HD + d] = O * (1.0f / S);
     }
 }
 
 // --------------------------------------------------------------------------
 int attn_decode_chunk(int hd, bool f16kv) {
     switch (hd) {
-        case 48: return f16kv ? DecLay<48, true>::CR : DecLay<48, false>::CR;
-        case 64: return f16kv ? DecLay<64, true>::CR : DecLay<64, false>::CR;
-        case 128: return f16kv ? DecLay<128, true>::CR : DecLay<128, false>::CR;
+        case 48: return f16kv ? dec_chunk<48, true, ATT_DEC_NL, ATT_DEC_IT>() : dec_chunk<48, false, ATT_DEC_NL, ATT_DEC_IT>();
+        case 64: return f16kv ? dec_chunk<64, true, ATT_DEC_NL, ATT_DEC_IT>() : dec_chunk<64, false, ATT_DEC_NL, ATT_DEC_IT>();
+        case 128: return f16kv ? dec_chunk<128, true, ATT_DEC_NL, ATT_DEC_IT>() : dec_chunk<128, false, ATT_DEC_NL, ATT_DEC_IT>();
     }
     return 0;
 }
@@ -386,20 +423,22 @@ int attn_decode_chunk(int hd, bool f16kv) {
 template <int HD, bool F16>
 static int dec_pick_g(hipStream_t st, const AttnArgs &a) {
     const int G = a.n_heads / a.n_kv;
-    dim3 grid(a.max_chunks, a.n_kv);
-    if (G <= 1) hipLaunchKernelGGL((k_attn_dec<HD, 1, F16>), grid, dim3(WG), 0, st, a);
-    else if (G <= 2) hipLaunchKernelGGL((k_attn_dec<HD, 2, F16>), grid, dim3(WG), 0, st, a);
-    else if (G <= 4) hipLaunchKernelGGL((k_attn_dec<HD, 4, F16>), grid, dim3(WG), 0, st, a);
-    else if (G <= 8) hipLaunchKernelGGL((k_attn_dec<HD, 8, F16>), grid, dim3(WG), 0, st, a);
+    dim3 grid(a.n_kv, a.max_chunks);
+    constexpr int NL = ATT_DEC_NL, IT = ATT_DEC_IT;
+    if (G <= 1) hipLaunchKernelGGL((k_attn_dec<HD, 1, F16, NL, IT>), grid, dim3(WG), 0, st, a);
+    else if (G <= 2) hipLaunchKernelGGL((k_attn_dec<HD, 2, F16, NL, IT>), grid, dim3(WG), 0, st, a);
+    else if (G <= 4) hipLaunchKernelGGL((k_attn_dec<HD, 4, F16, NL, IT>), grid, dim3(WG), 0, st, a);
+    else if (G <= 8) hipLaunchKernelGGL((k_attn_dec<HD, 8, F16, NL, IT>), grid, dim3(WG), 0, st, a);
     else return -1;
-    hipLaunchKernelGGL((k_attn_merge<HD>), dim3(a.n_heads), dim3(WG), 0, st, a, DecLay<HD, F16>::CR);
+    const size_t lds = 8 * (size_t)a.max_chunks + 4 * (size_t)(WG / (HD / 4)) * HD;
+    hipLaunchKernelGGL((k_attn_merge<HD>), dim3(a.n_heads), dim3(WG), lds, st, a, dec_chunk<HD, F16, NL, IT>());
     return 0;
 }
 
 int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a) {
-    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0) return -1;
+    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || !a.part) return -1;
     const int cr = attn_decode_chunk(a.hd, f16kv);
-    if (cr <= 0 || (a.ctx + cr - 1) / cr > a.max_chunks || a.max_chunks > MERGE_MAX_CHUNKS) return -1;
+    if (cr <= 0 || (a.ctx + cr - 1) / cr > a.max_chunks) return -1;
     switch (a.hd) {
         case 48: return f16kv ? dec_pick_g<48, true>(st, a) : dec_pick_g<48, false>(st, a);
         case 64: return f16kv ? dec_pick_g<64, true>(st, a) : dec_pick_g<64, false>(st, a);

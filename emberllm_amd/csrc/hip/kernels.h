@@ -69,6 +69,8 @@ constexpr int ATT_CHUNK_MAX = 256;  // positions held in LDS per workgroup
 // least ceil(ctx / attn_decode_chunk(hd, f16kv))
 int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a);
 int attn_decode_chunk(int hd, bool f16kv);
+constexpr int ATT_DEC_NL = 4;   // K and V pieces per thread per batch in the decode attention
+constexpr int ATT_DEC_IT = 2;   // batches per chunk
 
 // QK-norm + RoPE of n_tok tokens' q (in place) and k, and the k/v cache
 // store, for prefill.  qkv rows are [q | k | v] with row stride `stride`.

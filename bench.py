@@ -261,8 +261,9 @@ def main():
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(achieved / (HBM_PEAK / 1e9), 4),
                 "traffic": profiled_traffic("ehip::k_attn_dec", args.model, depth, args.kv),
-                "kernel": f"k_attn (split-K GQA attention, one layer) at position {depth}, "
-                          f"{ab} algorithmic bytes per launch, mean of {reps_k} launches"}
+                "kernel": f"k_attn_dec (split-K GQA attention chunk kernel, one layer) at position {depth}, "
+                          f"{ab} algorithmic bytes per launch, mean of {reps_k} launches walking the "
+                          f"{c['n_layers']} layers' caches"}
 
         # ---- depth 128 ------------------------------------------------------
         eng.generate_greedy(tok0, 128, W)

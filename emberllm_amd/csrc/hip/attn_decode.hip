@@ -421,7 +421,7 @@ int attn_decode_chunk(int hd, bool f16kv) {
 }
 
 template <int HD, bool F16>
-static int dec_pick_g(hipStream_t st, const AttnArgs &a) {
+static int dec_pick_g(hipStream_t st, const AttnArgs &a, bool with_merge) {
     const int G = a.n_heads / a.n_kv;
     dim3 grid(a.n_kv, a.max_chunks);
     constexpr int NL = ATT_DEC_NL, IT = ATT_DEC_IT;
@@ -430,19 +430,20 @@ static int dec_pick_g(hipStream_t st, const AttnArgs &a) {
     else if (G <= 4) hipLaunchKernelGGL((k_attn_dec<HD, 4, F16, NL, IT>), grid, dim3(WG), 0, st, a);
     else if (G <= 8) hipLaunchKernelGGL((k_attn_dec<HD, 8, F16, NL, IT>), grid, dim3(WG), 0, st, a);
     else return -1;
+    if (!with_merge) return 0;
     const size_t lds = 8 * (size_t)a.max_chunks + 4 * (size_t)(WG / (HD / 4)) * HD;
     hipLaunchKernelGGL((k_attn_merge<HD>), dim3(a.n_heads), dim3(WG), lds, st, a, dec_chunk<HD, F16, NL, IT>());
     return 0;
 }
 
-int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a) {
+int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_merge) {
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || !a.part) return -1;
     const int cr = attn_decode_chunk(a.hd, f16kv);
     if (cr <= 0 || (a.ctx + cr - 1) / cr > a.max_chunks) return -1;
     switch (a.hd) {
-        case 48: return f16kv ? dec_pick_g<48, true>(st, a) : dec_pick_g<48, false>(st, a);
-        case 64: return f16kv ? dec_pick_g<64, true>(st, a) : dec_pick_g<64, false>(st, a);
-        case 128: return f16kv ? dec_pick_g<128, true>(st, a) : dec_pick_g<128, false>(st, a);
+        case 48: return f16kv ? dec_pick_g<48, true>(st, a, with_merge) : dec_pick_g<48, false>(st, a, with_merge);
+        case 64: return f16kv ? dec_pick_g<64, true>(st, a, with_merge) : dec_pick_g<64, false>(st, a, with_merge);
+        case 128: return f16kv ? dec_pick_g<128, true>(st, a, with_merge) : dec_pick_g<128, false>(st, a, with_merge);
     }
     return -1;
 }

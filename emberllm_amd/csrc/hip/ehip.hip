@@ -366,12 +366,12 @@ static AttnArgs attn_args(EhipState *s, int l) {
     return a;
 }
 
-static int enq_attn_decode(EhipState *s, int l) {
+static int enq_attn_decode(EhipState *s, int l, bool with_merge = true) {
     AttnArgs a = attn_args(s, l);
     a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
     a.part = s->part; a.max_chunks = s->mc_dec;
     a.out = s->o;
-    return launch_attn_decode(s->st, s->f16kv, a);
+    return launch_attn_decode(s->st, s->f16kv, a, with_merge);
 }
 
 static MatvecArgs head_args(EhipState *s, const float *xin) {
@@ -646,16 +646,21 @@ extern "C" int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, flo
     s->tokpos_h[0] = 0;
     s->tokpos_h[1] = pos;
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 8, hipMemcpyHostToDevice, s->st), -1);
+    // successive launches walk through the layers, so each reads weights or
+    // cache rows of its own, as in a decode step (the lm_head is one matrix)
+    const int L = s->m->cfg.n_layers;
+    int i = 0;
     auto one = [&]() -> int {
-        if (kernel == 0) return enq_attn_decode(s, 0);
+        const int l = i++ % L;
+        if (kernel == 0) return enq_attn_decode(s, l, false);
         if (kernel == 1) return enq_head(s, s->x);
-        if (kernel == 2) return enq_w13(s, 0);
+        if (kernel == 2) return enq_w13(s, l);
         return -1;
     };
     if (one()) { set_err("time_kernel: unknown kernel %d", kernel); return -1; }  // warm-up
     HCHK(hipStreamSynchronize(s->st), -1);
     HCHK(hipEventRecord(s->ev0, s->st), -1);
-    for (int i = 0; i < reps; i++) if (one()) return -1;
+    for (int r = 0; r < reps; r++) if (one()) return -1;
     HCHK(hipEventRecord(s->ev1, s->st), -1);
     HCHK(hipEventSynchronize(s->ev1), -1);
     float t = 0.0f;

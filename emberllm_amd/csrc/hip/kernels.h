@@ -67,7 +67,8 @@ int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
 constexpr int ATT_CHUNK_MAX = 256;  // positions held in LDS per workgroup
 // decode (one token, fused QK-norm / RoPE / KV store); max_chunks must be at
 // least ceil(ctx / attn_decode_chunk(hd, f16kv))
-int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a);
+// with_merge = false launches the chunk kernel alone (measurement)
+int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_merge = true);
 int attn_decode_chunk(int hd, bool f16kv);
 constexpr int ATT_DEC_NL = 4;   // K and V pieces per thread per batch in the decode attention
 constexpr int ATT_DEC_IT = 2;   // batches per chunk

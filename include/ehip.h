@@ -96,9 +96,12 @@ int ehip_set_graph_mode(EhipState *s, int mode);
  * the state's stream; writes the average step time in ms.  Tokens follow the
  * reference bench stream (pos*131+7) % vocab. */
 int ehip_time_decode(EhipState *s, int pos0, int steps, float *ms_per_step);
-/* Time `reps` launches of one decode-step kernel in isolation on the
- * state's stream (kernel: 0 = attention of layer 0, 1 = lm_head matvec,
- * 2 = fused w1|w3 matvec of layer 0) at position pos; writes average ms. */
+/* Time `reps` back-to-back launches of one decode-step kernel on the
+ * state's stream with HIP events, at position pos; writes average ms.
+ * kernel: 0 = the split-K attention chunk kernel (without its merge),
+ * 1 = lm_head matvec, 2 = fused w1|w3 matvec.  Launches of kernels 0 and 2
+ * walk through the layers, so each streams its own cache rows or weights
+ * from HBM as in a decode step. */
 int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms_per_launch);
 
 #ifdef __cplusplus

@@ -5,36 +5,240 @@
 // QK-norm / RoPE / kv_store loop (model.c:323-333, k_qkpost).  The decode
 // form lives in attn_decode.hip.
 //
-// Roofline: HBM-bound.  Algorithmic bytes per decode step and layer =
-// 2 * (pos+1) * kv_dim * esize (K and V read once) + 2 * kv_dim * esize (the
-// new position written).
-//
-// Grid = (chunks, kv heads, tokens).  A workgroup owns one kv head and one
-// chunk of positions, and computes all kv_mul query heads of that group from
-// the same K/V rows, so each cache row is read once per step.  Lanes are laid
-// out LPR per cache row (4 elements each): a wave load covers 64/LPR whole
-// rows.  Scores for the chunk stay in LDS; each chunk produces (max, sum,
-// unnormalised output) and the last workgroup of the (token, kv head) to
-// finish — detected with an agent-scope atomic counter — merges them.  The
-// split keeps >= 256 workgroups busy at long context with only 8 kv heads.
+// The reference's activations are re-quantized to Q8_0 before every matmul,
+// so a one-ulp difference in an attention output can move an int8 code and
+// cascade through the following layers.  Prefill attention therefore keeps
+// the reference's floating-point order exactly, and gets its speed from
+// parallelism across (head, token, key) and from sharing every K/V tile in
+// LDS among many rows, in three kernels per layer:
+//   k_pf_scores   s[h][b][t] = (sum over d in order of q*k) / sqrt(hd), one
+//                 lane per key, each lane carrying up to 8 (token, head)
+//                 rows of its kv group; K tile and Q rows staged in LDS
+//   k_pf_softmax  per row: max, e_t = expf(s_t - max) (in place), the sum
+//                 taken in t order by one lane per row, 1/sum
+//                 (model.c:57-64)
+//   k_pf_pv       o[b][h][d] = sum over t in order of (e_t * (1/sum)) * v_t[d],
+//                 one thread per (row set, d); V tile and probabilities
+//                 staged in LDS
+// Roofline: VALU-bound, 2 * hd multiply-adds per (head, token, key) pair,
+// each as a separately rounded multiply and add like the reference's
+// -ffp-contract=off build.
 #include "kernels.h"
 
 namespace ehip {
 
-template <int HD> struct Lay {
-    static constexpr int P = HD / 4;                        // 4-element pieces per row
-    static constexpr int LPR = P <= 8 ? 8 : (P <= 16 ? 16 : (P <= 32 ? 32 : 64));
-    static constexpr int RPL = 64 / LPR;                    // rows per wave load
-};
+constexpr int PF_KT = 64;   // keys per tile
 
-template <bool F16>
-__device__ __forceinline__ float4 load4(const void *base, size_t idx) {
-    if (F16) {
-        const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(base) + idx);
-        return make_float4(h2f((uint16_t)(u.x & 0xffff)), h2f((uint16_t)(u.x >> 16)),
-                           h2f((uint16_t)(u.y & 0xffff)), h2f((uint16_t)(u.y >> 16)));
-    } else {
-        return *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(base) + idx);
+// rows of (token, head) per lane or thread: tokens x heads <= 8
+template <int GM> struct PfRows { static constexpr int QW = GM >= 8 ? 1 : 8 / GM; };
+
+template <int HD, bool F16>
+__device__ __forceinline__ void stage_rows(float *dst, int pitch, const void *cache, int kv_dim, size_t hoff,
+                                           int t0, int tmax, int tid) {
+    // PF_KT rows of hd elements of one kv head, widened to fp32, row t at dst + t * pitch
+    constexpr int F4 = HD / 4;
+    for (int f = tid; f < PF_KT * F4; f += WG) {
+        const int t = f / F4, c = (f % F4) * 4;
+        const size_t off = (size_t)min(t0 + t, tmax) * kv_dim + hoff + c;
+        float4 v;
+        if (F16) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(cache) + off);
+            v = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
+        } else {
+            v = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(cache) + off);
+        }
+        *reinterpret_cast<float4 *>(dst + t * pitch + c) = v;
+    }
+}
+
+// grid (key tiles, token tiles of 4*QW, kv groups); wave w carries tokens
+// b0 + w*QW .. + QW-1 and the group's heads; lane = key
+template <int HD, int GM, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
+    constexpr int QW = PfRows<GM>::QW, QT = 4 * QW, KP = HD + 4;
+    __shared__ __align__(16) float ks[PF_KT * KP];
+    __shared__ __align__(16) float qs[QT * GM * HD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.n_heads / a.n_kv, g = blockIdx.z;
+    const int kt0 = blockIdx.x * PF_KT, b0 = blockIdx.y * QT;
+    const int blast = min(a.n_tok, b0 + QT) - 1;
+    if (b0 >= a.n_tok || kt0 > a.pos_base + blast) return;   // causal: no key of this tile is visible
+    stage_rows<HD, F16>(ks, KP, a.kc, a.kv_dim, (size_t)g * HD, kt0, a.pos_base + blast, tid);
+    for (int f = tid; f < QT * GM * (HD / 4); f += WG) {
+        const int r = f / (HD / 4), c = (f % (HD / 4)) * 4;
+        const int qb = r / GM, h = r % GM;
+        const int b = min(b0 + qb, a.n_tok - 1);
+        const float4 v = *reinterpret_cast<const float4 *>(
+            a.q + (size_t)b * a.q_stride + (size_t)(g * G + min(h, G - 1)) * HD + c);
+        *reinterpret_cast<float4 *>(&qs[r * HD + c]) = v;
+    }
+    __syncthreads();
+    float acc[QW][GM];
+#pragma unroll
+    for (int i = 0; i < QW; i++)
+#pragma unroll
+        for (int h = 0; h < GM; h++) acc[i][h] = 0.0f;
+    const float *kr = &ks[lane * KP];
+    const float *qw = &qs[wave * QW * GM * HD];
+    for (int d = 0; d < HD; d += 4) {
+        const float4 kf = *reinterpret_cast<const float4 *>(kr + d);
+#pragma unroll
+        for (int i = 0; i < QW; i++)
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                const float4 qf = *reinterpret_cast<const float4 *>(qw + (i * GM + h) * HD + d);
+                float s = acc[i][h];            // dims in order, multiply and add rounded apart
+                s = s + qf.x * kf.x;
+                s = s + qf.y * kf.y;
+                s = s + qf.z * kf.z;
+                s = s + qf.w * kf.w;
+                acc[i][h] = s;
+            }
+    }
+    const int t = kt0 + lane;
+#pragma unroll
+    for (int i = 0; i < QW; i++) {
+        const int b = b0 + wave * QW + i;
+        if (b >= a.n_tok || t > a.pos_base + b) continue;
+#pragma unroll
+        for (int h = 0; h < GM; h++)
+            if (h < G) a.scores[((size_t)(g * G + h) * a.n_tok + b) * a.ldk + t] = acc[i][h] * a.inv_sqrt;
+    }
+}
+
+// grid (n_heads * n_tok / 64 rounded up); 64 rows per workgroup.  Every
+// loop issues a batch of independent loads before using any of them.
+constexpr int SM_B = 8;
+__global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nrows = a.n_heads * a.n_tok;
+    const int r0 = blockIdx.x * 64;
+    // 1. each wave: max and exponentials of 16 rows, lanes across positions
+    for (int k = 0; k < 16; k++) {
+        const int r = r0 + wave * 16 + k;
+        if (r >= nrows) break;
+        const int b = r % a.n_tok, len = a.pos_base + b + 1;
+        float *row = a.scores + (size_t)r * a.ldk;
+        float mx = -INFINITY;
+        for (int t0 = 0; t0 < len; t0 += 64 * SM_B) {
+            float v[SM_B];
+#pragma unroll
+            for (int i = 0; i < SM_B; i++) v[i] = row[min(t0 + lane + 64 * i, len - 1)];
+#pragma unroll
+            for (int i = 0; i < SM_B; i++) mx = fmaxf(mx, v[i]);
+        }
+        mx = wave_max(mx);
+        for (int t0 = 0; t0 < len; t0 += 64 * SM_B) {
+            float v[SM_B];
+#pragma unroll
+            for (int i = 0; i < SM_B; i++) v[i] = row[min(t0 + lane + 64 * i, len - 1)];
+#pragma unroll
+            for (int i = 0; i < SM_B; i++)
+                if (t0 + lane + 64 * i < len) row[t0 + lane + 64 * i] = expf(v[i] - mx);
+        }
+    }
+    __syncthreads();
+    // 2. one lane per row: the sum in position order, then 1/sum; batches of
+    // SM_B float4 double-buffered so the loads run ahead of the adds
+    if (wave == 0) {
+        const int r = min(r0 + lane, nrows - 1);
+        const int b = r % a.n_tok, len = a.pos_base + b + 1;
+        const float *row = a.scores + (size_t)r * a.ldk;
+        const int last4 = a.ldk - 4;   // loads stay inside the row
+        float4 cur[SM_B], nxt[SM_B];
+#pragma unroll
+        for (int i = 0; i < SM_B; i++) cur[i] = *reinterpret_cast<const float4 *>(row + min(4 * i, last4));
+        float sum = 0.0f;
+        for (int t0 = 0; t0 < len; t0 += 4 * SM_B) {
+            if (t0 + 4 * SM_B < len) {
+#pragma unroll
+                for (int i = 0; i < SM_B; i++)
+                    nxt[i] = *reinterpret_cast<const float4 *>(row + min(t0 + 4 * SM_B + 4 * i, last4));
+            }
+#pragma unroll
+            for (int i = 0; i < SM_B; i++) {
+                const int t = t0 + 4 * i;
+                if (t < len) sum = sum + cur[i].x;
+                if (t + 1 < len) sum = sum + cur[i].y;
+                if (t + 2 < len) sum = sum + cur[i].z;
+                if (t + 3 < len) sum = sum + cur[i].w;
+            }
+#pragma unroll
+            for (int i = 0; i < SM_B; i++) cur[i] = nxt[i];
+        }
+        if (r0 + lane < nrows) a.rowinv[r] = 1.0f / sum;
+    }
+}
+
+// grid (token tiles of QT, kv groups); thread (row set, d) with d = tid % HD
+template <int HD, int GM, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
+    constexpr int QW = PfRows<GM>::QW, QT = 4 * QW, R = QT * GM;
+    constexpr int NSET = WG / HD, RS = (R + NSET - 1) / NSET;   // rows per thread
+    constexpr int VP = HD + 4;
+    __shared__ __align__(16) float vs[PF_KT * VP];
+    __shared__ __align__(16) float ps[R * PF_KT];
+    const int tid = threadIdx.x;
+    const int G = a.n_heads / a.n_kv, g = blockIdx.y;
+    const int b0 = blockIdx.x * QT;
+    if (b0 >= a.n_tok) return;
+    const int blast = min(a.n_tok, b0 + QT) - 1;
+    const int tmax = a.pos_base + blast;                  // last key any row here needs
+    const int d = tid % HD, set = tid / HD;
+    const bool act = set < NSET;
+    float acc[RS];
+    int rpos[RS];
+#pragma unroll
+    for (int k = 0; k < RS; k++) {
+        acc[k] = 0.0f;
+        const int r = set * RS + k;                       // row = (token r / GM, head r % GM)
+        const int b = b0 + r / GM, h = r % GM;
+        rpos[k] = (act && r < R && b < a.n_tok && h < G) ? a.pos_base + b : -1;
+    }
+    for (int t0 = 0; t0 <= tmax; t0 += PF_KT) {
+        __syncthreads();
+        stage_rows<HD, F16>(vs, VP, a.vc, a.kv_dim, (size_t)g * HD, t0, tmax, tid);
+        for (int f = tid; f < R * (PF_KT / 4); f += WG) {   // p = e * (1/sum), model.c:62-63
+            const int r = f / (PF_KT / 4), c = (f % (PF_KT / 4)) * 4;
+            const int b = b0 + r / GM, h = r % GM;
+            float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (b < a.n_tok && h < G) {
+                const size_t row = (size_t)(g * G + h) * a.n_tok + b;
+                const int len = a.pos_base + b + 1;
+                if (t0 + c < len) {
+                    const float inv = a.rowinv[row];
+                    const float4 e = *reinterpret_cast<const float4 *>(a.scores + row * a.ldk + t0 + c);
+                    p = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
+                }
+            }
+            *reinterpret_cast<float4 *>(&ps[r * PF_KT + c]) = p;
+        }
+        __syncthreads();
+        if (!act) continue;
+        for (int t = 0; t < PF_KT; t += 4) {
+            const float v0 = vs[t * VP + d], v1 = vs[(t + 1) * VP + d];
+            const float v2 = vs[(t + 2) * VP + d], v3 = vs[(t + 3) * VP + d];
+#pragma unroll
+            for (int k = 0; k < RS; k++) {
+                const int r = min(set * RS + k, R - 1);
+                const float4 p = *reinterpret_cast<const float4 *>(&ps[r * PF_KT + t]);
+                const int lim = rpos[k] - (t0 + t);   // positions t0+t .. t0+t+lim are visible
+                float o = acc[k];
+                if (lim >= 0) o = o + p.x * v0;
+                if (lim >= 1) o = o + p.y * v1;
+                if (lim >= 2) o = o + p.z * v2;
+                if (lim >= 3) o = o + p.w * v3;
+                acc[k] = o;
+            }
+        }
+    }
+    if (!act) return;
+#pragma unroll
+    for (int k = 0; k < RS; k++) {
+        if (rpos[k] < 0) continue;
+        const int r = set * RS + k;
+        const int b = b0 + r / GM, h = r % GM;
+        a.out[(size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + d] = acc[k];
     }
 }
 
@@ -57,159 +261,6 @@ __device__ __forceinline__ void rope_pair(float *v, int i, int hd, float2 cs, in
     const float v0 = v[ia], v1 = v[ib];
     v[ia] = v0 * cs.x - v1 * cs.y;
     v[ib] = v0 * cs.y + v1 * cs.x;
-}
-
-template <int HD, int GM, bool F16>
-__global__ __launch_bounds__(WG) void k_attn(AttnArgs a) {
-    using L = Lay<HD>;
-    __shared__ __align__(16) float qs[GM][HD];
-    __shared__ float sc[GM][ATT_CHUNK_MAX];
-    __shared__ __align__(16) float vacc[NWAVE][GM][HD];
-    __shared__ float ml[GM][2];
-    __shared__ int is_last;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int G = a.n_heads / a.n_kv;
-    const int pos = a.pos_base + b;
-    const int npos = pos + 1;
-
-    // chunking, identical in every workgroup of this (token, kv head)
-    int nc = (npos + a.min_chunk - 1) / a.min_chunk;
-    if (nc > a.max_chunks) nc = a.max_chunks;
-    const int need = (npos + ATT_CHUNK_MAX - 1) / ATT_CHUNK_MAX;
-    if (nc < need) nc = need;
-    const int clen = (npos + nc - 1) / nc;
-    nc = (npos + clen - 1) / clen;
-    if (c >= nc) return;
-    const int t0 = c * clen, t1 = min(npos, t0 + clen), len = t1 - t0;
-    const size_t hoff = (size_t)g * HD;
-
-    // ---- prologue: q rows of the group --------------------------------------
-    {
-        const float *qrow = a.q + (size_t)b * a.q_stride + (size_t)g * G * HD;
-        for (int i = tid; i < G * HD; i += WG) qs[i / HD][i % HD] = qrow[i];
-        __syncthreads();
-    }
-
-    const int j = lane % L::LPR, rw = lane / L::LPR;
-    const bool pj = j < L::P;
-    float4 qr[GM];
-#pragma unroll
-    for (int h = 0; h < GM; h++)
-        qr[h] = (h < G && pj) ? *reinterpret_cast<const float4 *>(&qs[h][4 * j]) : make_float4(0, 0, 0, 0);
-
-    // ---- scores --------------------------------------------------------
-    for (int t = t0 + wave * L::RPL + rw; t < t1; t += NWAVE * L::RPL) {
-        float4 k4 = make_float4(0, 0, 0, 0);
-        if (pj) k4 = load4<F16>(a.kc, (size_t)t * a.kv_dim + hoff + 4 * j);
-        float p[GM];
-#pragma unroll
-        for (int h = 0; h < GM; h++) {
-            p[h] = qr[h].x * k4.x + qr[h].y * k4.y + qr[h].z * k4.z + qr[h].w * k4.w;
-#pragma unroll
-            for (int off = 1; off < L::LPR; off <<= 1) p[h] += __shfl_xor(p[h], off);
-        }
-        if (j == 0) {
-#pragma unroll
-            for (int h = 0; h < GM; h++)
-                if (h < G) sc[h][t - t0] = p[h] * a.inv_sqrt;
-        }
-    }
-    __syncthreads();
-
-    // ---- softmax statistics of the chunk -------------------------------
-    for (int h = wave; h < G; h += NWAVE) {
-        float m = -INFINITY;
-        for (int i = lane; i < len; i += 64) m = fmaxf(m, sc[h][i]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int i = lane; i < len; i += 64) { const float e = expf(sc[h][i] - m); sc[h][i] = e; l += e; }
-        l = wave_sum(l);
-        if (nc == 1) {  // whole row here: normalise first, as model.c:62-63
-            const float inv = 1.0f / l;
-            for (int i = lane; i < len; i += 64) sc[h][i] *= inv;
-        }
-        if (lane == 0) { ml[h][0] = m; ml[h][1] = l; }
-    }
-    __syncthreads();
-
-    // ---- p . V ----------------------------------------------------------
-    float4 acc[GM];
-#pragma unroll
-    for (int h = 0; h < GM; h++) acc[h] = make_float4(0, 0, 0, 0);
-    for (int t = t0 + wave * L::RPL + rw; t < t1; t += NWAVE * L::RPL) {
-        float4 v4 = make_float4(0, 0, 0, 0);
-        if (pj) v4 = load4<F16>(a.vc, (size_t)t * a.kv_dim + hoff + 4 * j);
-#pragma unroll
-        for (int h = 0; h < GM; h++) {
-            if (h < G) {
-                const float pr = sc[h][t - t0];
-                acc[h].x += pr * v4.x; acc[h].y += pr * v4.y;
-                acc[h].z += pr * v4.z; acc[h].w += pr * v4.w;
-            }
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < GM; h++) {
-#pragma unroll
-        for (int off = L::LPR; off < 64; off <<= 1) {
-            acc[h].x += __shfl_xor(acc[h].x, off); acc[h].y += __shfl_xor(acc[h].y, off);
-            acc[h].z += __shfl_xor(acc[h].z, off); acc[h].w += __shfl_xor(acc[h].w, off);
-        }
-        if (rw == 0 && pj && h < G) *reinterpret_cast<float4 *>(&vacc[wave][h][4 * j]) = acc[h];
-    }
-    __syncthreads();
-
-    const size_t head0 = (size_t)b * a.n_heads + (size_t)g * G;   // first query head row
-    if (nc == 1) {
-        for (int i = tid; i < G * HD; i += WG) {
-            const int h = i / HD, d = i % HD;
-            float o = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NWAVE; w++) o += vacc[w][h][d];
-            a.out[(head0 + h) * HD + d] = o;
-        }
-        return;
-    }
-
-    // ---- split: publish the partial, last workgroup merges --------------
-    const int stride = HD + 2;
-    for (int i = tid; i < G * HD; i += WG) {
-        const int h = i / HD, d = i % HD;
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NWAVE; w++) o += vacc[w][h][d];
-        a.part[((head0 + h) * a.max_chunks + c) * stride + d] = o;
-    }
-    if (tid < G) {
-        float *pm = a.part + ((head0 + tid) * a.max_chunks + c) * stride + HD;
-        pm[0] = ml[tid][0]; pm[1] = ml[tid][1];
-    }
-    __threadfence();
-    __syncthreads();
-    unsigned *ctr = a.counters + (size_t)b * a.n_kv + g;
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = prev == (unsigned)(nc - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    for (int i = tid; i < G * HD; i += WG) {
-        const int h = i / HD, d = i % HD;
-        const float *ph = a.part + (head0 + h) * a.max_chunks * stride;
-        float M = -INFINITY;
-        for (int k = 0; k < nc; k++) M = fmaxf(M, ph[k * stride + HD]);
-        float Ls = 0.0f, O = 0.0f;
-        for (int k = 0; k < nc; k++) {
-            const float f = expf(ph[k * stride + HD] - M);
-            Ls += ph[k * stride + HD + 1] * f;
-            O += ph[k * stride + d] * f;
-        }
-        a.out[(head0 + h) * HD + d] = O * (1.0f / Ls);
-    }
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- prefill QK-norm + RoPE + KV store -----------------------------------
@@ -245,29 +296,33 @@ __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
 
 // --------------------------------------------------------------------------
 template <int HD, int GM, bool F16>
-static void go_attn(hipStream_t st, const AttnArgs &a) {
-    dim3 grid(a.max_chunks, a.n_kv, a.n_tok);
-    hipLaunchKernelGGL((k_attn<HD, GM, F16>), grid, dim3(WG), 0, st, a);
+static void pf_go(hipStream_t st, const AttnArgs &a) {
+    constexpr int QT = 4 * PfRows<GM>::QW;
+    const int ktiles = (a.pos_base + a.n_tok + PF_KT - 1) / PF_KT;
+    const int qtiles = (a.n_tok + QT - 1) / QT;
+    hipLaunchKernelGGL((k_pf_scores<HD, GM, F16>), dim3(ktiles, qtiles, a.n_kv), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(k_pf_softmax, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL((k_pf_pv<HD, GM, F16>), dim3(qtiles, a.n_kv), dim3(WG), 0, st, a);
 }
 
 template <int HD, bool F16>
-static int pick_g(hipStream_t st, const AttnArgs &a) {
+static int pf_pick_g(hipStream_t st, const AttnArgs &a) {
     const int G = a.n_heads / a.n_kv;
-    if (G <= 1) go_attn<HD, 1, F16>(st, a);
-    else if (G <= 2) go_attn<HD, 2, F16>(st, a);
-    else if (G <= 4) go_attn<HD, 4, F16>(st, a);
-    else if (G <= 8) go_attn<HD, 8, F16>(st, a);
+    if (G <= 1) pf_go<HD, 1, F16>(st, a);
+    else if (G <= 2) pf_go<HD, 2, F16>(st, a);
+    else if (G <= 4) pf_go<HD, 4, F16>(st, a);
+    else if (G <= 8) pf_go<HD, 8, F16>(st, a);
     else return -1;
     return 0;
 }
 
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a) {
-    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0) return -1;
-    if ((a.ctx + ATT_CHUNK_MAX - 1) / ATT_CHUNK_MAX > a.max_chunks) return -1;
+    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || !a.scores || !a.rowinv) return -1;
+    if (a.ldk < a.pos_base + a.n_tok || a.ldk % 4) return -1;
     switch (a.hd) {
-        case 48: return f16kv ? pick_g<48, true>(st, a) : pick_g<48, false>(st, a);
-        case 64: return f16kv ? pick_g<64, true>(st, a) : pick_g<64, false>(st, a);
-        case 128: return f16kv ? pick_g<128, true>(st, a) : pick_g<128, false>(st, a);
+        case 48: return f16kv ? pf_pick_g<48, true>(st, a) : pf_pick_g<48, false>(st, a);
+        case 64: return f16kv ? pf_pick_g<64, true>(st, a) : pf_pick_g<64, false>(st, a);
+        case 128: return f16kv ? pf_pick_g<128, true>(st, a) : pf_pick_g<128, false>(st, a);
     }
     return -1;
 }

@@ -224,7 +224,8 @@ fail:
 }
 
 // ---------------------------------------------------------------- state ----
-constexpr int PF_CHUNK = 256;  // prefill tokens per pass through the layers
+constexpr int PF_CHUNK = 2048;  // prefill tokens per pass through the layers (at most)
+constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores per pass (at most)
 
 struct EhipState {
     EhipModel *m;
@@ -237,9 +238,10 @@ struct EhipState {
     float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
     int mc_dec;
     // prefill scratch
-    float *X, *QKV, *O, *H, *xf, *dxp, *part_pf;
-    int8_t *qx; int *xsum, *ids_d; unsigned *ctr_pf;
-    int mc_pf;
+    float *X, *QKV, *O, *H, *xf, *dxp;
+    int8_t *qx; int *xsum, *ids_d;
+    float *pf_scores, *pf_rowinv;   // prefill attention scratch [n_heads][pf_chunk][ldk], [n_heads][pf_chunk]
+    int pf_chunk;       // tokens per prefill pass
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
@@ -289,7 +291,6 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     const size_t kvb = (size_t)c.n_layers * ctx * kvd * s->esize;
-    const int need = (ctx + ATT_CHUNK_MAX - 1) / ATT_CHUNK_MAX;
     const int dch = attn_decode_chunk(hd, s->f16kv != 0);
     if (dch <= 0) {
         set_err("head_dim %d not supported by the attention kernel", hd);
@@ -297,7 +298,10 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     s->mc_dec = (ctx + dch - 1) / dch;
-    s->mc_pf = need;
+    const size_t ldk_max = (size_t)attn_prefill_ldk(0, ctx);
+    s->pf_chunk = (int)std::max<size_t>(1, std::min<size_t>(std::min(PF_CHUNK, ctx),
+                                                            PF_SCORES_MAX / (4 * ldk_max * c.n_heads)));
+    const size_t pfc = (size_t)s->pf_chunk;
     const int wide = std::max(std::max(c.dim, c.hidden_dim), qd);
     bool ok = (s->kc = salloc(s, kvb, true)) && (s->vc = salloc(s, kvb, true)) &&
               (s->tokpos_d = (int *)salloc(s, 16, true)) &&
@@ -307,20 +311,20 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->h = (float *)salloc(s, 4 * (size_t)c.hidden_dim)) &&
               (s->logits_d = (float *)salloc(s, 4 * (size_t)c.vocab_size, true)) &&
               (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * s->mc_dec * (hd + 2))) &&
-              (s->X = (float *)salloc(s, 4 * (size_t)PF_CHUNK * c.dim)) &&
-              (s->QKV = (float *)salloc(s, 4 * (size_t)PF_CHUNK * (qd + 2 * kvd))) &&
-              (s->O = (float *)salloc(s, 4 * (size_t)PF_CHUNK * qd)) &&
-              (s->H = (float *)salloc(s, 4 * (size_t)PF_CHUNK * 2 * c.hidden_dim)) &&
-              (s->qx = (int8_t *)salloc(s, (size_t)PF_CHUNK * wide)) &&
-              (s->dxp = (float *)salloc(s, 4 * (size_t)PF_CHUNK * (wide / QB + 1))) &&
-              (s->xsum = (int *)salloc(s, 4 * (size_t)PF_CHUNK * (wide / QB + 1))) &&
-              (s->ids_d = (int *)salloc(s, 4 * (size_t)PF_CHUNK)) &&
-              (s->part_pf = (float *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_heads * s->mc_pf * (hd + 2))) &&
-              (s->ctr_pf = (unsigned *)salloc(s, 4 * (size_t)PF_CHUNK * c.n_kv_heads, true)) &&
+              (s->X = (float *)salloc(s, 4 * pfc * c.dim)) &&
+              (s->QKV = (float *)salloc(s, 4 * pfc * (qd + 2 * kvd))) &&
+              (s->O = (float *)salloc(s, 4 * pfc * qd)) &&
+              (s->H = (float *)salloc(s, 4 * pfc * 2 * c.hidden_dim)) &&
+              (s->qx = (int8_t *)salloc(s, pfc * wide)) &&
+              (s->dxp = (float *)salloc(s, 4 * pfc * (wide / QB + 1))) &&
+              (s->xsum = (int *)salloc(s, 4 * pfc * (wide / QB + 1))) &&
+              (s->ids_d = (int *)salloc(s, 4 * pfc)) &&
+              (s->pf_scores = (float *)salloc(s, 4 * pfc * ldk_max * c.n_heads)) &&
+              (s->pf_rowinv = (float *)salloc(s, 4 * pfc * c.n_heads)) &&
               (s->am_val = (float *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->am_idx = (int *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true));
-    if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * (size_t)PF_CHUNK * wide)) != nullptr;
+    if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
     if (ok) {
         // RoPE table with the reference's arithmetic (model.c:69-71): the
         // angle pos * freq in fp32, then the host libm cosf / sinf
@@ -523,8 +527,8 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
     const EhipConfig &c = m->cfg;
     const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd, hid = c.hidden_dim;
     const int stride = qd + 2 * kvd;
-    for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {
-        const int mt = std::min(PF_CHUNK, n - c0);
+    for (int c0 = 0; c0 < n; c0 += s->pf_chunk) {
+        const int mt = std::min(s->pf_chunk, n - c0);
         HCHK(hipMemcpyAsync(s->ids_d, ids + c0, 4 * (size_t)mt, hipMemcpyHostToDevice, s->st), nullptr);
         for (int l = 0; l < c.n_layers; l++) {
             const DevLayer &y = m->layers[l];
@@ -546,8 +550,8 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             p.n_kv = c.n_kv_heads; p.pos_base = start + c0; p.n_tok = mt;
             rc |= launch_qkpost(s->st, s->f16kv, p);
             at.q = s->QKV; at.q_stride = stride; at.pos_base = start + c0; at.n_tok = mt;
-            at.part = s->part_pf; at.counters = s->ctr_pf; at.max_chunks = s->mc_pf;
-            at.min_chunk = ATT_CHUNK_MAX; at.out = s->O;
+            at.out = s->O;
+            at.scores = s->pf_scores; at.rowinv = s->pf_rowinv; at.ldk = attn_prefill_ldk(start + c0, mt);
             rc |= launch_attention(s->st, s->f16kv, at);
             QuantRowsArgs q2{};
             q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;

@@ -39,9 +39,9 @@ constexpr int MATVEC_MAX_GRID = 2048;
 int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
 
 // ------------------------------------------------------------- attention --
-// GQA attention of n_tok query tokens against the cache, split over chunks
-// of positions (flash-decoding); the last workgroup of each (token, kv head)
-// combines the chunk partials.  In the decode form the single token's raw
+// GQA attention against the cache.  Prefill: causal flash attention of n_tok
+// query tokens on the fp32 matrix cores.  Decode: one token, split over
+// chunks of positions (flash-decoding) with a merge kernel; the token's raw
 // q/k/v (straight out of the QKV matvec) is QK-normed and rotated in the
 // prologue and its k/v are written to the cache at `pos` by the chunk that
 // owns it.
@@ -57,14 +57,17 @@ struct AttnArgs {
     const int *tokpos;     // fused (decode): device {tok, pos}
     int pos_base;          // unfused (prefill): token b sits at pos_base + b
     int n_tok;
-    float *part;           // [n_tok][n_heads][max_chunks][hd + 2]
-    unsigned *counters;    // [n_tok][n_kv], zero between launches
-    int max_chunks, min_chunk;
+    float *part;           // decode: chunk partials, o [n_heads][max_chunks][hd] then (m, l) [n_heads][max_chunks]
+    int max_chunks;
     float *out;            // [n_tok][n_heads*hd]
+    // prefill scratch: scores, then probabilities, [n_heads][n_tok][ldk]
+    // (ldk >= pos_base + n_tok, a multiple of 4) and 1/sum per row [n_heads][n_tok]
+    float *scores, *rowinv;
+    int ldk;
 };
 // prefill: q rows already normed and rotated, k/v already in the cache
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
-constexpr int ATT_CHUNK_MAX = 256;  // positions held in LDS per workgroup
+inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }
 // decode (one token, fused QK-norm / RoPE / KV store); max_chunks must be at
 // least ceil(ctx / attn_decode_chunk(hd, f16kv))
 // with_merge = false launches the chunk kernel alone (measurement)

@@ -170,13 +170,18 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
     }
 }
 
-// grid (token tiles of QT, kv groups); thread (row set, d) with d = tid % HD
+// grid (token tiles of QT, kv groups); thread (row set, d) with d = tid % HD.
+// V is staged transposed (vt[d][t]) so a thread reads four positions of its
+// dim in one 16-byte load; probabilities past a row's position are staged as
+// zero, and adding a zero product leaves a nonzero sum bit-identical (a sum
+// that is exactly zero can at most change the sign of that zero, which no
+// later operation observes).
 template <int HD, int GM, bool F16>
 __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
     constexpr int QW = PfRows<GM>::QW, QT = 4 * QW, R = QT * GM;
     constexpr int NSET = WG / HD, RS = (R + NSET - 1) / NSET;   // rows per thread
-    constexpr int VP = HD + 4;
-    __shared__ __align__(16) float vs[PF_KT * VP];
+    constexpr int TP = PF_KT + 4;                                // vt row pitch
+    __shared__ __align__(16) float vt[HD * TP];
     __shared__ __align__(16) float ps[R * PF_KT];
     const int tid = threadIdx.x;
     const int G = a.n_heads / a.n_kv, g = blockIdx.y;
@@ -187,17 +192,24 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
     const int d = tid % HD, set = tid / HD;
     const bool act = set < NSET;
     float acc[RS];
-    int rpos[RS];
 #pragma unroll
-    for (int k = 0; k < RS; k++) {
-        acc[k] = 0.0f;
-        const int r = set * RS + k;                       // row = (token r / GM, head r % GM)
-        const int b = b0 + r / GM, h = r % GM;
-        rpos[k] = (act && r < R && b < a.n_tok && h < G) ? a.pos_base + b : -1;
-    }
+    for (int k = 0; k < RS; k++) acc[k] = 0.0f;
+    const size_t hoff = (size_t)g * HD;
     for (int t0 = 0; t0 <= tmax; t0 += PF_KT) {
         __syncthreads();
-        stage_rows<HD, F16>(vs, VP, a.vc, a.kv_dim, (size_t)g * HD, t0, tmax, tid);
+        for (int f = tid; f < PF_KT * (HD / 4); f += WG) {     // V rows -> vt[d][t]
+            const int t = f / (HD / 4), c = (f % (HD / 4)) * 4;
+            const size_t off = (size_t)min(t0 + t, tmax) * a.kv_dim + hoff + c;
+            float4 v;
+            if (F16) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
+                v = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
+            } else {
+                v = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.vc) + off);
+            }
+            vt[(c + 0) * TP + t] = v.x; vt[(c + 1) * TP + t] = v.y;
+            vt[(c + 2) * TP + t] = v.z; vt[(c + 3) * TP + t] = v.w;
+        }
         for (int f = tid; f < R * (PF_KT / 4); f += WG) {   // p = e * (1/sum), model.c:62-63
             const int r = f / (PF_KT / 4), c = (f % (PF_KT / 4)) * 4;
             const int b = b0 + r / GM, h = r % GM;
@@ -208,26 +220,29 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
                 if (t0 + c < len) {
                     const float inv = a.rowinv[row];
                     const float4 e = *reinterpret_cast<const float4 *>(a.scores + row * a.ldk + t0 + c);
-                    p = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
+                    const int t = t0 + c;
+                    p.x = e.x * inv;
+                    p.y = t + 1 < len ? e.y * inv : 0.0f;
+                    p.z = t + 2 < len ? e.z * inv : 0.0f;
+                    p.w = t + 3 < len ? e.w * inv : 0.0f;
                 }
             }
             *reinterpret_cast<float4 *>(&ps[r * PF_KT + c]) = p;
         }
         __syncthreads();
         if (!act) continue;
+        const float *vrow = &vt[d * TP];
         for (int t = 0; t < PF_KT; t += 4) {
-            const float v0 = vs[t * VP + d], v1 = vs[(t + 1) * VP + d];
-            const float v2 = vs[(t + 2) * VP + d], v3 = vs[(t + 3) * VP + d];
+            const float4 v = *reinterpret_cast<const float4 *>(vrow + t);
 #pragma unroll
             for (int k = 0; k < RS; k++) {
                 const int r = min(set * RS + k, R - 1);
                 const float4 p = *reinterpret_cast<const float4 *>(&ps[r * PF_KT + t]);
-                const int lim = rpos[k] - (t0 + t);   // positions t0+t .. t0+t+lim are visible
-                float o = acc[k];
-                if (lim >= 0) o = o + p.x * v0;
-                if (lim >= 1) o = o + p.y * v1;
-                if (lim >= 2) o = o + p.z * v2;
-                if (lim >= 3) o = o + p.w * v3;
+                float o = acc[k];          // positions in order, multiply and add rounded apart
+                o = o + p.x * v.x;
+                o = o + p.y * v.y;
+                o = o + p.z * v.z;
+                o = o + p.w * v.w;
                 acc[k] = o;
             }
         }
@@ -235,9 +250,9 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
     if (!act) return;
 #pragma unroll
     for (int k = 0; k < RS; k++) {
-        if (rpos[k] < 0) continue;
         const int r = set * RS + k;
         const int b = b0 + r / GM, h = r % GM;
+        if (r >= R || b >= a.n_tok || h >= G) continue;
         a.out[(size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + d] = acc[k];
     }
 }

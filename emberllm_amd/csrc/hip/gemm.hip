@@ -6,10 +6,14 @@
 //
 // k_quant_rows: one workgroup per token row builds the Q8_0 activation codes
 // (optionally after the embedding lookup, an RMSNorm or the SwiGLU gate).
-// k_gemm: a 64 (units) x 64 (tokens) output tile per workgroup, walking K one
-// 32-weight quant block at a time.  Each thread owns a 4 x 4 micro-tile and
-// accumulates the block products in block order, (acc * dw) * dx, the same
-// order as vecdot_q8 / vecdot_q4 (kernels.c:151-183).
+// k_gemm_mfma (Q8_0 / Q4_0 weights): int8 matrix cores, one
+// v_mfma_i32_32x32x32_i8 per 32-weight quant block, so each block's integer
+// dot product is exact and separately available; the fp32 epilogue of every
+// block applies the reference's order sum += ((float)isum * dw) * dx
+// (vecdot_q8 / vecdot_q4, kernels.c:151-183).  Roofline: the epilogue's four
+// VALU operations per output element and block bound it, not the MFMA rate.
+// k_gemm (F32 weights): a 64 x 64 tile per workgroup, 4 x 4 micro-tiles per
+// thread, dot_f32 order.
 #include "kernels.h"
 
 namespace ehip {
@@ -193,8 +197,157 @@ __global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
     }
 }
 
+// --------------------------------------------------------------------------
+// int8 MFMA GEMM.  Workgroup tile GM_U (units) x GM_T (tokens), four waves in
+// a 2 x 2 arrangement, each owning 2 x 2 MFMA tiles of 32 x 32.  K advances
+// GM_KB quant blocks per stage; stages are double-buffered in LDS (the next
+// stage's global loads are issued before the current stage's products).
+// Output (i, j) of an MFMA tile sits in lane j + 32*((i/4)%2), accumulator
+// (i%4) + 4*(i/8); A fragments hold W[u][16h .. 16h+15] of one block, B
+// fragments X[t][16h .. 16h+15], h = lane / 32.
+constexpr int GM_U = 128, GM_T = 128, GM_KB = 2;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
+
+template <int DT, int EPI>
+__global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
+    constexpr int WB = DT == DT_Q8 ? 32 : 16;          // weight bytes per row and block
+    constexpr int WROW = GM_KB * WB, XROW = GM_KB * 32; // stage bytes per row
+    __shared__ __align__(16) uint8_t ws[2][GM_U * WROW];
+    __shared__ __align__(16) int8_t xsm[2][GM_T * XROW];
+    __shared__ float dws[2][GM_KB][GM_U], dxs[2][GM_KB][GM_T];
+    __shared__ int sxs[2][GM_KB][GM_T];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const int u0 = blockIdx.x * GM_U, t0 = blockIdx.y * GM_T;
+    const int K = a.W.cols, nb = K / QB, nst = (nb + GM_KB - 1) / GM_KB;
+    const int wu = (wave & 1) * 64, wt = (wave >> 1) * 64;   // this wave's 64 x 64 corner
+
+    // global -> registers for one stage: weights (WROW bytes per row), codes, scales
+    constexpr int WLD = GM_U * WROW / 16 / WG, XLD = GM_T * XROW / 16 / WG;
+    int4 wr[WLD], xr[XLD];
+    float dwr, dxr; int xsr;
+    auto load = [&](int st) {
+        const int b0 = st * GM_KB;
+#pragma unroll
+        for (int i = 0; i < WLD; i++) {
+            const int f = tid + i * WG, row = f / (WROW / 16), c = (f % (WROW / 16)) * 16;
+            const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
+            wr[i] = *reinterpret_cast<const int4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
+        }
+#pragma unroll
+        for (int i = 0; i < XLD; i++) {
+            const int f = tid + i * WG, row = f / (XROW / 16), c = (f % (XROW / 16)) * 16;
+            const int t = min(t0 + row, a.n - 1), blk = min(b0 + c / 32, nb - 1);
+            xr[i] = *reinterpret_cast<const int4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
+        }
+        {   // GM_KB * (GM_U + GM_T) = 512 scales: two per thread
+            const int kb = tid / GM_U, r = tid % GM_U;
+            const int blk = min(b0 + kb, nb - 1);
+            dwr = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk]);
+            const int t = min(t0 + r, a.n - 1);
+            dxr = a.dx[(size_t)t * nb + blk];
+            xsr = DT == DT_Q4 ? a.xs[(size_t)t * nb + blk] : 0;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < WLD; i++) reinterpret_cast<int4 *>(ws[buf])[tid + i * WG] = wr[i];
+#pragma unroll
+        for (int i = 0; i < XLD; i++) reinterpret_cast<int4 *>(xsm[buf])[tid + i * WG] = xr[i];
+        const int kb = tid / GM_U, r = tid % GM_U;
+        dws[buf][kb][r] = dwr;
+        dxs[buf][kb][r] = dxr;
+        sxs[buf][kb][r] = xsr;
+    };
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int x = 0; x < 2; x++)
+#pragma unroll
+        for (int y = 0; y < 2; y++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[x][y][r] = 0.0f;
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int st = 0; st < nst; st++) {
+        const int buf = st & 1;
+        if (st + 1 < nst) load(st + 1);
+#pragma unroll
+        for (int kb = 0; kb < GM_KB; kb++) {
+            if (st * GM_KB + kb >= nb) break;
+            i32x4 af[2], bf[2];
+#pragma unroll
+            for (int x = 0; x < 2; x++) {      // weight rows wu + 32x + j, k-half h
+                const uint8_t *src = ws[buf] + (size_t)(wu + 32 * x + j) * WROW + kb * WB;
+                if (DT == DT_Q8) {
+                    af[x] = *reinterpret_cast<const i32x4 *>(src + 16 * h);
+                } else {                       // nibbles: low = weights 0..15, high = 16..31
+                    const i32x4 raw = *reinterpret_cast<const i32x4 *>(src);
+                    const int sh = 4 * h, m = 0x0f0f0f0f;
+                    af[x] = i32x4{(raw[0] >> sh) & m, (raw[1] >> sh) & m, (raw[2] >> sh) & m, (raw[3] >> sh) & m};
+                }
+            }
+#pragma unroll
+            for (int y = 0; y < 2; y++)
+                bf[y] = *reinterpret_cast<const i32x4 *>(xsm[buf] + (size_t)(wt + 32 * y + j) * XROW + kb * 32 + 16 * h);
+#pragma unroll
+            for (int x = 0; x < 2; x++)
+#pragma unroll
+                for (int y = 0; y < 2; y++) {
+                    i32x16 d = {};
+                    d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[x], bf[y], d, 0, 0, 0);
+                    const float dx = dxs[buf][kb][wt + 32 * y + j];
+                    const int xsum = DT == DT_Q4 ? sxs[buf][kb][wt + 32 * y + j] : 0;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
+                        const float dw = dws[buf][kb][wu + 32 * x + mrow(r, h)];
+                        acc[x][y][r] += ((float)isum * dw) * dx;
+                    }
+                }
+        }
+        __syncthreads();
+        if (st + 1 < nst) {
+            store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < 2; x++)
+#pragma unroll
+        for (int y = 0; y < 2; y++) {
+            const int t = t0 + wt + 32 * y + j;
+            if (t >= a.n) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int u = u0 + wu + 32 * x + mrow(r, h);
+                if (u >= a.units) continue;
+                float *o = a.out + (size_t)t * a.out_stride + u;
+                if (EPI == EPI_STORE) *o = a.bias ? acc[x][y][r] + a.bias[u] : acc[x][y][r];
+                else *o += acc[x][y][r];
+            }
+        }
+}
+
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
+    if (a.W.dtype == DT_Q8 || a.W.dtype == DT_Q4) {
+        dim3 g((a.units + GM_U - 1) / GM_U, (a.n + GM_T - 1) / GM_T);
+#define GMF(DT)                                                                                  \
+    if (a.W.dtype == DT) {                                                                       \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE>), g, dim3(WG), 0, st, a); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID>), g, dim3(WG), 0, st, a); \
+        else return -1;                                                                          \
+        return 0;                                                                                \
+    }
+        GMF(DT_Q8) GMF(DT_Q4)
+#undef GMF
+    }
     dim3 grid((a.units + TM - 1) / TM, (a.n + TN - 1) / TN);
 #define G(DT)                                                                              \
     if (a.W.dtype == DT) {                                                                 \

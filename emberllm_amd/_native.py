@@ -127,6 +127,9 @@ PROTOTYPES = {
     "ehip_debug_buffer": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_uint64]),
     "ehip_time_decode": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _FP]),
     "ehip_generate_greedy": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _IP, _FP]),
+    "ehip_sample": (ctypes.c_int, [_P, _FP, ctypes.c_int, ctypes.POINTER(EmberSampler), _IP]),
+    "ehip_generate_sampled": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.POINTER(EmberSampler), _IP, _FP]),
     "ehip_time_kernel": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP]),
     # ember_synth.h
     "ember_synth_write": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(EmberSynthConfig)]),

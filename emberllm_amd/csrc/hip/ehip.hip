@@ -22,6 +22,7 @@
 #include <cstring>
 #include <vector>
 
+#include "../../../include/ember.h"
 #include "../../../include/ehip.h"
 #include "kernels.h"
 
@@ -246,6 +247,12 @@ struct EhipState {
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
     hipGraph_t graph_gen; hipGraphExec_t gexec_gen;
+    // device sampler: xorshift64* state, history ring, candidates; the
+    // sampling decode graph is captured for one parameter set
+    unsigned long long *smp_rng; int *smp_meta, *smp_hist; int smp_hist_cap;
+    float *smp_pmax, *smp_psum, *smp_cval; int *smp_cidx;
+    hipGraph_t graph_smp; hipGraphExec_t gexec_smp;
+    SampleParams smp_graph_p; int smp_graph_cap;
     hipEvent_t ev0, ev1;
     std::vector<void *> allocs;
 };
@@ -265,6 +272,9 @@ extern "C" void ehip_state_destroy(EhipState *s) {
     if (s->graph) (void)hipGraphDestroy(s->graph);
     if (s->gexec_gen) (void)hipGraphExecDestroy(s->gexec_gen);
     if (s->graph_gen) (void)hipGraphDestroy(s->graph_gen);
+    if (s->gexec_smp) (void)hipGraphExecDestroy(s->gexec_smp);
+    if (s->graph_smp) (void)hipGraphDestroy(s->graph_smp);
+    if (s->smp_hist) (void)hipFree(s->smp_hist);
     for (void *p : s->allocs) (void)hipFree(p);
     if (s->tokpos_h) (void)hipHostFree(s->tokpos_h);
     if (s->logits_h) (void)hipHostFree(s->logits_h);
@@ -323,7 +333,13 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->pf_rowinv = (float *)salloc(s, 4 * pfc * c.n_heads)) &&
               (s->am_val = (float *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->am_idx = (int *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
-              (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true));
+              (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true)) &&
+              (s->smp_rng = (unsigned long long *)salloc(s, 8)) &&
+              (s->smp_meta = (int *)salloc(s, 8, true)) &&
+              (s->smp_pmax = (float *)salloc(s, 4 * SAMPLE_GRID)) &&
+              (s->smp_psum = (float *)salloc(s, 4 * SAMPLE_GRID)) &&
+              (s->smp_cval = (float *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX)) &&
+              (s->smp_cidx = (int *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
     if (ok) {
         // RoPE table with the reference's arithmetic (model.c:69-71): the
@@ -518,6 +534,136 @@ extern "C" int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *
         HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
         *ms = t;
     }
+    if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
+// ---------------------------------------------------------- sampling ----
+static bool same_params(const SampleParams &a, const SampleParams &b) {
+    return a.temperature == b.temperature && a.top_p == b.top_p && a.min_p == b.min_p &&
+           a.repeat_penalty == b.repeat_penalty && a.presence_penalty == b.presence_penalty &&
+           a.frequency_penalty == b.frequency_penalty && a.top_k == b.top_k;
+}
+
+static SampleParams sampler_params(const EmberSampler *smp) {
+    SampleParams p{};
+    p.temperature = smp->temperature; p.top_p = smp->top_p; p.min_p = smp->min_p;
+    p.repeat_penalty = smp->repeat_penalty; p.presence_penalty = smp->presence_penalty;
+    p.frequency_penalty = smp->frequency_penalty; p.top_k = smp->top_k;
+    return p;
+}
+
+// Bring the sampler's RNG and history ring to the device (ring storage is
+// grown outside any capture).
+static int sampler_upload(EhipState *s, const EmberSampler *smp) {
+    const int cap = smp->history ? smp->hist_cap : 0;
+    if (cap > s->smp_hist_cap) {
+        if (s->gexec_smp) { (void)hipGraphExecDestroy(s->gexec_smp); s->gexec_smp = nullptr; }
+        if (s->graph_smp) { (void)hipGraphDestroy(s->graph_smp); s->graph_smp = nullptr; }
+        if (s->smp_hist) (void)hipFree(s->smp_hist);
+        s->smp_hist = nullptr;
+        s->smp_hist_cap = 0;
+        HCHK(hipMalloc(&s->smp_hist, 4 * (size_t)cap), -1);
+        s->smp_hist_cap = cap;
+    }
+    const unsigned long long rng = smp->rng_state;
+    const int meta[2] = { smp->hist_len, smp->hist_pos };
+    HCHK(hipMemcpyAsync(s->smp_rng, &rng, 8, hipMemcpyHostToDevice, s->st), -1);
+    HCHK(hipMemcpyAsync(s->smp_meta, meta, 8, hipMemcpyHostToDevice, s->st), -1);
+    if (cap > 0) HCHK(hipMemcpyAsync(s->smp_hist, smp->history, 4 * (size_t)cap, hipMemcpyHostToDevice, s->st), -1);
+    HCHK(hipStreamSynchronize(s->st), -1);
+    return 0;
+}
+
+static int sampler_download(EhipState *s, EmberSampler *smp) {
+    const int cap = smp->history ? smp->hist_cap : 0;
+    unsigned long long rng = 0;
+    int meta[2] = { 0, 0 };
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipMemcpy(&rng, s->smp_rng, 8, hipMemcpyDeviceToHost), -1);
+    HCHK(hipMemcpy(meta, s->smp_meta, 8, hipMemcpyDeviceToHost), -1);
+    if (cap > 0) HCHK(hipMemcpy(smp->history, s->smp_hist, 4 * (size_t)cap, hipMemcpyDeviceToHost), -1);
+    smp->rng_state = rng;
+    smp->hist_len = meta[0];
+    smp->hist_pos = meta[1];
+    return 0;
+}
+
+static SampleArgs sample_args(EhipState *s, const SampleParams &p, int cap, int n) {
+    SampleArgs a{};
+    a.logits = s->logits_d; a.n = n; a.p = p;
+    a.rng = s->smp_rng; a.hist = cap > 0 ? s->smp_hist : nullptr; a.hist_meta = s->smp_meta; a.hist_cap = cap;
+    a.pmax = s->smp_pmax; a.psum = s->smp_psum; a.cval = s->smp_cval; a.cidx = s->smp_cidx;
+    a.am_val = s->am_val; a.am_idx = s->am_idx;
+    a.tokpos = s->tokpos_d; a.out = s->gen_tok; a.cap = s->ctx;
+    return a;
+}
+
+static bool sampler_supported(const EmberSampler *smp) {
+    return smp->temperature <= 0.0f || (smp->top_k >= 1 && smp->top_k <= SAMPLE_TOPK_MAX);
+}
+
+extern "C" int ehip_sample(EhipState *s, const float *logits, int n, EmberSampler *smp, int *token) {
+    if (!sampler_supported(smp)) { set_err("device sampler: top_k %d outside [1,%d]", smp->top_k, SAMPLE_TOPK_MAX); return -1; }
+    if (n <= 0 || n > s->m->cfg.vocab_size) { set_err("device sampler: %d logits for a vocabulary of %d", n, s->m->cfg.vocab_size); return -1; }
+    if (logits) HCHK(hipMemcpyAsync(s->logits_d, logits, 4 * (size_t)n, hipMemcpyHostToDevice, s->st), -1);
+    if (sampler_upload(s, smp)) return -1;
+    s->tokpos_h[2] = 0;
+    HCHK(hipMemcpyAsync(s->tokpos_d + 2, s->tokpos_h + 2, 4, hipMemcpyHostToDevice, s->st), -1);
+    const int cap = smp->history ? smp->hist_cap : 0;
+    if (launch_sample(s->st, sample_args(s, sampler_params(smp), cap, n))) { set_err("sampler launch failed"); return -1; }
+    if (sampler_download(s, smp)) return -1;
+    HCHK(hipMemcpy(token, s->gen_tok, 4, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
+extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, EmberSampler *smp, int *out_tokens,
+                                     float *ms) {
+    const int V = s->m->cfg.vocab_size;
+    if (n <= 0 || pos < 0 || (long)pos + n > s->ctx) { set_err("generate: positions %d..%d exceed the context of %d", pos, pos + n - 1, s->ctx); return -1; }
+    if (tok < 0 || tok >= V) { set_err("generate: token id %d out of range [0,%d)", tok, V); return -1; }
+    if (!sampler_supported(smp)) { set_err("device sampler: top_k %d outside [1,%d]", smp->top_k, SAMPLE_TOPK_MAX); return -1; }
+    if (sampler_upload(s, smp)) return -1;
+    const SampleParams p = sampler_params(smp);
+    const int cap = smp->history ? smp->hist_cap : 0;
+    s->tokpos_h[0] = tok;
+    s->tokpos_h[1] = pos;
+    s->tokpos_h[2] = 0;
+    s->tokpos_h[3] = 0;
+    HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
+    HCHK(hipStreamSynchronize(s->st), -1);
+    auto enq = [&]() -> int {
+        if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
+        if (launch_sample(s->st, sample_args(s, p, cap, V))) { set_err("sampler launch failed"); return -1; }
+        return 0;
+    };
+    if (s->graph_mode && (!s->gexec_smp || !same_params(p, s->smp_graph_p) || cap != s->smp_graph_cap)) {
+        if (s->gexec_smp) { (void)hipGraphExecDestroy(s->gexec_smp); s->gexec_smp = nullptr; }
+        if (s->graph_smp) { (void)hipGraphDestroy(s->graph_smp); s->graph_smp = nullptr; }
+        HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), -1);
+        const int rc = enq();
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(s->st, &g);
+        if (rc) { if (g) (void)hipGraphDestroy(g); return -1; }
+        if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return -1; }
+        s->graph_smp = g;
+        HCHK(hipGraphInstantiate(&s->gexec_smp, g, nullptr, nullptr, 0), -1);
+        s->smp_graph_p = p;
+        s->smp_graph_cap = cap;
+    }
+    HCHK(hipEventRecord(s->ev0, s->st), -1);
+    for (int i = 0; i < n; i++) {
+        if (s->graph_mode) HCHK(hipGraphLaunch(s->gexec_smp, s->st), -1);
+        else if (enq()) return -1;
+    }
+    HCHK(hipEventRecord(s->ev1, s->st), -1);
+    HCHK(hipEventSynchronize(s->ev1), -1);
+    if (ms) {
+        float t = 0.0f;
+        HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
+        *ms = t;
+    }
+    if (sampler_download(s, smp)) return -1;
     if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
     return 0;
 }

@@ -130,4 +130,28 @@ int launch_argmax(hipStream_t st, const ArgmaxArgs &a);
 int launch_argmax_merge(hipStream_t st, const float *pval, const int *pidx, int nparts, int n,
                         int *tokpos, int *out, int cap);
 
+// ---------------------------------------------------------- full sampler --
+// ember_sample (src/sample.c:76-175) on the device: penalties over a device
+// history ring, then either the first maximum (temperature <= 0) or
+// temperature -> softmax -> top-k -> min-p -> top-p -> one xorshift64* draw,
+// for top_k in [1, SAMPLE_TOPK_MAX].  The chosen token is accepted into the
+// ring and fed to the decode loop as the argmax path does (tokpos/out).
+struct SampleParams {
+    float temperature, top_p, min_p, repeat_penalty, presence_penalty, frequency_penalty;
+    int top_k;
+};
+constexpr int SAMPLE_TOPK_MAX = 64, SAMPLE_GRID = 64, SAMPLE_SLICE_MAX = 4096;
+struct SampleArgs {
+    float *logits; int n;            // device logits, overwritten as the reference does
+    SampleParams p;
+    unsigned long long *rng;         // device xorshift64* state
+    int *hist, *hist_meta;           // ring [hist_cap]; {hist_len, hist_pos}
+    int hist_cap;
+    float *pmax, *psum;              // [SAMPLE_GRID]
+    float *cval; int *cidx;          // [SAMPLE_GRID][SAMPLE_TOPK_MAX] candidates
+    float *am_val; int *am_idx;      // argmax partials (greedy)
+    int *tokpos; int *out; int cap;  // as ArgmaxArgs
+};
+int launch_sample(hipStream_t st, const SampleArgs &a);
+
 }  // namespace ehip

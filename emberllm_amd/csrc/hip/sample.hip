@@ -109,4 +109,216 @@ int launch_argmax(hipStream_t st, const ArgmaxArgs &a) {
     return launch_argmax_merge(st, a.pval, a.pidx, nb, a.n, a.tokpos, a.out, a.cap);
 }
 
+// --------------------------------------------------------------------------
+// Full sampler.  The per-token ordering work is exact: penalties in history
+// order, division by the temperature, expf, division by the sum, candidates
+// ordered by (probability descending, index ascending) — what the reference's
+// stable qsort yields — and the cumulative sums of top-p and of the draw in
+// that order.  Only the softmax sum is taken in a fixed tree order instead
+// of index order, so a probability can differ from the reference's in its
+// last bit; a draw could then differ only when it lands within that of a
+// cumulative boundary.
+
+// penalties (sample.c:76-96): one lane, history in array order
+__global__ void k_samp_pen(SampleArgs a) {
+    if (threadIdx.x != 0 || !a.hist || a.hist_cap <= 0) return;
+    const int len = a.hist_meta[0];
+    const bool rep = a.p.repeat_penalty != 1.0f, freq = a.p.frequency_penalty != 0.0f,
+               pres = a.p.presence_penalty != 0.0f;
+    if (len == 0 || (!rep && !freq && !pres)) return;
+    for (int i = 0; i < len; i++) {
+        const int t = a.hist[i];
+        if (t < 0 || t >= a.n) continue;
+        bool first = true;
+        for (int j = 0; j < i; j++) if (a.hist[j] == t) { first = false; break; }
+        float l = a.logits[t];
+        if (first) {
+            if (rep) l = l > 0.0f ? l / a.p.repeat_penalty : l * a.p.repeat_penalty;
+            if (pres) l -= a.p.presence_penalty;
+        }
+        if (freq) l -= a.p.frequency_penalty;
+        a.logits[t] = l;
+    }
+}
+
+__device__ __forceinline__ void samp_slice(int n, int &lo, int &hi) {
+    const int per = (n + SAMPLE_GRID - 1) / SAMPLE_GRID;
+    lo = min(n, (int)blockIdx.x * per);
+    hi = min(n, lo + per);
+}
+
+// logits /= T, slice maximum
+__global__ __launch_bounds__(WG) void k_samp_a(SampleArgs a) {
+    __shared__ float red[NWAVE];
+    int lo, hi;
+    samp_slice(a.n, lo, hi);
+    float mx = -INFINITY;
+    for (int i = lo + threadIdx.x; i < hi; i += WG) {
+        const float l = a.logits[i] / a.p.temperature;
+        a.logits[i] = l;
+        mx = fmaxf(mx, l);
+    }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = red[0];
+        for (int w = 1; w < NWAVE; w++) m = fmaxf(m, red[w]);
+        a.pmax[blockIdx.x] = m;
+    }
+}
+
+// e = expf(l - max) in place, slice sum
+__global__ __launch_bounds__(WG) void k_samp_b(SampleArgs a) {
+    __shared__ float red[NWAVE];
+    float M = -INFINITY;
+    for (int w = 0; w < SAMPLE_GRID; w++) M = fmaxf(M, a.pmax[w]);
+    int lo, hi;
+    samp_slice(a.n, lo, hi);
+    float s = 0.0f;
+    for (int i = lo + threadIdx.x; i < hi; i += WG) {
+        const float e = expf(a.logits[i] - M);
+        a.logits[i] = e;
+        s += e;
+    }
+    const float t = block_sum(s, red);
+    if (threadIdx.x == 0) a.psum[blockIdx.x] = t;
+}
+
+// (p desc, index asc): the order of the reference's stable sort
+__device__ __forceinline__ bool samp_before(float pa, int ia, float pb, int ib) {
+    return pa > pb || (pa == pb && ia < ib);
+}
+
+// bitonic sort of N (p, idx) pairs in LDS into samp_before order
+template <int N>
+__device__ __forceinline__ void samp_sort(float *sp, int *si) {
+    for (int k = 2; k <= N; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < N; i += blockDim.x) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const bool up = (i & k) == 0;   // this block ascends in samp_before order
+                    const bool sw = up ? samp_before(sp[l], si[l], sp[i], si[i])
+                                       : samp_before(sp[i], si[i], sp[l], si[l]);
+                    if (sw) {
+                        const float tp = sp[i]; sp[i] = sp[l]; sp[l] = tp;
+                        const int ti = si[i]; si[i] = si[l]; si[l] = ti;
+                    }
+                }
+            }
+        }
+    __syncthreads();
+}
+
+// p = e / sum; the slice's first SAMPLE_TOPK_MAX candidates
+__global__ __launch_bounds__(WG) void k_samp_c(SampleArgs a) {
+    __shared__ float sp[SAMPLE_SLICE_MAX];
+    __shared__ int si[SAMPLE_SLICE_MAX];
+    __shared__ float S;
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+        for (int w = 0; w < SAMPLE_GRID; w++) t += a.psum[w];
+        S = t;
+    }
+    __syncthreads();
+    int lo, hi;
+    samp_slice(a.n, lo, hi);
+    for (int i = threadIdx.x; i < SAMPLE_SLICE_MAX; i += WG) {
+        const bool in = lo + i < hi;
+        sp[i] = in ? a.logits[lo + i] / S : -1.0f;
+        si[i] = in ? lo + i : INT_MAX;
+    }
+    samp_sort<SAMPLE_SLICE_MAX>(sp, si);
+    for (int i = threadIdx.x; i < SAMPLE_TOPK_MAX; i += WG) {
+        a.cval[blockIdx.x * SAMPLE_TOPK_MAX + i] = sp[i];
+        a.cidx[blockIdx.x * SAMPLE_TOPK_MAX + i] = si[i];
+    }
+}
+
+__device__ __forceinline__ void samp_emit(const SampleArgs &a, int tok) {
+    if (a.hist && a.hist_cap > 0) {   // ember_sampler_accept
+        const int pos = a.hist_meta[1];
+        a.hist[pos] = tok;
+        a.hist_meta[1] = (pos + 1) % a.hist_cap;
+        if (a.hist_meta[0] < a.hist_cap) a.hist_meta[0] += 1;
+    }
+    a.tokpos[0] = tok;
+    a.tokpos[1] += 1;
+    const int k = a.tokpos[2];
+    if (k < a.cap) a.out[k] = tok;
+    a.tokpos[2] = k + 1;
+}
+
+// merge the candidates, then top-k / min-p / top-p and the draw (sample.c:136-175)
+__global__ __launch_bounds__(WG) void k_samp_d(SampleArgs a) {
+    constexpr int NC = SAMPLE_GRID * SAMPLE_TOPK_MAX;
+    __shared__ float sp[NC];
+    __shared__ int si[NC];
+    for (int i = threadIdx.x; i < NC; i += WG) { sp[i] = a.cval[i]; si[i] = a.cidx[i]; }
+    samp_sort<NC>(sp, si);
+    if (threadIdx.x != 0) return;
+    int m = min(a.n, a.p.top_k);
+    if (a.p.min_p > 0.0f && a.p.min_p < 1.0f) {
+        const float thresh = a.p.min_p * sp[0];
+        int keep = 1;
+        while (keep < m && sp[keep] >= thresh) keep++;
+        m = keep;
+    }
+    float cutoff;
+    if (a.p.top_p > 0.0f && a.p.top_p < 1.0f) {
+        float cum = 0.0f;
+        int last = m - 1;
+        for (int i = 0; i < m; i++) { cum += sp[i]; if (cum >= a.p.top_p) { last = i; break; } }
+        m = last + 1;
+        cutoff = cum;
+    } else {
+        cutoff = 0.0f;
+        for (int i = 0; i < m; i++) cutoff += sp[i];
+    }
+    unsigned long long x = a.rng[0];   // xorshift64* (sample.c:98-105)
+    x ^= x >> 12; x ^= x << 25; x ^= x >> 27;
+    a.rng[0] = x;
+    const unsigned int u = (unsigned int)((x * 0x2545F4914F6CDD1DULL) >> 32);
+    const float r = (float)(u >> 8) / 16777216.0f * cutoff;
+    float cum = 0.0f;
+    int chosen = si[m - 1];
+    for (int i = 0; i < m; i++) { cum += sp[i]; if (r < cum) { chosen = si[i]; break; } }
+    samp_emit(a, chosen);
+}
+
+// greedy with penalties: first maximum over the penalized logits
+__global__ void k_samp_greedy_emit(SampleArgs a) {
+    if (threadIdx.x == 0) {
+        const int tok = a.tokpos[0];   // written by the argmax merge
+        // the argmax merge already advanced tokpos and out; only the ring is left
+        if (a.hist && a.hist_cap > 0) {
+            const int pos = a.hist_meta[1];
+            a.hist[pos] = tok;
+            a.hist_meta[1] = (pos + 1) % a.hist_cap;
+            if (a.hist_meta[0] < a.hist_cap) a.hist_meta[0] += 1;
+        }
+    }
+}
+
+int launch_sample(hipStream_t st, const SampleArgs &a) {
+    if (a.n <= 0 || (a.n + SAMPLE_GRID - 1) / SAMPLE_GRID > SAMPLE_SLICE_MAX) return -1;
+    hipLaunchKernelGGL(k_samp_pen, dim3(1), dim3(64), 0, st, a);
+    if (a.p.temperature <= 0.0f) {
+        ArgmaxArgs g{};
+        g.logits = a.logits; g.n = a.n; g.pval = a.am_val; g.pidx = a.am_idx;
+        g.tokpos = a.tokpos; g.out = a.out; g.cap = a.cap;
+        if (launch_argmax(st, g)) return -1;
+        hipLaunchKernelGGL(k_samp_greedy_emit, dim3(1), dim3(64), 0, st, a);
+        return 0;
+    }
+    if (a.p.top_k < 1 || a.p.top_k > SAMPLE_TOPK_MAX) return -1;
+    hipLaunchKernelGGL(k_samp_a, dim3(SAMPLE_GRID), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(k_samp_b, dim3(SAMPLE_GRID), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(k_samp_c, dim3(SAMPLE_GRID), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(k_samp_d, dim3(1), dim3(WG), 0, st, a);
+    return 0;
+}
+
 }  // namespace ehip

@@ -83,6 +83,26 @@ class Engine:
             raise RuntimeError(_native.last_error())
         return out, ms.value
 
+    def sample(self, logits, sampler):
+        """ember_sample on the device (ehip_sample); `sampler` is an
+        _native.EmberSampler, updated in place."""
+        x = np.ascontiguousarray(logits, dtype=np.float32)
+        tok = ctypes.c_int()
+        if self.lib.ehip_sample(self.dev, x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(x),
+                                ctypes.byref(sampler), ctypes.byref(tok)) != 0:
+            raise RuntimeError(_native.last_error())
+        return tok.value
+
+    def generate_sampled(self, tok, pos, n, sampler):
+        """Decode + device sampler loop held on the device; returns (tokens, ms)."""
+        out = np.zeros(n, dtype=np.int32)
+        ms = ctypes.c_float()
+        if self.lib.ehip_generate_sampled(self.dev, int(tok), int(pos), int(n), ctypes.byref(sampler),
+                                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                                          ctypes.byref(ms)) != 0:
+            raise RuntimeError(_native.last_error())
+        return out, ms.value
+
     def time_kernel(self, kernel, pos, reps):
         ms = ctypes.c_float()
         if self.lib.ehip_time_kernel(self.dev, int(kernel), int(pos), int(reps), ctypes.byref(ms)) != 0:

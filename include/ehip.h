@@ -19,6 +19,8 @@
 
 #include <stdint.h>
 
+#include "ember.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -80,6 +82,27 @@ float *ehip_prefill(EhipState *s, const int *ids, int n, int start);
  * stop-token handling: exactly n tokens are generated.  Returns 0, or
  * nonzero with ehip_last_error() set. */
 int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *out_tokens, float *ms);
+
+/* ember_sample(smp, logits, n) (src/sample.c:120-175) on the device:
+ * penalties over the sampler's history ring, then the first maximum
+ * (temperature <= 0) or temperature -> softmax -> top-k -> min-p -> top-p
+ * -> one draw from the sampler's xorshift64* stream; the token is accepted
+ * into the ring.  `logits` (host, n <= vocab floats) is copied to the device
+ * and left unmodified; NULL samples (and overwrites) the logits the last
+ * decode step left on the device.  The sampler's rng_state, history,
+ * hist_len and hist_pos are updated as ember_sample would.  Supports
+ * temperature <= 0 or top_k in [1, 64]; otherwise returns nonzero (use
+ * ember_sample on the host).  Returns 0 and *token, or nonzero. */
+int ehip_sample(EhipState *s, const float *logits, int n, EmberSampler *smp, int *token);
+
+/* The generate loop of src/main.c:197-206 held on the device with the full
+ * sampler: starting from token `tok` at position `pos`, n steps of decode
+ * followed by ehip_sample's selection, the chosen token feeding the next step
+ * with no host round trip (one hipGraph per step, captured for the sampler's
+ * parameters).  Tokens go to out_tokens (if non-NULL), the sampler state is
+ * updated as after n ember_sample calls, *ms (if non-NULL) receives the
+ * device time.  Same parameter support as ehip_sample. */
+int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, EmberSampler *smp, int *out_tokens, float *ms);
 
 /* ---- inspection and measurement (tests and bench) ----------------------- */
 /* Copy the KV cache of the given layers to/from host memory in the cache's

@@ -1,0 +1,122 @@
+"""GPU parity of the device sampler (ehip_sample, ehip_generate_sampled)
+against ember_sample: the reference's own chosen tokens and RNG states
+(tests/golden/sampler.npz, from the compiled reference), and the host
+sampler (itself pinned to the reference) on vocabulary-sized logits with
+ties.  Chosen tokens and RNG states are integers and must match exactly.
+"""
+import ctypes
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from emberllm_amd import _native, configs, emberllm
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+L = None
+
+
+def lib():
+    global L
+    if L is None:
+        L = _native.lib()
+    return L
+
+
+def say(msg):
+    print(f"[gpu-sampler] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def small_model(vocab):
+    cfg = dict(configs.TINY["t_llama"], vocab_size=vocab, n_layers=1)
+    return configs.model_path(f"samp_v{vocab}", cfg)
+
+
+def sampler(temp, top_p, top_k, seed, rp=1.0, last_n=0, pres=0.0, freq=0.0, min_p=0.0):
+    s = _native.EmberSampler()
+    lib().ember_sampler_init(ctypes.byref(s), temp, top_p, int(top_k), int(seed))
+    lib().ember_sampler_set_penalties(ctypes.byref(s), rp, int(last_n), pres, freq, min_p)
+    return s
+
+
+def supported(temp, top_k):
+    return temp <= 0.0 or 1 <= top_k <= 64
+
+
+def test_device_sampler_reference_golden():
+    g = np.load(os.path.join(GOLD, "sampler.npz"))
+    V = g["logits"].shape[1]
+    say(f"reference golden, vocab {V}")
+    eng = emberllm.Engine(small_model(V))
+    ran = 0
+    for k, (t, p, topk, seed, rp, ln, pr, fr, mp) in enumerate(g["settings"]):
+        if not supported(t, int(topk)):
+            continue
+        s = sampler(t, p, topk, seed, rp, ln, pr, fr, mp)
+        for i in range(g["logits"].shape[0]):
+            c = eng.sample(g["logits"][i], s)
+            assert c == g["chosen"][k, i] and s.rng_state == g["states"][k, i], (k, i, c, g["chosen"][k, i])
+        lib().ember_sampler_free(ctypes.byref(s))
+        ran += 1
+    assert ran >= 3
+    eng.close()
+
+
+@pytest.mark.parametrize("params", [
+    dict(temp=0.8, top_p=0.9, top_k=40),
+    dict(temp=1.0, top_p=1.0, top_k=1),
+    dict(temp=0.7, top_p=0.95, top_k=64, min_p=0.05),
+    dict(temp=1.3, top_p=0.8, top_k=20, rp=1.2, last_n=32, pres=0.3, freq=0.2),
+    dict(temp=0.0, top_p=0.9, top_k=0, rp=1.5, last_n=8),
+], ids=["t08p09k40", "k1", "minp", "penalties", "greedy-penalties"])
+def test_device_sampler_matches_host_on_vocab_logits(params):
+    V = 151936
+    say(f"vocab {V}: {params}")
+    eng = emberllm.Engine(small_model(V))
+    rng = np.random.default_rng(11)
+    p = dict(params)
+    a = sampler(p.pop("temp"), p.pop("top_p"), p.pop("top_k"), 77, **p)
+    b = sampler(params["temp"], params["top_p"], params["top_k"], 77,
+                **{k: v for k, v in params.items() if k not in ("temp", "top_p", "top_k")})
+    for step in range(24):
+        lg = rng.normal(0, 3, V).astype(np.float32)
+        lg[rng.integers(0, V, 64)] = lg[int(np.argmax(lg))]      # ties at the top
+        x = lg.copy()
+        host = lib().ember_sample(ctypes.byref(b), x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), V)
+        dev = eng.sample(lg, a)
+        assert dev == host and a.rng_state == b.rng_state, (step, dev, host)
+        assert a.hist_len == b.hist_len and a.hist_pos == b.hist_pos
+        assert [a.history[i] for i in range(a.hist_len)] == [b.history[i] for i in range(b.hist_len)]
+    eng.close()
+
+
+def test_generate_sampled_equals_host_loop():
+    """ehip_generate_sampled = the generate loop of forward + ember_sample."""
+    path = configs.model_path("t_qwen3")
+    say("device sampling loop vs host loop")
+    a, b = emberllm.Engine(path), emberllm.Engine(path)
+    ids = np.array([3, 77, 12, 500, 9], dtype=np.int32)
+    a.prefill(ids)
+    lg = b.prefill(ids)
+    sa = sampler(0.8, 0.9, 40, 4242, rp=1.1, last_n=16)
+    sb = sampler(0.8, 0.9, 40, 4242, rp=1.1, last_n=16)
+    for t in ids:
+        lib().ember_sampler_accept(ctypes.byref(sa), int(t))
+        lib().ember_sampler_accept(ctypes.byref(sb), int(t))
+    first = lib().ember_sample(ctypes.byref(sb), lg.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(lg))
+    lib().ember_sampler_accept(ctypes.byref(sa), first)   # both loops have now taken `first`
+    sa.rng_state = sb.rng_state
+    n = 24
+    dev, _ = a.generate_sampled(first, len(ids), n, sa)
+    host, tok = [], first
+    for i in range(n):
+        lg = b.forward(tok, len(ids) + i)
+        tok = lib().ember_sample(ctypes.byref(sb), lg.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(lg))
+        host.append(tok)
+    assert list(dev) == host, (list(dev), host)
+    assert sa.rng_state == sb.rng_state
+    a.close()
+    b.close()

@@ -17,6 +17,8 @@ reported, never as `value`:
                         logits over PCIe each step (the reference bench's
                         loop, src/main.c:258-263)
   decode_tok_s_depth128 the same device loop at depth 128
+  decode_tok_s_sampled  the device loop with the full sampler (temperature
+                        0.8, top-k 40, top-p 0.9, fixed seed) at the same depth
   prefill_tok_s_pp128 / _pp4096   ember_prefill at position 0 (mean of 5
                         after 1 warmup, src/main.c:251-266)
   roofline              the dominant kernel (split-K attention of one layer
@@ -84,7 +86,7 @@ def profiled_traffic(kernel, model, depth, kv):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (FETCH_SIZE and WRITE_SIZE runs, scaled against a copy kernel of
     known size), when one exists for this exact workload; else None."""
-    path = os.path.join(ROOT, "profiles", f"decode_qwen3_q8_depth{depth}_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"qwen3_q8_depth{depth}_traffic.md")
     if model != "qwen3_06b" or kv != "f32" or not os.path.exists(path):
         return None
     with open(path) as f:
@@ -136,7 +138,7 @@ def cpu_baseline(path, c, depth, budget_s):
         eng.forward((pos * 131 + 7) % V, pos)       # warmup (first touch of pages)
         pos += 1
         n, t0 = 0, time.perf_counter()
-        while n < 2 or (time.perf_counter() - t0 < per_point * 0.6 and n < 32):
+        while n < 2 or (time.perf_counter() - t0 < per_point * 0.6 and n < 96):
             eng.forward((pos * 131 + 7) % V, pos)
             pos += 1
             n += 1
@@ -171,7 +173,19 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill and kernel timings")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only copy 64 MiB device-to-device 8 times (a kernel of known traffic, for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "64 MiB device-to-device copy x 8"}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the token loop is "
               "single-stream on one MI355X; multi-GPU sharding is a design note only)", file=sys.stderr)
@@ -270,6 +284,15 @@ def main():
         _, ms128 = eng.generate_greedy(tok0, 128, K)
         out["decode_tok_s_depth128"] = K / (ms128 / 1e3)
         log(f"decode @128: {out['decode_tok_s_depth128']:.1f} tok/s")
+
+        # ---- sampled decode at depth (T 0.8, top-k 40, top-p 0.9) ---------
+        smp = _native.EmberSampler()
+        lib.ember_sampler_init(ctypes.byref(smp), 0.8, 0.9, 40, 1234)
+        eng.generate_sampled(tok0, depth, W, smp)
+        _, mss = eng.generate_sampled(tok0, depth, K, smp)
+        lib.ember_sampler_free(ctypes.byref(smp))
+        out["decode_tok_s_sampled"] = K / (mss / 1e3)
+        log(f"decode @{depth} sampled (T 0.8, top-k 40, top-p 0.9): {out['decode_tok_s_sampled']:.1f} tok/s")
     eng.close()
 
     cpu = None

@@ -119,27 +119,32 @@ int launch_argmax(hipStream_t st, const ArgmaxArgs &a) {
 // last bit; a draw could then differ only when it lands within that of a
 // cumulative boundary.
 
-// penalties (sample.c:76-96): one lane, history in array order
-__global__ void k_samp_pen(SampleArgs a) {
-    if (threadIdx.x != 0 || !a.hist || a.hist_cap <= 0) return;
+// penalties (sample.c:76-96).  Each token's updates depend only on its own
+// occurrences, so the lane holding a token's first occurrence in history
+// order applies all of them, in that order: the repetition and presence
+// penalties once, then the frequency penalty once per occurrence.
+__global__ __launch_bounds__(WG) void k_samp_pen(SampleArgs a) {
+    if (!a.hist || a.hist_cap <= 0) return;
     const int len = a.hist_meta[0];
     const bool rep = a.p.repeat_penalty != 1.0f, freq = a.p.frequency_penalty != 0.0f,
                pres = a.p.presence_penalty != 0.0f;
-    if (len == 0 || (!rep && !freq && !pres)) return;
-    for (int i = 0; i < len; i++) {
+    for (int i = threadIdx.x; i < len; i += WG) {
         const int t = a.hist[i];
         if (t < 0 || t >= a.n) continue;
         bool first = true;
         for (int j = 0; j < i; j++) if (a.hist[j] == t) { first = false; break; }
+        if (!first) continue;
+        int occ = 1;
+        for (int j = i + 1; j < len; j++) occ += a.hist[j] == t;
         float l = a.logits[t];
-        if (first) {
-            if (rep) l = l > 0.0f ? l / a.p.repeat_penalty : l * a.p.repeat_penalty;
-            if (pres) l -= a.p.presence_penalty;
-        }
-        if (freq) l -= a.p.frequency_penalty;
+        if (rep) l = l > 0.0f ? l / a.p.repeat_penalty : l * a.p.repeat_penalty;
+        if (pres) l -= a.p.presence_penalty;
+        if (freq) for (int k = 0; k < occ; k++) l -= a.p.frequency_penalty;
         a.logits[t] = l;
     }
 }
+
+constexpr int SAMP_E = SAMPLE_SLICE_MAX / WG;   // slice elements per thread
 
 __device__ __forceinline__ void samp_slice(int n, int &lo, int &hi) {
     const int per = (n + SAMPLE_GRID - 1) / SAMPLE_GRID;
@@ -147,16 +152,26 @@ __device__ __forceinline__ void samp_slice(int n, int &lo, int &hi) {
     hi = min(n, lo + per);
 }
 
-// logits /= T, slice maximum
+// logits /= T, slice maximum.  Every load is issued before the first use.
 __global__ __launch_bounds__(WG) void k_samp_a(SampleArgs a) {
     __shared__ float red[NWAVE];
     int lo, hi;
     samp_slice(a.n, lo, hi);
+    float l[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + (int)threadIdx.x + k * WG;
+        l[k] = i < hi ? a.logits[i] : 0.0f;
+    }
     float mx = -INFINITY;
-    for (int i = lo + threadIdx.x; i < hi; i += WG) {
-        const float l = a.logits[i] / a.p.temperature;
-        a.logits[i] = l;
-        mx = fmaxf(mx, l);
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + (int)threadIdx.x + k * WG;
+        if (i < hi) {
+            const float v = l[k] / a.p.temperature;
+            a.logits[i] = v;
+            mx = fmaxf(mx, v);
+        }
     }
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -171,15 +186,25 @@ __global__ __launch_bounds__(WG) void k_samp_a(SampleArgs a) {
 // e = expf(l - max) in place, slice sum
 __global__ __launch_bounds__(WG) void k_samp_b(SampleArgs a) {
     __shared__ float red[NWAVE];
-    float M = -INFINITY;
-    for (int w = 0; w < SAMPLE_GRID; w++) M = fmaxf(M, a.pmax[w]);
     int lo, hi;
     samp_slice(a.n, lo, hi);
+    float l[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + (int)threadIdx.x + k * WG;
+        l[k] = i < hi ? a.logits[i] : 0.0f;
+    }
+    float M = -INFINITY;
+    for (int w = 0; w < SAMPLE_GRID; w++) M = fmaxf(M, a.pmax[w]);
     float s = 0.0f;
-    for (int i = lo + threadIdx.x; i < hi; i += WG) {
-        const float e = expf(a.logits[i] - M);
-        a.logits[i] = e;
-        s += e;
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + (int)threadIdx.x + k * WG;
+        if (i < hi) {
+            const float e = expf(l[k] - M);
+            a.logits[i] = e;
+            s += e;
+        }
     }
     const float t = block_sum(s, red);
     if (threadIdx.x == 0) a.psum[blockIdx.x] = t;
@@ -190,51 +215,174 @@ __device__ __forceinline__ bool samp_before(float pa, int ia, float pb, int ib) 
     return pa > pb || (pa == pb && ia < ib);
 }
 
-// bitonic sort of N (p, idx) pairs in LDS into samp_before order
-template <int N>
-__device__ __forceinline__ void samp_sort(float *sp, int *si) {
-    for (int k = 2; k <= N; k <<= 1)
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            __syncthreads();
-            for (int i = threadIdx.x; i < N; i += blockDim.x) {
-                const int l = i ^ j;
-                if (l > i) {
-                    const bool up = (i & k) == 0;   // this block ascends in samp_before order
-                    const bool sw = up ? samp_before(sp[l], si[l], sp[i], si[i])
-                                       : samp_before(sp[i], si[i], sp[l], si[l]);
-                    if (sw) {
-                        const float tp = sp[i]; sp[i] = sp[l]; sp[l] = tp;
-                        const int ti = si[i]; si[i] = si[l]; si[l] = ti;
-                    }
-                }
-            }
-        }
-    __syncthreads();
+// Unsigned key with the order of the float (for the non-NaN values here).
+__device__ __forceinline__ unsigned samp_key(float p) {
+    const unsigned b = __float_as_uint(p);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// p = e / sum; the slice's first SAMPLE_TOPK_MAX candidates
+struct SelLds {
+    alignas(16) unsigned hist[512];
+    int cnt[SAMP_E * NWAVE];
+    int sel[3];
+};
+
+// Radix selection of the K-th largest key among the valid ones (1 <= K <=
+// their count), from the top in digits of 9 (sign and exponent), 8, 8 and 7
+// bits, stopping once the bin holding the K-th key is taken whole.  On
+// return the keys with (key & M) > P are taken (K - R of them) and R of the
+// C keys with (key & M) == P complete the K: all of them when C == R, else
+// (M == ~0, exactly equal keys) the first R in index order.
+__device__ __forceinline__ void radix_select(const unsigned (&key)[SAMP_E], const bool (&val)[SAMP_E], int K,
+                                             SelLds &s, unsigned &P, unsigned &M, int &R, int &C) {
+    P = 0; M = 0; R = K; C = 0;
+#pragma unroll 1
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = pass == 0 ? 23 : pass == 1 ? 15 : pass == 2 ? 7 : 0;
+        const int bits = pass == 0 ? 9 : pass == 3 ? 7 : 8;
+        const unsigned dmask = (1u << bits) - 1u;
+        s.hist[threadIdx.x] = 0;
+        s.hist[threadIdx.x + WG] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < SAMP_E; k++)
+            if (val[k] && (key[k] & M) == P) atomicAdd(&s.hist[(key[k] >> shift) & dmask], 1u);
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            // lane l holds bins 8l..8l+7; find the bin where the count from the top reaches R
+            const int l = threadIdx.x;
+            const uint4 h0 = reinterpret_cast<const uint4 *>(s.hist)[2 * l];
+            const uint4 h1 = reinterpret_cast<const uint4 *>(s.hist)[2 * l + 1];
+            const unsigned hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            unsigned own = 0;
+#pragma unroll
+            for (int b = 0; b < 8; b++) own += hb[b];
+            unsigned suf = own;   // count in lanes >= l
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned t = __shfl_down(suf, off);
+                if (l + off < 64) suf += t;
+            }
+            const unsigned r = (unsigned)R;
+            unsigned c = suf - own;   // count above this lane's bins
+            if (c < r && r <= suf) {
+                int sb = 0;
+                unsigned sc = 0, sh = 0;
+                bool found = false;
+#pragma unroll
+                for (int b = 7; b >= 0; b--) {
+                    if (!found && c + hb[b] >= r) { found = true; sb = b; sc = c; sh = hb[b]; }
+                    c += hb[b];
+                }
+                s.sel[0] = 8 * l + sb;
+                s.sel[1] = (int)sc;
+                s.sel[2] = (int)sh;
+            }
+        }
+        __syncthreads();
+        P |= (unsigned)s.sel[0] << shift;
+        M |= dmask << shift;
+        R -= s.sel[1];
+        C = s.sel[2];
+        if (C == R) break;   // the whole bin is taken: no further digits needed
+    }
+}
+
+// Rank of each flagged element among the flagged ones in index order, where
+// thread t holds elements t + k*WG (k = 0..SAMP_E-1); *total gets their count.
+__device__ __forceinline__ void block_rank(const bool (&f)[SAMP_E], int (&rank)[SAMP_E], int &total, SelLds &s) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    __syncthreads();   // s.cnt may still be read by a previous call
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const unsigned long long b = __ballot(f[k]);
+        rank[k] = __popcll(b & below);
+        if (lane == 0) s.cnt[k * NWAVE + w] = __popcll(b);
+    }
+    __syncthreads();
+    int base = 0;
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        int row = 0, pre = 0;
+#pragma unroll
+        for (int v = 0; v < NWAVE; v++) {
+            const int c = s.cnt[k * NWAVE + v];
+            pre += v < w ? c : 0;
+            row += c;
+        }
+        rank[k] += base + pre;
+        base += row;
+    }
+    total = base;
+}
+
+// Which of the held elements belong to the first K in samp_before order
+// (keys from samp_key, distinct indices increasing with position).
+__device__ __forceinline__ void samp_top(const unsigned (&key)[SAMP_E], const bool (&val)[SAMP_E], int K,
+                                         bool (&take)[SAMP_E], SelLds &s) {
+    unsigned P, M;
+    int R, C;
+    radix_select(key, val, K, s, P, M, R, C);
+    bool tie[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        take[k] = val[k] && (key[k] & M) > P;
+        tie[k] = val[k] && (key[k] & M) == P;
+    }
+    if (C == R) {
+#pragma unroll
+        for (int k = 0; k < SAMP_E; k++) take[k] = take[k] || tie[k];
+    } else {   // equal probabilities: the smaller indices come first
+        int rk[SAMP_E], nt;
+        block_rank(tie, rk, nt, s);
+#pragma unroll
+        for (int k = 0; k < SAMP_E; k++) take[k] = take[k] || (tie[k] && rk[k] < R);
+    }
+}
+
+// p = e / sum; the slice's first SAMPLE_TOPK_MAX candidates in samp_before
+// order, written in index order (which k_samp_d's tie ranking relies on).
 __global__ __launch_bounds__(WG) void k_samp_c(SampleArgs a) {
-    __shared__ float sp[SAMPLE_SLICE_MAX];
-    __shared__ int si[SAMPLE_SLICE_MAX];
+    __shared__ SelLds s;
     __shared__ float S;
+    int lo, hi;
+    samp_slice(a.n, lo, hi);
+    float e[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + (int)threadIdx.x + k * WG;
+        e[k] = i < hi ? a.logits[i] : 0.0f;
+    }
     if (threadIdx.x == 0) {
         float t = 0.0f;
         for (int w = 0; w < SAMPLE_GRID; w++) t += a.psum[w];
         S = t;
     }
     __syncthreads();
-    int lo, hi;
-    samp_slice(a.n, lo, hi);
-    for (int i = threadIdx.x; i < SAMPLE_SLICE_MAX; i += WG) {
-        const bool in = lo + i < hi;
-        sp[i] = in ? a.logits[lo + i] / S : -1.0f;
-        si[i] = in ? lo + i : INT_MAX;
+    float p[SAMP_E];
+    unsigned key[SAMP_E];
+    bool val[SAMP_E], take[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        val[k] = lo + (int)threadIdx.x + k * WG < hi;
+        p[k] = e[k] / S;
+        key[k] = samp_key(p[k]);
+        take[k] = false;
     }
-    samp_sort<SAMPLE_SLICE_MAX>(sp, si);
-    for (int i = threadIdx.x; i < SAMPLE_TOPK_MAX; i += WG) {
-        a.cval[blockIdx.x * SAMPLE_TOPK_MAX + i] = sp[i];
-        a.cidx[blockIdx.x * SAMPLE_TOPK_MAX + i] = si[i];
-    }
+    const int K = min(hi - lo, SAMPLE_TOPK_MAX);
+    if (K > 0) samp_top(key, val, K, take, s);
+    int pos[SAMP_E], nt;
+    block_rank(take, pos, nt, s);
+    float *cv = a.cval + blockIdx.x * SAMPLE_TOPK_MAX;
+    int *ci = a.cidx + blockIdx.x * SAMPLE_TOPK_MAX;
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++)
+        if (take[k] && pos[k] < SAMPLE_TOPK_MAX) {
+            cv[pos[k]] = p[k];
+            ci[pos[k]] = lo + (int)threadIdx.x + k * WG;
+        }
+    for (int j = nt + (int)threadIdx.x; j < SAMPLE_TOPK_MAX; j += WG) { cv[j] = -1.0f; ci[j] = INT_MAX; }
 }
 
 __device__ __forceinline__ void samp_emit(const SampleArgs &a, int tok) {
@@ -251,41 +399,84 @@ __device__ __forceinline__ void samp_emit(const SampleArgs &a, int tok) {
     a.tokpos[2] = k + 1;
 }
 
-// merge the candidates, then top-k / min-p / top-p and the draw (sample.c:136-175)
+__device__ __forceinline__ float lane_f(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+// The first min(n, top_k) of all candidates, then top-k / min-p / top-p and
+// the draw (sample.c:136-175).  Candidate position order is index order.
+// The final 64 are sorted by one wave (bitonic network over lanes); the
+// cumulative sums are taken sequentially in sorted order as the reference's
+// loops take them.
 __global__ __launch_bounds__(WG) void k_samp_d(SampleArgs a) {
     constexpr int NC = SAMPLE_GRID * SAMPLE_TOPK_MAX;
-    __shared__ float sp[NC];
-    __shared__ int si[NC];
-    for (int i = threadIdx.x; i < NC; i += WG) { sp[i] = a.cval[i]; si[i] = a.cidx[i]; }
-    samp_sort<NC>(sp, si);
-    if (threadIdx.x != 0) return;
-    int m = min(a.n, a.p.top_k);
+    static_assert(NC == SAMP_E * WG, "candidate count");
+    __shared__ SelLds s;
+    __shared__ float tp[SAMPLE_TOPK_MAX];
+    __shared__ int ti[SAMPLE_TOPK_MAX];
+    float p[SAMP_E];
+    int id[SAMP_E];
+    unsigned key[SAMP_E];
+    bool val[SAMP_E], take[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        p[k] = a.cval[threadIdx.x + k * WG];
+        id[k] = a.cidx[threadIdx.x + k * WG];
+    }
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        val[k] = id[k] >= 0 && id[k] < a.n;
+        key[k] = samp_key(p[k]);
+    }
+    const int K = min(a.n, a.p.top_k);   // 1..SAMPLE_TOPK_MAX, checked at launch
+    samp_top(key, val, K, take, s);
+    int pos[SAMP_E], nt;
+    block_rank(take, pos, nt, s);
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++)
+        if (take[k] && pos[k] < SAMPLE_TOPK_MAX) { tp[pos[k]] = p[k]; ti[pos[k]] = id[k]; }
+    for (int j = nt + (int)threadIdx.x; j < SAMPLE_TOPK_MAX; j += WG) { tp[j] = -1.0f; ti[j] = INT_MAX; }
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    float v = tp[lane];
+    int ix = ti[lane];
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const float pv = __shfl_xor(v, j);
+            const int pi = __shfl_xor(ix, j);
+            const bool want_first = ((lane & j) == 0) == ((lane & k) == 0);
+            if (want_first ? samp_before(pv, pi, v, ix) : samp_before(v, ix, pv, pi)) { v = pv; ix = pi; }
+        }
+    int m = min(nt, K);
     if (a.p.min_p > 0.0f && a.p.min_p < 1.0f) {
-        const float thresh = a.p.min_p * sp[0];
-        int keep = 1;
-        while (keep < m && sp[keep] >= thresh) keep++;
-        m = keep;
+        const float thresh = a.p.min_p * lane_f(v, 0);
+        const unsigned long long drop = __ballot(lane >= 1 && lane < m && !(v >= thresh));
+        if (drop) m = __builtin_ctzll(drop);
     }
-    float cutoff;
+    float cum = 0.0f, c = 0.0f;   // cum = sum of the sorted p[0..lane], in order
+#pragma unroll
+    for (int i = 0; i < 64; i++) {
+        c += lane_f(v, i);
+        if (lane == i) cum = c;
+    }
     if (a.p.top_p > 0.0f && a.p.top_p < 1.0f) {
-        float cum = 0.0f;
-        int last = m - 1;
-        for (int i = 0; i < m; i++) { cum += sp[i]; if (cum >= a.p.top_p) { last = i; break; } }
-        m = last + 1;
-        cutoff = cum;
-    } else {
-        cutoff = 0.0f;
-        for (int i = 0; i < m; i++) cutoff += sp[i];
+        const unsigned long long hit = __ballot(lane < m && cum >= a.p.top_p);
+        if (hit) m = __builtin_ctzll(hit) + 1;
     }
+    const float cutoff = __shfl(cum, m - 1);
     unsigned long long x = a.rng[0];   // xorshift64* (sample.c:98-105)
     x ^= x >> 12; x ^= x << 25; x ^= x >> 27;
-    a.rng[0] = x;
     const unsigned int u = (unsigned int)((x * 0x2545F4914F6CDD1DULL) >> 32);
     const float r = (float)(u >> 8) / 16777216.0f * cutoff;
-    float cum = 0.0f;
-    int chosen = si[m - 1];
-    for (int i = 0; i < m; i++) { cum += sp[i]; if (r < cum) { chosen = si[i]; break; } }
-    samp_emit(a, chosen);
+    const unsigned long long in = __ballot(lane < m && r < cum);
+    const int chosen = __shfl(ix, in ? __builtin_ctzll(in) : m - 1);
+    if (lane == 0) {
+        a.rng[0] = x;
+        samp_emit(a, chosen);
+    }
 }
 
 // greedy with penalties: first maximum over the penalized logits
@@ -304,7 +495,9 @@ __global__ void k_samp_greedy_emit(SampleArgs a) {
 
 int launch_sample(hipStream_t st, const SampleArgs &a) {
     if (a.n <= 0 || (a.n + SAMPLE_GRID - 1) / SAMPLE_GRID > SAMPLE_SLICE_MAX) return -1;
-    hipLaunchKernelGGL(k_samp_pen, dim3(1), dim3(64), 0, st, a);
+    const bool pen = a.hist && a.hist_cap > 0 &&
+        (a.p.repeat_penalty != 1.0f || a.p.frequency_penalty != 0.0f || a.p.presence_penalty != 0.0f);
+    if (pen) hipLaunchKernelGGL(k_samp_pen, dim3(1), dim3(WG), 0, st, a);
     if (a.p.temperature <= 0.0f) {
         ArgmaxArgs g{};
         g.logits = a.logits; g.n = a.n; g.pval = a.am_val; g.pidx = a.am_idx;

@@ -8,46 +8,42 @@
 // 2 * (pos+1) * kv_dim * esize (K and V rows read once) + 2 * kv_dim * esize
 // (the new row written) + the q|k|v input and the output (a few KB).
 //
-// Grid = (kv heads, chunks), kv heads varying fastest so that neighbouring
-// workgroups read whole cache rows.  A workgroup owns CR = IT * NL * RPB
-// consecutive positions of one kv head and serves all kv_mul query heads of
-// that group from the same K/V rows, so each cache row is read once per step.
-// Lane (rw, j) of a wave holds 16-byte piece j of row rw of each wave load:
+// Grid = (kv heads, max_chunks), kv heads varying fastest, so neighbouring
+// workgroups read whole cache rows.  Rows [0, pos] of each kv head are split
+// into equal chunks, one per workgroup of that head; with max_chunks =
+// 2 * #CUs / n_kv every CU streams the same share whatever the position (a CU
+// holding one more chunk than the others would set the kernel's length).  A
+// workgroup serves all kv_mul query heads of its kv head from the same K/V
+// rows, so each cache row is read once per step.  Lane (rw, j) of a wave holds
+// 16-byte piece j of row rw of each wave load:
 //   1. loads: the token's q heads / k / v pieces (straight out of the QKV
 //      matvec), the QK-norm weights and the RoPE (cos, sin) of its piece, then
 //      the first batch of NL K pieces and NL V pieces per thread;
 //   2. QK-norm and RoPE in registers: a head's sum of squares is a reduction
 //      over the LPR lanes of its row, a NEOX partner element sits P/2 lanes
-//      away, an interleaved partner in the same lane; the chunk holding
-//      `pos` stores the new k/v row;
-//   3. IT batches, each issuing the next batch's loads before its own scores
-//      (cross-lane sums over the row's lanes), with a running softmax
-//      (max, sum of exp, sum of exp * V) per wave;
+//      away, an interleaved partner in the same lane; the chunk holding `pos`
+//      stores the new k/v row;
+//   3. batches, each issuing the next batch's loads before its own scores
+//      (cross-lane sums over the row's lanes), with a running softmax (max,
+//      sum of exp, sum of exp * V) per wave.  Scores are kept in log2 units
+//      (scaled by log2(e)/sqrt(hd)), so each probability is one v_exp_f32;
 //   4. the four waves' partials combine in LDS.  With one chunk that is the
 //      output (model.c:57-64: max, exp, 1/sum); otherwise the chunk's
-//      (o, m, l) is stored and k_attn_merge, the next kernel, combines them.
-// Measured on the MI355X, the kernel boundary is the cheapest way to order
-// the partials before the merge: a last-arriver merge inside this kernel
-// needs device-scope stores, a wait for their completion and an atomic,
-// three memory round trips on the critical path while the HBM queues are
-// full, and cost more than the extra launch.
+//      (o, m, l) partial is stored.
+// Merging the chunks of a kv head: when all workgroups of each kv head run on
+// one XCD (checked at state creation by k_xcc_probe and again by every
+// workgroup), the last workgroup of the head to finish merges them through
+// that XCD's L2: partial stores complete in L2, an L2 atomic counts arrivals,
+// and the last arriver reads the partials back from L2 — no device-scope
+// round trip and no second kernel.  Otherwise k_attn_merge, the next kernel
+// on the stream, merges them.
 #include <algorithm>
 
 #include "kernels.h"
 
 namespace ehip {
 
-template <int HD, bool F16> struct DecLay {
-    static constexpr int PE = F16 ? 8 : 4;                 // elements per 16-byte piece
-    static constexpr int P = HD / PE;                      // pieces per row
-    static constexpr int LPR = P <= 8 ? 8 : (P <= 16 ? 16 : (P <= 32 ? 32 : 64));
-    static constexpr int RPL = 64 / LPR;                   // rows per wave load
-    static constexpr int RPB = NWAVE * RPL;                // rows per workgroup load
-    static_assert(HD % PE == 0 && P % 2 == 0, "head_dim must split into an even number of pieces");
-};
-
-template <int HD, bool F16, int NL, int IT>
-constexpr int dec_chunk() { return NL * DecLay<HD, F16>::RPB * IT; }
+constexpr float LOG2E = 1.4426950408889634f;
 
 // Sum over aligned groups of N lanes (N = 8 .. 64), every lane of the group
 // receiving it: DPP moves within rows of 16, lane swaps across rows.
@@ -109,22 +105,45 @@ __device__ __forceinline__ void load_floats(float (&v)[PE], const float *p) {
     }
 }
 
-template <int HD, int GM, bool F16, int NL, int IT>
+__device__ __forceinline__ int xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return (int)x;
+}
+
+template <int HD, bool F16> struct DecLay {
+    static constexpr int PE = F16 ? 8 : 4;                 // elements per 16-byte piece
+    static constexpr int P = HD / PE;                      // pieces per row
+    static constexpr int LPR = P <= 8 ? 8 : (P <= 16 ? 16 : (P <= 32 ? 32 : 64));
+    static constexpr int RPL = 64 / LPR;                   // rows per wave load
+    static constexpr int RPB = NWAVE * RPL;                // rows per workgroup load
+    static_assert(HD % PE == 0 && P % 2 == 0, "head_dim must split into an even number of pieces");
+};
+
+template <int HD, int GM, bool F16, int NL, bool XM>
 __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     using L = DecLay<HD, F16>;
     constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL, RPB = L::RPB;
     constexpr int BR = NL * RPB;      // rows per batch
-    constexpr int CR = BR * IT;       // rows per chunk
+    constexpr int QPR = HD / 4;                                   // float4s per head row (merge)
+    constexpr int NSL = GM * QPR >= WG ? 1 : WG / (GM * QPR);     // chunk slices in the merge
     __shared__ float sm_m[NWAVE][GM], sm_l[NWAVE][GM];
     __shared__ __align__(16) float sm_o[NWAVE][GM][HD];
+    __shared__ float sm_xm[NSL][GM], sm_xl[NSL][GM];
+    __shared__ __align__(16) float4 sm_acc[WG];
+    __shared__ int sm_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = blockIdx.x, c = blockIdx.y;   // kv heads vary fastest: neighbours read whole cache rows
     const int G = a.n_heads / a.n_kv;
     const int pos = a.tokpos[1];
-    const int nc = (pos + 1 + CR - 1) / CR;
+    // rows [0, pos] split into equal chunks over the grid's max_chunks
+    // workgroups of this kv head (two per CU over all kv heads)
+    const int R = (pos + 1 + a.max_chunks - 1) / a.max_chunks;
+    const int nc = (pos + 1 + R - 1) / R;
     if (c >= nc) return;
-    const int t0 = c * CR, t1 = min(pos + 1, t0 + CR);
+    const int t0 = c * R, t1 = min(pos + 1, t0 + R);
+    const int xcc_want = XM ? a.xm_xcc[g] : 0;
     const int j = lane % LPR, rw = lane / LPR;
     const bool pj = j < P;
     const int jc = pj ? j : P - 1;   // clamped piece index for loads
@@ -158,14 +177,14 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     auto load_batch = [&](int tb) {   // K rows first, then V rows
 #pragma unroll
         for (int i = 0; i < NL; i++) {
-            const int t = min(tb + i * RPB + wave * RPL + rw, pos);
+            const int t = min(tb + i * RPB + wave * RPL + rw, t1 - 1);
             const size_t off = (size_t)t * a.kv_dim + hoff + (size_t)jc * PE;
             kr[i] = F16 ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.kc) + off)
                         : *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.kc) + off);
         }
 #pragma unroll
         for (int i = 0; i < NL; i++) {
-            const int t = min(tb + i * RPB + wave * RPL + rw, pos);
+            const int t = min(tb + i * RPB + wave * RPL + rw, t1 - 1);
             const size_t off = (size_t)t * a.kv_dim + hoff + (size_t)jc * PE;
             vr[i] = F16 ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.vc) + off)
                         : *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.vc) + off);
@@ -233,7 +252,10 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     }
 
     // ---- 3. batches of BR rows: the next batch's loads are issued before the
-    // current batch's scores; a running (max, sum, output) per wave --------
+    // current batch's scores; a running (max, sum, output) per wave.  Scores
+    // are in log2 units (scaled by log2(e)/sqrt(hd)), so a probability is one
+    // v_exp_f32. ------------------------------------------------------------
+    const float sscale = a.inv_sqrt * LOG2E;
     float m[GM], l[GM], o[GM][PE];
 #pragma unroll
     for (int h = 0; h < GM; h++) {
@@ -242,13 +264,11 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < PE; e++) o[h][e] = 0.0f;
     }
-    for (int it = 0; it < IT; it++) {
-        const int tb = t0 + it * BR;
-        if (tb >= t1) break;
+    for (int tb = t0; tb < t1; tb += BR) {
         uint4 kc[NL], vc[NL];
 #pragma unroll
         for (int i = 0; i < NL; i++) { kc[i] = kr[i]; vc[i] = vr[i]; }
-        if (it + 1 < IT && tb + BR < t1) load_batch(tb + BR);
+        if (tb + BR < t1) load_batch(tb + BR);
         float sc[NL][GM];
 #pragma unroll
         for (int i = 0; i < NL; i++) {
@@ -262,10 +282,10 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
             }
 #pragma unroll
             for (int h = 0; h < GM; h++) {
-                float sv = 0.0f;
+                float sv = qv[h][0] * kf[0];
 #pragma unroll
-                for (int e = 0; e < PE; e++) sv += qv[h][e] * kf[e];
-                sc[i][h] = group_sum<LPR>(pj ? sv : 0.0f) * a.inv_sqrt;
+                for (int e = 1; e < PE; e++) sv = fmaf(qv[h][e], kf[e], sv);
+                sc[i][h] = group_sum<LPR>(pj ? sv : 0.0f) * sscale;
             }
         }
         float mn[GM];
@@ -276,7 +296,7 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
             for (int i = 0; i < NL; i++)
                 if (tb + i * RPB + wave * RPL + rw < t1) mx = fmaxf(mx, sc[i][h]);
             mn[h] = fmaxf(m[h], stride_max<LPR>(mx));
-            const float r = m[h] == -INFINITY ? 0.0f : expf(m[h] - mn[h]);
+            const float r = m[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[h] - mn[h]);
             l[h] *= r;
 #pragma unroll
             for (int e = 0; e < PE; e++) o[h][e] *= r;
@@ -295,10 +315,10 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
             }
 #pragma unroll
             for (int h = 0; h < GM; h++) {
-                const float p = expf(sc[i][h] - m[h]);
+                const float p = __builtin_amdgcn_exp2f(sc[i][h] - m[h]);
                 l[h] += p;
 #pragma unroll
-                for (int e = 0; e < PE; e++) o[h][e] += p * vf[e];
+                for (int e = 0; e < PE; e++) o[h][e] = fmaf(p, vf[e], o[h][e]);
             }
         }
     }
@@ -315,7 +335,8 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     __syncthreads();
 
     // ---- 4. combine the waves; publish or write ----------------------------
-    // Partials: o at part[head][chunk][HD], (m, l) at part_ml[head][chunk][2].
+    // Partials: o at part[head][chunk][HD], (m, l) at part_ml[head][chunk][2],
+    // m in log2 units.
     const size_t head0 = (size_t)g * G;   // first query head of the group
     float *part_ml = a.part + (size_t)a.n_heads * a.max_chunks * HD;
     for (int i = tid; i < G * HD; i += WG) {
@@ -327,9 +348,9 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
 #pragma unroll
         for (int w = 0; w < NWAVE; w++) {
             const float mw = sm_m[w][h];
-            const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
-            O += f * sm_o[w][h][d];
-            S += f * sm_l[w][h];
+            const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            O = fmaf(f, sm_o[w][h][d], O);
+            S = fmaf(f, sm_l[w][h], S);
         }
         if (nc == 1) {
             a.out[(head0 + h) * HD + d] = O * (1.0f / S);
@@ -339,22 +360,107 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
             if (d == 0) { part_ml[2 * slot] = M; part_ml[2 * slot + 1] = S; }
         }
     }
+    if (!XM || nc == 1) return;
+
+    // ---- 5. the last chunk of this kv head to finish merges through L2 ------
+    // Every workgroup of kv head g runs on XCD a.xm_xcc[g]: its partial
+    // stores are complete in that L2 after the wait, the counter lives in the
+    // same L2 (workgroup-scope atomics are performed there), and the last
+    // arriver's loads of the partials hit it (its L1 has never held them).
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        if (xcc_id() != xcc_want) __hip_atomic_fetch_or(a.xm_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(a.xm_cnt + g * XM_CNT_STRIDE, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        sm_last = old == nc - 1;
+    }
+    __syncthreads();
+    if (!sm_last) return;
+    // o = sum_k o_k 2^(m_k - M) / sum_k l_k 2^(m_k - M),  M = max_k m_k;
+    // thread (s, h, q) owns float4 q of head h and chunks s, s + NSL, ...
+    // (one wave per (s, h) when GM * QPR = 64, so its chunk loop is uniform),
+    // merged online in rounds of KB chunks whose loads are all in flight
+    const int u = tid % (GM * QPR), hh = u / QPR, q = u % QPR, sl = tid / (GM * QPR);
+    const bool act = sl < NSL && hh < G;
+    const float2 *pml = reinterpret_cast<const float2 *>(part_ml) + (head0 + min(hh, G - 1)) * a.max_chunks;
+    const float *po = a.part + (head0 + min(hh, G - 1)) * a.max_chunks * HD + 4 * q;
+    float mr = -INFINITY, sr = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (act) {
+        constexpr int KB = 8;
+        for (int k0 = sl; k0 < nc; k0 += KB * NSL) {
+            float2 ml[KB];
+            float4 ov[KB];
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                const int k = k0 + b * NSL;
+                if (k < nc) {
+                    ml[b] = pml[k];
+                    ov[b] = *reinterpret_cast<const float4 *>(po + (size_t)k * HD);
+                } else {
+                    ml[b] = make_float2(-INFINITY, 0.0f);
+                    ov[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+            }
+            float mn = mr;
+#pragma unroll
+            for (int b = 0; b < KB; b++) mn = fmaxf(mn, ml[b].x);
+            const float r = mr == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr - mn);
+            sr *= r; acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
+            mr = mn;
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                const float f = ml[b].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[b].x - mr);
+                sr = fmaf(ml[b].y, f, sr);
+                acc.x = fmaf(f, ov[b].x, acc.x); acc.y = fmaf(f, ov[b].y, acc.y);
+                acc.z = fmaf(f, ov[b].z, acc.z); acc.w = fmaf(f, ov[b].w, acc.w);
+            }
+        }
+        if (q == 0) sm_xm[sl][hh] = mr;
+    }
+    __syncthreads();
+    if (act) {
+        float MM = sm_xm[0][hh];
+#pragma unroll
+        for (int s2 = 1; s2 < NSL; s2++) MM = fmaxf(MM, sm_xm[s2][hh]);
+        const float r = mr == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr - MM);
+        acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
+        sm_acc[tid] = acc;
+        if (q == 0) sm_xl[sl][hh] = sr * r;
+    }
+    __syncthreads();
+    if (sl == 0 && hh < G) {
+        float4 O = sm_acc[u];
+        float S = sm_xl[0][hh];
+#pragma unroll
+        for (int s2 = 1; s2 < NSL; s2++) {
+            const float4 v = sm_acc[s2 * GM * QPR + u];
+            O.x += v.x; O.y += v.y; O.z += v.z; O.w += v.w;
+            S += sm_xl[s2][hh];
+        }
+        const float r = 1.0f / S;
+        *reinterpret_cast<float4 *>(a.out + (head0 + hh) * HD + 4 * q) = make_float4(O.x * r, O.y * r, O.z * r, O.w * r);
+    }
+    if (tid == 0) __hip_atomic_store(a.xm_cnt + g * XM_CNT_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Split-K merge, one workgroup per query head (the next kernel on the
-// stream, so the partials written above are visible without fences):
-//   o = sum_k o_k e^(m_k - M) / sum_k l_k e^(m_k - M),  M = max_k m_k.
-// Thread (s, q) owns float4 quad q of the head row and chunks k = s, s + NS,
-// ...; every partial it needs is loaded in one batch, issued together with
-// the chunk statistics, before any reduction.
+// Split-K merge, one workgroup per query head, when the chunks of a kv head
+// do not all run on one XCD (the next kernel on the stream, so the partials
+// written above are visible without fences):
+//   o = sum_k o_k 2^(m_k - M) / sum_k l_k 2^(m_k - M),  M = max_k m_k
+// (chunk maxima are in log2 units).  Thread (s, q) owns float4 quad q of the
+// head row and chunks k = s, s + NS, ...; every partial it needs is loaded in
+// one batch, issued together with the chunk statistics, before any reduction.
 template <int HD>
-__global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a, int chunk) {
+__global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a) {
     constexpr int QPR = HD / 4, NS = WG / QPR, KB = 16;
     extern __shared__ __align__(16) float dyn[];   // [max_chunks] float2, then [NS][HD]
     __shared__ float red[NWAVE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
     const int pos = a.tokpos[1];
-    const int nc = (pos + 1 + chunk - 1) / chunk;
+    const int R = (pos + 1 + a.max_chunks - 1) / a.max_chunks;
+    const int nc = (pos + 1 + R - 1) / R;
     if (nc == 1) return;   // the attention kernel wrote the output
     float2 *sml = reinterpret_cast<float2 *>(dyn);
     float *slice = dyn + 2 * a.max_chunks;
@@ -384,7 +490,7 @@ __global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a, int chunk) {
     for (int w = 1; w < NWAVE; w++) M = fmaxf(M, red[w]);
     float sp = 0.0f;
     for (int k = tid; k < nc; k += WG) {
-        const float f = expf(sml[k].x - M);
+        const float f = __builtin_amdgcn_exp2f(sml[k].x - M);
         sml[k].x = f;
         sp += sml[k].y * f;
     }
@@ -410,36 +516,51 @@ __global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a, int chunk) {
     }
 }
 
-// --------------------------------------------------------------------------
-int attn_decode_chunk(int hd, bool f16kv) {
-    switch (hd) {
-        case 48: return f16kv ? dec_chunk<48, true, ATT_DEC_NL, ATT_DEC_IT>() : dec_chunk<48, false, ATT_DEC_NL, ATT_DEC_IT>();
-        case 64: return f16kv ? dec_chunk<64, true, ATT_DEC_NL, ATT_DEC_IT>() : dec_chunk<64, false, ATT_DEC_NL, ATT_DEC_IT>();
-        case 128: return f16kv ? dec_chunk<128, true, ATT_DEC_NL, ATT_DEC_IT>() : dec_chunk<128, false, ATT_DEC_NL, ATT_DEC_IT>();
-    }
+// Records the XCD of every workgroup of a (gx, gy) grid: out[y * gx + x].
+__global__ void k_xcc_probe(int *out) {
+    if (threadIdx.x == 0) out[blockIdx.y * gridDim.x + blockIdx.x] = xcc_id();
+}
+
+int launch_xcc_probe(hipStream_t st, int gx, int gy, int *out) {
+    if (gx <= 0 || gy <= 0) return -1;
+    hipLaunchKernelGGL(k_xcc_probe, dim3(gx, gy), dim3(64), 0, st, out);
     return 0;
+}
+
+// --------------------------------------------------------------------------
+int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu) {
+    if (hd != 48 && hd != 64 && hd != 128) return 0;
+    const int by_rows = (ctx + ATT_DEC_CR - 1) / ATT_DEC_CR;
+    const int by_cus = n_kv > 0 ? 2 * n_cu / n_kv : 1;
+    return std::max(1, std::max(by_rows, by_cus));
+}
+
+template <int HD, bool F16, int GM>
+static void dec_launch(hipStream_t st, const AttnArgs &a, dim3 grid) {
+    constexpr int NL = ATT_DEC_NL;
+    if (a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, true>), grid, dim3(WG), 0, st, a);
+    else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, false>), grid, dim3(WG), 0, st, a);
 }
 
 template <int HD, bool F16>
 static int dec_pick_g(hipStream_t st, const AttnArgs &a, bool with_merge) {
     const int G = a.n_heads / a.n_kv;
     dim3 grid(a.n_kv, a.max_chunks);
-    constexpr int NL = ATT_DEC_NL, IT = ATT_DEC_IT;
-    if (G <= 1) hipLaunchKernelGGL((k_attn_dec<HD, 1, F16, NL, IT>), grid, dim3(WG), 0, st, a);
-    else if (G <= 2) hipLaunchKernelGGL((k_attn_dec<HD, 2, F16, NL, IT>), grid, dim3(WG), 0, st, a);
-    else if (G <= 4) hipLaunchKernelGGL((k_attn_dec<HD, 4, F16, NL, IT>), grid, dim3(WG), 0, st, a);
-    else if (G <= 8) hipLaunchKernelGGL((k_attn_dec<HD, 8, F16, NL, IT>), grid, dim3(WG), 0, st, a);
+    if (G <= 1) dec_launch<HD, F16, 1>(st, a, grid);
+    else if (G <= 2) dec_launch<HD, F16, 2>(st, a, grid);
+    else if (G <= 4) dec_launch<HD, F16, 4>(st, a, grid);
+    else if (G <= 8) dec_launch<HD, F16, 8>(st, a, grid);
     else return -1;
-    if (!with_merge) return 0;
+    if (!with_merge || a.xm_cnt) return 0;
     const size_t lds = 8 * (size_t)a.max_chunks + 4 * (size_t)(WG / (HD / 4)) * HD;
-    hipLaunchKernelGGL((k_attn_merge<HD>), dim3(a.n_heads), dim3(WG), lds, st, a, dec_chunk<HD, F16, NL, IT>());
+    hipLaunchKernelGGL((k_attn_merge<HD>), dim3(a.n_heads), dim3(WG), lds, st, a);
     return 0;
 }
 
 int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_merge) {
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || !a.part) return -1;
-    const int cr = attn_decode_chunk(a.hd, f16kv);
-    if (cr <= 0 || (a.ctx + cr - 1) / cr > a.max_chunks) return -1;
+    if (a.xm_cnt && (!a.xm_err || !a.xm_xcc)) return -1;
+    if ((long)a.max_chunks * ATT_DEC_CR < a.ctx) return -1;
     switch (a.hd) {
         case 48: return f16kv ? dec_pick_g<48, true>(st, a, with_merge) : dec_pick_g<48, false>(st, a, with_merge);
         case 64: return f16kv ? dec_pick_g<64, true>(st, a, with_merge) : dec_pick_g<64, false>(st, a, with_merge);

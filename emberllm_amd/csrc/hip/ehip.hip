@@ -238,6 +238,12 @@ struct EhipState {
     float *part;
     float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
     int mc_dec;
+    // in-kernel merge of the decode attention chunks (see attn_decode.hip):
+    // arrival counters [n_layers][n_kv][XM_CNT_STRIDE], the XCD of each kv
+    // head's workgroups, and the error flag, which sits at logits_d[vocab] so
+    // the per-step logits copy brings it to the host
+    bool xm_on;
+    int *xm_cnt, *xm_xcc, *xm_err;
     // prefill scratch
     float *X, *QKV, *O, *H, *xf, *dxp;
     int8_t *qx; int *xsum, *ids_d;
@@ -289,6 +295,50 @@ static int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
+// Decide whether the decode attention merges its chunks in-kernel: run the
+// probe kernel on the attention's grid and require every workgroup of each kv
+// head to report the same XCD (the dispatcher deals a grid's workgroups to
+// the XCDs round-robin, so with n_kv a multiple of the XCD count each head
+// stays on one).  EHIP_XMERGE=0 forces the merge kernel.
+static int xm_probe(EhipState *s) {
+    const int nkv = s->m->cfg.n_kv_heads, gy = s->mc_dec;
+    s->xm_on = false;
+    if (!env_int("EHIP_XMERGE", 1)) return 0;
+    std::vector<int> h((size_t)nkv * gy, -1);
+    int *d = nullptr;
+    HCHK(hipMalloc(&d, 4 * h.size()), -1);
+    const int rc = launch_xcc_probe(s->st, nkv, gy, d);
+    const hipError_t e1 = hipStreamSynchronize(s->st);
+    const hipError_t e2 = hipMemcpy(h.data(), d, 4 * h.size(), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (rc || e1 != hipSuccess || e2 != hipSuccess) { set_err("XCD probe kernel failed"); return -1; }
+    bool ok = true;
+    for (int g = 0; g < nkv && ok; g++)
+        for (int y = 1; y < gy && ok; y++) ok = h[(size_t)y * nkv + g] == h[g];
+    if (!ok) return 0;
+    HCHK(hipMemcpy(s->xm_xcc, h.data(), 4 * (size_t)nkv, hipMemcpyHostToDevice), -1);
+    s->xm_on = true;
+    return 0;
+}
+
+// After a launch that found a workgroup on an unexpected XCD the counters may
+// hold stale arrivals: clear them with the flag.
+static int xm_reset(EhipState *s) {
+    const EhipConfig &c = s->m->cfg;
+    HCHK(hipMemsetAsync(s->xm_cnt, 0, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, s->st), -1);
+    HCHK(hipMemsetAsync(s->xm_err, 0, 4, s->st), -1);
+    HCHK(hipStreamSynchronize(s->st), -1);
+    return 0;
+}
+
+static int xm_check(EhipState *s, int flag) {
+    if (!flag) return 0;
+    xm_reset(s);
+    set_err("decode attention: a workgroup ran on another XCD than the state's probe found; its chunk merge "
+            "is invalid (set EHIP_XMERGE=0 to merge with a second kernel)");
+    return -1;
+}
+
 extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     const EhipConfig &c = m->cfg;
     const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
@@ -301,13 +351,14 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     const size_t kvb = (size_t)c.n_layers * ctx * kvd * s->esize;
-    const int dch = attn_decode_chunk(hd, s->f16kv != 0);
-    if (dch <= 0) {
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || n_cu <= 0) n_cu = 1;
+    s->mc_dec = attn_decode_chunks(ctx, c.n_kv_heads, hd, n_cu);
+    if (s->mc_dec <= 0) {
         set_err("head_dim %d not supported by the attention kernel", hd);
         ehip_state_destroy(s);
         return nullptr;
     }
-    s->mc_dec = (ctx + dch - 1) / dch;
     const size_t ldk_max = (size_t)attn_prefill_ldk(0, ctx);
     s->pf_chunk = (int)std::max<size_t>(1, std::min<size_t>(std::min(PF_CHUNK, ctx),
                                                             PF_SCORES_MAX / (4 * ldk_max * c.n_heads)));
@@ -319,7 +370,9 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->qkv = (float *)salloc(s, 4 * (size_t)(qd + 2 * kvd))) &&
               (s->o = (float *)salloc(s, 4 * (size_t)qd)) &&
               (s->h = (float *)salloc(s, 4 * (size_t)c.hidden_dim)) &&
-              (s->logits_d = (float *)salloc(s, 4 * (size_t)c.vocab_size, true)) &&
+              (s->logits_d = (float *)salloc(s, 4 * ((size_t)c.vocab_size + 4), true)) &&
+              (s->xm_cnt = (int *)salloc(s, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, true)) &&
+              (s->xm_xcc = (int *)salloc(s, 4 * (size_t)c.n_kv_heads)) &&
               (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * s->mc_dec * (hd + 2))) &&
               (s->X = (float *)salloc(s, 4 * pfc * c.dim)) &&
               (s->QKV = (float *)salloc(s, 4 * pfc * (qd + 2 * kvd))) &&
@@ -359,14 +412,19 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         ehip_state_destroy(s);
         return nullptr;
     }
+    s->xm_err = reinterpret_cast<int *>(s->logits_d + c.vocab_size);
+    if (xm_probe(s)) {
+        ehip_state_destroy(s);
+        return nullptr;
+    }
     if (hipHostMalloc(&s->tokpos_h, 16, hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc(&s->logits_h, 4 * (size_t)c.vocab_size, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(&s->logits_h, 4 * ((size_t)c.vocab_size + 4), hipHostMallocDefault) != hipSuccess ||
         hipEventCreate(&s->ev0) != hipSuccess || hipEventCreate(&s->ev1) != hipSuccess) {
         set_err("pinned host allocation failed");
         ehip_state_destroy(s);
         return nullptr;
     }
-    memset(s->logits_h, 0, 4 * (size_t)c.vocab_size);
+    memset(s->logits_h, 0, 4 * ((size_t)c.vocab_size + 4));
     return s;
 }
 
@@ -390,6 +448,11 @@ static int enq_attn_decode(EhipState *s, int l, bool with_merge = true) {
     AttnArgs a = attn_args(s, l);
     a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
     a.part = s->part; a.max_chunks = s->mc_dec;
+    if (s->xm_on) {
+        a.xm_cnt = s->xm_cnt + (size_t)l * s->m->cfg.n_kv_heads * XM_CNT_STRIDE;
+        a.xm_xcc = s->xm_xcc;
+        a.xm_err = s->xm_err;
+    }
     a.out = s->o;
     return launch_attn_decode(s->st, s->f16kv, a, with_merge);
 }
@@ -447,7 +510,7 @@ static int enq_step(EhipState *s) {
     const int V = s->m->cfg.vocab_size;
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 8, hipMemcpyHostToDevice, s->st), -1);
     if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
-    HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * (size_t)V, hipMemcpyDeviceToHost, s->st), -1);
+    HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * ((size_t)V + 1), hipMemcpyDeviceToHost, s->st), -1);
     return 0;
 }
 
@@ -475,7 +538,17 @@ extern "C" float *ehip_forward(EhipState *s, int tok, int pos) {
     s->tokpos_h[1] = pos;
     if (run_step(s)) return nullptr;
     HCHK(hipStreamSynchronize(s->st), nullptr);
+    int flag;
+    memcpy(&flag, s->logits_h + s->m->cfg.vocab_size, 4);
+    if (xm_check(s, flag)) return nullptr;
     return s->logits_h;
+}
+
+// The error flag after a device-held loop.
+static int xm_flag(EhipState *s) {
+    int flag = 0;
+    HCHK(hipMemcpy(&flag, s->xm_err, 4, hipMemcpyDeviceToHost), -1);
+    return xm_check(s, flag);
 }
 
 // One step of the device-resident greedy loop: the decode launches, then the
@@ -534,6 +607,7 @@ extern "C" int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *
         HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
         *ms = t;
     }
+    if (xm_flag(s)) return -1;
     if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
     return 0;
 }
@@ -664,6 +738,7 @@ extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, Embe
         *ms = t;
     }
     if (sampler_download(s, smp)) return -1;
+    if (xm_flag(s)) return -1;
     if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
     return 0;
 }

@@ -39,12 +39,12 @@ constexpr int MATVEC_MAX_GRID = 2048;
 int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
 
 // ------------------------------------------------------------- attention --
-// GQA attention against the cache.  Prefill: causal flash attention of n_tok
-// query tokens on the fp32 matrix cores.  Decode: one token, split over
-// chunks of positions (flash-decoding) with a merge kernel; the token's raw
-// q/k/v (straight out of the QKV matvec) is QK-normed and rotated in the
-// prologue and its k/v are written to the cache at `pos` by the chunk that
-// owns it.
+// GQA attention against the cache.  Prefill: causal attention of n_tok query
+// tokens in the reference's floating-point order.  Decode: one token, split
+// over chunks of positions (flash-decoding), merged in-kernel or by a merge
+// kernel; the token's raw q/k/v (straight out of the QKV matvec) is
+// QK-normed and rotated in the prologue and its k/v are written to the cache
+// at `pos` by the chunk that owns it.
 struct AttnArgs {
     const float *q;        // fused: raw q|k|v row; else rotated Q rows
     int q_stride;          // floats between consecutive tokens' q
@@ -59,6 +59,12 @@ struct AttnArgs {
     int n_tok;
     float *part;           // decode: chunk partials, o [n_heads][max_chunks][hd] then (m, l) [n_heads][max_chunks]
     int max_chunks;
+    // decode, optional: merge the chunks of each kv head inside the chunk
+    // kernel through the L2 of the one XCD all of them run on.  xm_cnt:
+    // arrival counters of this layer, [n_kv] spaced XM_CNT_STRIDE ints apart,
+    // zero between launches; xm_xcc: the XCD of each kv head's workgroups;
+    // xm_err: set nonzero by a workgroup that finds itself on another XCD.
+    int *xm_cnt; const int *xm_xcc; int *xm_err;
     float *out;            // [n_tok][n_heads*hd]
     // prefill scratch: scores, then probabilities, [n_heads][n_tok][ldk]
     // (ldk >= pos_base + n_tok, a multiple of 4) and 1/sum per row [n_heads][n_tok]
@@ -68,13 +74,19 @@ struct AttnArgs {
 // prefill: q rows already normed and rotated, k/v already in the cache
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
 inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }
-// decode (one token, fused QK-norm / RoPE / KV store); max_chunks must be at
-// least ceil(ctx / attn_decode_chunk(hd, f16kv))
-// with_merge = false launches the chunk kernel alone (measurement)
+// decode (one token, fused QK-norm / RoPE / KV store) over a grid of
+// (n_kv, max_chunks) workgroups, max_chunks = attn_decode_chunks(...).
+// Without xm_cnt the merge is a second kernel; with_merge = false leaves it
+// out (measurement).
 int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_merge = true);
-int attn_decode_chunk(int hd, bool f16kv);
-constexpr int ATT_DEC_NL = 4;   // K and V pieces per thread per batch in the decode attention
-constexpr int ATT_DEC_IT = 2;   // batches per chunk
+// workgroups per kv head: two per CU over all kv heads, or more when a chunk
+// would exceed ATT_DEC_CR rows (0: head_dim not supported)
+int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu);
+constexpr int ATT_DEC_NL = 5;       // K and V pieces per thread per batch in the decode attention
+constexpr int ATT_DEC_CR = 160;     // positions per decode attention workgroup before more are added
+constexpr int XM_CNT_STRIDE = 32;   // ints between arrival counters (one 128-byte line each)
+// out[y * gx + x] = the XCD that workgroup (x, y) of a (gx, gy) grid ran on
+int launch_xcc_probe(hipStream_t st, int gx, int gy, int *out);
 
 // QK-norm + RoPE of n_tok tokens' q (in place) and k, and the k/v cache
 // store, for prefill.  qkv rows are [q | k | v] with row stride `stride`.

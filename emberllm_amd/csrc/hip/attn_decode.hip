@@ -11,7 +11,7 @@
 // Grid = (kv heads, max_chunks), kv heads varying fastest, so neighbouring
 // workgroups read whole cache rows.  Rows [0, pos] of each kv head are split
 // into equal chunks, one per workgroup of that head; with max_chunks =
-// 2 * #CUs / n_kv every CU streams the same share whatever the position (a CU
+// ATT_DEC_WPC * #CUs / n_kv every CU streams the same share whatever the position (a CU
 // holding one more chunk than the others would set the kernel's length).  A
 // workgroup serves all kv_mul query heads of its kv head from the same K/V
 // rows, so each cache row is read once per step.  Lane (rw, j) of a wave holds
@@ -116,21 +116,21 @@ template <int HD, bool F16> struct DecLay {
     static constexpr int P = HD / PE;                      // pieces per row
     static constexpr int LPR = P <= 8 ? 8 : (P <= 16 ? 16 : (P <= 32 ? 32 : 64));
     static constexpr int RPL = 64 / LPR;                   // rows per wave load
-    static constexpr int RPB = NWAVE * RPL;                // rows per workgroup load
     static_assert(HD % PE == 0 && P % 2 == 0, "head_dim must split into an even number of pieces");
 };
 
-template <int HD, int GM, bool F16, int NL, bool XM>
-__global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
+template <int HD, int GM, bool F16, int NL, int NW, bool XM>
+__global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     using L = DecLay<HD, F16>;
-    constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL, RPB = L::RPB;
+    constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL;
+    constexpr int NT = NW * 64, RPB = NW * RPL;   // threads, rows per workgroup load
     constexpr int BR = NL * RPB;      // rows per batch
     constexpr int QPR = HD / 4;                                   // float4s per head row (merge)
-    constexpr int NSL = GM * QPR >= WG ? 1 : WG / (GM * QPR);     // chunk slices in the merge
-    __shared__ float sm_m[NWAVE][GM], sm_l[NWAVE][GM];
-    __shared__ __align__(16) float sm_o[NWAVE][GM][HD];
+    constexpr int NSL = GM * QPR >= NT ? 1 : NT / (GM * QPR);     // chunk slices in the merge
+    __shared__ float sm_m[NW][GM], sm_l[NW][GM];
+    __shared__ __align__(16) float sm_o[NW][GM][HD];
     __shared__ float sm_xm[NSL][GM], sm_xl[NSL][GM];
-    __shared__ __align__(16) float4 sm_acc[WG];
+    __shared__ __align__(16) float4 sm_acc[NT];
     __shared__ int sm_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -339,14 +339,14 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     // m in log2 units.
     const size_t head0 = (size_t)g * G;   // first query head of the group
     float *part_ml = a.part + (size_t)a.n_heads * a.max_chunks * HD;
-    for (int i = tid; i < G * HD; i += WG) {
+    for (int i = tid; i < G * HD; i += NT) {
         const int h = i / HD, d = i % HD;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NWAVE; w++) M = fmaxf(M, sm_m[w][h]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_m[w][h]);
         float O = 0.0f, S = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NWAVE; w++) {
+        for (int w = 0; w < NW; w++) {
             const float mw = sm_m[w][h];
             const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
             O = fmaf(f, sm_o[w][h][d], O);
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(WG) void k_attn_dec(AttnArgs a) {
     float mr = -INFINITY, sr = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (act) {
-        constexpr int KB = 8;
+        constexpr int KB = 16;   // one round for up to 16 * NSL chunks (64 with two query heads of 128)
         for (int k0 = sl; k0 < nc; k0 += KB * NSL) {
             float2 ml[KB];
             float4 ov[KB];
@@ -531,15 +531,15 @@ int launch_xcc_probe(hipStream_t st, int gx, int gy, int *out) {
 int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu) {
     if (hd != 48 && hd != 64 && hd != 128) return 0;
     const int by_rows = (ctx + ATT_DEC_CR - 1) / ATT_DEC_CR;
-    const int by_cus = n_kv > 0 ? 2 * n_cu / n_kv : 1;
+    const int by_cus = n_kv > 0 ? ATT_DEC_WPC * n_cu / n_kv : 1;
     return std::max(1, std::max(by_rows, by_cus));
 }
 
 template <int HD, bool F16, int GM>
 static void dec_launch(hipStream_t st, const AttnArgs &a, dim3 grid) {
-    constexpr int NL = ATT_DEC_NL;
-    if (a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, true>), grid, dim3(WG), 0, st, a);
-    else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, false>), grid, dim3(WG), 0, st, a);
+    constexpr int NL = ATT_DEC_NL, NW = ATT_DEC_NW;
+    if (a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, true>), grid, dim3(NW * 64), 0, st, a);
+    else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, false>), grid, dim3(NW * 64), 0, st, a);
 }
 
 template <int HD, bool F16>

@@ -83,6 +83,8 @@ int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_
 // would exceed ATT_DEC_CR rows (0: head_dim not supported)
 int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu);
 constexpr int ATT_DEC_NL = 5;       // K and V pieces per thread per batch in the decode attention
+constexpr int ATT_DEC_NW = 4;       // waves per decode attention workgroup
+constexpr int ATT_DEC_WPC = 2;      // decode attention workgroups per CU
 constexpr int ATT_DEC_CR = 160;     // positions per decode attention workgroup before more are added
 constexpr int XM_CNT_STRIDE = 32;   // ints between arrival counters (one 128-byte line each)
 // out[y * gx + x] = the XCD that workgroup (x, y) of a (gx, gy) grid ran on

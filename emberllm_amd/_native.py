@@ -124,6 +124,7 @@ PROTOTYPES = {
     "ehip_kv_read": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]),
     "ehip_kv_write": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]),
     "ehip_set_graph_mode": (ctypes.c_int, [_P, ctypes.c_int]),
+    "ehip_decode_fusion": (ctypes.c_int, [_P]),
     "ehip_debug_buffer": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_uint64]),
     "ehip_time_decode": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _FP]),
     "ehip_generate_greedy": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _IP, _FP]),

@@ -841,6 +841,10 @@ extern "C" int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t b
     return 0;
 }
 
+extern "C" int ehip_decode_fusion(const EhipState *s) {
+    return s->xm_on ? 1 : 0;
+}
+
 extern "C" int ehip_set_graph_mode(EhipState *s, int mode) {
     s->graph_mode = mode ? 1 : 0;
     return 0;

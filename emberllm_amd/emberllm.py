@@ -66,6 +66,11 @@ class Engine:
     def set_graph(self, on):
         self.lib.ehip_set_graph_mode(self.dev, 1 if on else 0)
 
+    def decode_fusion(self):
+        """Bit 0: the attention kernel merges its chunks itself
+        (ehip_decode_fusion)."""
+        return self.lib.ehip_decode_fusion(self.dev)
+
     def time_decode(self, pos0, steps):
         ms = ctypes.c_float()
         if self.lib.ehip_time_decode(self.dev, int(pos0), int(steps), ctypes.byref(ms)) != 0:

@@ -115,6 +115,10 @@ int ehip_kv_write(EhipState *s, int which, int layer, int n_pos, const void *hos
 int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t bytes);
 /* 0: eager launches, 1: one hipGraph per decode step (default). */
 int ehip_set_graph_mode(EhipState *s, int mode);
+/* How the state's decode step is scheduled: bit 0 = the attention kernel
+ * merges its chunks itself (no merge kernel), which needs every workgroup of
+ * a kv head on one XCD; the state checks that at creation. */
+int ehip_decode_fusion(const EhipState *s);
 /* Time `steps` decode steps at positions pos0.. with HIP events recorded on
  * the state's stream; writes the average step time in ms.  Tokens follow the
  * reference bench stream (pos*131+7) % vocab. */

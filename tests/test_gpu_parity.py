@@ -66,6 +66,35 @@ def test_benchmark_shapes(case, oracle_threads):
     say(check_run(teacher_forced(case), case["id"]))
 
 
+@pytest.mark.parametrize("schedule", ["in-kernel-merge", "two-kernel"])
+def test_decode_schedules(schedule, oracle_threads, monkeypatch):
+    """The Qwen3-0.6B shape (8 kv heads: one per XCD of the MI355X) under each
+    decode schedule the state can choose: the attention kernel merging its
+    chunks through the XCD's L2 (the default there) and the chunk kernel +
+    merge kernel (EHIP_XMERGE=0).  Both must match the oracle, including past
+    one chunk per workgroup (prompt 300, decode to depth 332)."""
+    if schedule == "two-kernel":
+        monkeypatch.setenv("EHIP_XMERGE", "0")
+    name = "qwen3_06b"
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    rng = np.random.default_rng(77)
+    ids, toks = rng.integers(0, V, 300), rng.integers(0, V, 32)
+    say(f"qwen3_06b schedule={schedule} p300 d32")
+    eng = emberllm.Engine(path, ctx=400)
+    fusion = eng.decode_fusion()
+    want = {"in-kernel-merge": 1, "two-kernel": 0}[schedule]
+    assert fusion == want, f"state chose fusion {fusion}, expected {want} on this device"
+    orc = oracle.Oracle(path, ctx=400)
+    res = [compare(eng.prefill(ids), orc.prefill(ids))]
+    for i, t in enumerate(toks):
+        res.append(compare(eng.forward(int(t), 300 + i), orc.forward(int(t), 300 + i)))
+    eng.close()
+    orc.close()
+    # bars of the same shape's teacher-forced case (the reference builds' noise floor)
+    say(f"{schedule}: " + check_run(res, "qwen3_06b-p16-d32-s11"))
+
+
 def test_graph_equals_eager():
     """The captured graph replays exactly the eager launch sequence."""
     path = configs.model_path("t_qwen3")

@@ -360,12 +360,15 @@ static int go(hipStream_t st, const MatvecArgs &a, size_t lds) {
     return grid;
 }
 
-// rows per wave: the largest of 4, 2, 1 that still gives every CU a
-// workgroup, within a register budget (wide rows keep fewer rows in flight)
+// rows per wave: the largest of 4, 3, 2, 1 that still gives every CU a
+// workgroup, within a register budget (wide rows keep fewer rows in flight).
+// 3 keeps 3072-row products (Qwen3's w1|w3) at one workgroup per CU instead
+// of 1.5 (some CUs working twice as long as the others).
 template <int DT, int PRO, int EPI, int NCH>
 static int pick_upw(hipStream_t st, const MatvecArgs &a, size_t lds) {
     if constexpr (NCH <= 2) {
         if (a.units >= 4 * NWAVE * 256) return go<DT, PRO, EPI, NCH, 4>(st, a, lds);
+        if (a.units >= 3 * NWAVE * 256) return go<DT, PRO, EPI, NCH, 3>(st, a, lds);
     }
     if constexpr (NCH <= 3) {
         if (a.units >= 2 * NWAVE * 256) return go<DT, PRO, EPI, NCH, 2>(st, a, lds);

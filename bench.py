@@ -275,9 +275,10 @@ def main():
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(achieved / (HBM_PEAK / 1e9), 4),
                 "traffic": profiled_traffic("ehip::k_attn_dec", args.model, depth, args.kv),
-                "kernel": f"k_attn_dec (split-K GQA attention chunk kernel, one layer) at position {depth}, "
-                          f"{ab} algorithmic bytes per launch, mean of {reps_k} launches walking the "
-                          f"{c['n_layers']} layers' caches"}
+                "kernel": f"k_attn_dec (split-K GQA attention over one layer's KV cache"
+                          f"{', chunk partials merged in-kernel by the last workgroup of each kv head' if eng.decode_fusion() & 1 else ''}) "
+                          f"at position {depth}, {ab} algorithmic bytes per launch, mean of {reps_k} "
+                          f"launches walking the {c['n_layers']} layers' caches"}
 
         # ---- depth 128 ------------------------------------------------------
         eng.generate_greedy(tok0, 128, W)

@@ -228,6 +228,24 @@ fail:
 constexpr int PF_CHUNK = 2048;  // prefill tokens per pass through the layers (at most)
 constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores per pass (at most)
 
+// A captured run of device-loop steps.  One graph launch per token leaves
+// the GPU idle for ~7 us between graphs (against ~1.5 us between the kernels
+// inside one), so the device loops capture GEN_UNROLL steps per graph; the
+// steps read their token and position from device memory, so one graph
+// serves any starting point.
+constexpr int GEN_UNROLL = 8;
+struct StepGraph {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+};
+
+static void graph_free(StepGraph &sg) {
+    if (sg.x) (void)hipGraphExecDestroy(sg.x);
+    if (sg.g) (void)hipGraphDestroy(sg.g);
+    sg.x = nullptr;
+    sg.g = nullptr;
+}
+
 struct EhipState {
     EhipModel *m;
     int ctx, f16kv, esize, graph_mode;
@@ -252,16 +270,31 @@ struct EhipState {
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
-    hipGraph_t graph_gen; hipGraphExec_t gexec_gen;
+    StepGraph gen[2];   // device greedy loop: 1 step, GEN_UNROLL steps
     // device sampler: xorshift64* state, history ring, candidates; the
     // sampling decode graph is captured for one parameter set
     unsigned long long *smp_rng; int *smp_meta, *smp_hist; int smp_hist_cap;
     float *smp_pmax, *smp_psum, *smp_cval; int *smp_cidx;
-    hipGraph_t graph_smp; hipGraphExec_t gexec_smp;
+    StepGraph smp[2];   // device sampling loop: 1 step, GEN_UNROLL steps
     SampleParams smp_graph_p; int smp_graph_cap;
     hipEvent_t ev0, ev1;
     std::vector<void *> allocs;
 };
+
+template <class F>
+static int graph_capture(EhipState *s, StepGraph &sg, int steps, F enq) {
+    graph_free(sg);
+    HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), -1);
+    int rc = 0;
+    for (int i = 0; i < steps && !rc; i++) rc = enq();
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s->st, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return -1; }
+    if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return -1; }
+    sg.g = g;
+    HCHK(hipGraphInstantiate(&sg.x, g, nullptr, nullptr, 0), -1);
+    return 0;
+}
 
 static void *salloc(EhipState *s, size_t n, bool zero = false) {
     void *p = nullptr;
@@ -276,10 +309,8 @@ extern "C" void ehip_state_destroy(EhipState *s) {
     (void)hipStreamSynchronize(s->st);
     if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
     if (s->graph) (void)hipGraphDestroy(s->graph);
-    if (s->gexec_gen) (void)hipGraphExecDestroy(s->gexec_gen);
-    if (s->graph_gen) (void)hipGraphDestroy(s->graph_gen);
-    if (s->gexec_smp) (void)hipGraphExecDestroy(s->gexec_smp);
-    if (s->graph_smp) (void)hipGraphDestroy(s->graph_smp);
+    for (StepGraph &g : s->gen) graph_free(g);
+    for (StepGraph &g : s->smp) graph_free(g);
     if (s->smp_hist) (void)hipFree(s->smp_hist);
     for (void *p : s->allocs) (void)hipFree(p);
     if (s->tokpos_h) (void)hipHostFree(s->tokpos_h);
@@ -571,19 +602,20 @@ static int enq_gen_step(EhipState *s) {
     return 0;
 }
 
-static int run_gen_step(EhipState *s) {
-    if (!s->graph_mode) return enq_gen_step(s);
-    if (!s->gexec_gen) {
-        HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), -1);
-        int rc = enq_gen_step(s);
-        hipGraph_t g = nullptr;
-        hipError_t e = hipStreamEndCapture(s->st, &g);
-        if (rc) { if (g) (void)hipGraphDestroy(g); return -1; }
-        if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return -1; }
-        s->graph_gen = g;
-        HCHK(hipGraphInstantiate(&s->gexec_gen, g, nullptr, nullptr, 0), -1);
+// Enqueue n steps of a device loop: graphs of GEN_UNROLL steps, then single
+// steps (each captured on first use), or plain launches without graphs.
+template <class F>
+static int run_steps(EhipState *s, StepGraph (&gr)[2], int n, F enq) {
+    if (!s->graph_mode) {
+        for (int i = 0; i < n; i++)
+            if (enq()) return -1;
+        return 0;
     }
-    HCHK(hipGraphLaunch(s->gexec_gen, s->st), -1);
+    const int big = n / GEN_UNROLL, small = n % GEN_UNROLL;
+    if (big && !gr[1].x && graph_capture(s, gr[1], GEN_UNROLL, enq)) return -1;
+    if (small && !gr[0].x && graph_capture(s, gr[0], 1, enq)) return -1;
+    for (int i = 0; i < big; i++) HCHK(hipGraphLaunch(gr[1].x, s->st), -1);
+    for (int i = 0; i < small; i++) HCHK(hipGraphLaunch(gr[0].x, s->st), -1);
     return 0;
 }
 
@@ -598,8 +630,7 @@ extern "C" int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
     HCHK(hipStreamSynchronize(s->st), -1);
     HCHK(hipEventRecord(s->ev0, s->st), -1);
-    for (int i = 0; i < n; i++)
-        if (run_gen_step(s)) return -1;
+    if (run_steps(s, s->gen, n, [&]() { return enq_gen_step(s); })) return -1;
     HCHK(hipEventRecord(s->ev1, s->st), -1);
     HCHK(hipEventSynchronize(s->ev1), -1);
     if (ms) {
@@ -632,8 +663,7 @@ static SampleParams sampler_params(const EmberSampler *smp) {
 static int sampler_upload(EhipState *s, const EmberSampler *smp) {
     const int cap = smp->history ? smp->hist_cap : 0;
     if (cap > s->smp_hist_cap) {
-        if (s->gexec_smp) { (void)hipGraphExecDestroy(s->gexec_smp); s->gexec_smp = nullptr; }
-        if (s->graph_smp) { (void)hipGraphDestroy(s->graph_smp); s->graph_smp = nullptr; }
+        for (StepGraph &g : s->smp) graph_free(g);
         if (s->smp_hist) (void)hipFree(s->smp_hist);
         s->smp_hist = nullptr;
         s->smp_hist_cap = 0;
@@ -711,25 +741,13 @@ extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, Embe
         if (launch_sample(s->st, sample_args(s, p, cap, V))) { set_err("sampler launch failed"); return -1; }
         return 0;
     };
-    if (s->graph_mode && (!s->gexec_smp || !same_params(p, s->smp_graph_p) || cap != s->smp_graph_cap)) {
-        if (s->gexec_smp) { (void)hipGraphExecDestroy(s->gexec_smp); s->gexec_smp = nullptr; }
-        if (s->graph_smp) { (void)hipGraphDestroy(s->graph_smp); s->graph_smp = nullptr; }
-        HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), -1);
-        const int rc = enq();
-        hipGraph_t g = nullptr;
-        const hipError_t e = hipStreamEndCapture(s->st, &g);
-        if (rc) { if (g) (void)hipGraphDestroy(g); return -1; }
-        if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return -1; }
-        s->graph_smp = g;
-        HCHK(hipGraphInstantiate(&s->gexec_smp, g, nullptr, nullptr, 0), -1);
+    if (!same_params(p, s->smp_graph_p) || cap != s->smp_graph_cap) {   // graphs hold the parameters
+        for (StepGraph &g : s->smp) graph_free(g);
         s->smp_graph_p = p;
         s->smp_graph_cap = cap;
     }
     HCHK(hipEventRecord(s->ev0, s->st), -1);
-    for (int i = 0; i < n; i++) {
-        if (s->graph_mode) HCHK(hipGraphLaunch(s->gexec_smp, s->st), -1);
-        else if (enq()) return -1;
-    }
+    if (run_steps(s, s->smp, n, enq)) return -1;
     HCHK(hipEventRecord(s->ev1, s->st), -1);
     HCHK(hipEventSynchronize(s->ev1), -1);
     if (ms) {

@@ -95,18 +95,20 @@ def test_decode_schedules(schedule, oracle_threads, monkeypatch):
     say(f"{schedule}: " + check_run(res, "qwen3_06b-p16-d32-s11"))
 
 
-def test_graph_equals_eager():
+@pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])
+def test_graph_equals_eager(name):
     """The captured graph replays exactly the eager launch sequence."""
-    path = configs.model_path("t_qwen3")
-    say("graph vs eager bit equality")
+    path = configs.model_path(name)
+    say(f"graph vs eager bit equality ({name})")
+    V = configs.ALL[name]["vocab_size"]
     a = emberllm.Engine(path)
     b = emberllm.Engine(path)
     a.set_graph(True)
     b.set_graph(False)
-    ids = np.arange(5) * 7 % 640
+    ids = np.arange(5) * 7 % V
     np.testing.assert_array_equal(a.prefill(ids), b.prefill(ids))
     for pos in range(5, 15):
-        np.testing.assert_array_equal(a.forward(pos * 3, pos), b.forward(pos * 3, pos))
+        np.testing.assert_array_equal(a.forward(pos * 3 % V, pos), b.forward(pos * 3 % V, pos))
     a.close()
     b.close()
 

@@ -271,6 +271,12 @@ def main():
             "w1w3_swiglu": {"us": ms_w13 * 1e3, "GB_s": wb / (ms_w13 / 1e3) / 1e9, "bytes": wb},
         }
         log(f"kernels: {json.dumps(out['kernels'])}")
+        # the measured streaming-read peak, the second reference point for the step's fraction
+        peak_meas = eng.measure_read_bw(1 << 30, 10)
+        out["hbm_read_peak_measured_GB_s"] = peak_meas
+        out["hbm_roofline_frac_step_vs_measured"] = round(tok_s * mean_bytes / (peak_meas * 1e9), 4)
+        log(f"measured read peak {peak_meas:.0f} GB/s (1 GiB x 10): the step reaches "
+            f"{out['hbm_roofline_frac_step_vs_measured']:.3f} of it")
         achieved = ab / (ms_att / 1e3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(achieved / (HBM_PEAK / 1e9), 4),

@@ -888,6 +888,50 @@ extern "C" int ehip_time_decode(EhipState *s, int pos0, int steps, float *ms) {
     return 0;
 }
 
+// Streaming read: workgroup b reads the SR_PER_WG 16-byte pieces from
+// b * SR_PER_WG on, each thread SR_UNROLL of them 4 KB apart, all loads in
+// flight at once (the pattern of the decode matvecs: contiguous bytes per
+// workgroup, many workgroups).  The XOR of the data is kept alive by a store
+// that only a (practically impossible) zero checksum takes.
+constexpr int SR_UNROLL = 8, SR_PER_WG = SR_UNROLL * WG;   // 32 KB per workgroup
+__global__ __launch_bounds__(WG) void k_stream_read(const uint4 *__restrict__ p, size_t n16, unsigned *sink) {
+    const size_t base = (size_t)blockIdx.x * SR_PER_WG;
+    uint4 v[SR_UNROLL];
+#pragma unroll
+    for (int u = 0; u < SR_UNROLL; u++) v[u] = p[min(base + threadIdx.x + u * WG, n16 - 1)];
+    unsigned acc = 0;
+#pragma unroll
+    for (int u = 0; u < SR_UNROLL; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (acc == 0u && threadIdx.x == 0) sink[blockIdx.x & 63] = acc + 1u;
+}
+
+extern "C" int ehip_measure_read_bw(EhipState *s, uint64_t bytes, int reps, float *gbs) {
+    if (bytes < (1u << 20) || reps <= 0 || !gbs) { set_err("measure_read_bw: bad arguments"); return -1; }
+    if (bytes > (1ull << 36)) { set_err("measure_read_bw: at most 64 GiB"); return -1; }
+    const size_t n16 = (size_t)(bytes / 16);
+    void *buf = nullptr;
+    unsigned *sink = nullptr;
+    HCHK(hipMalloc(&buf, n16 * 16), -1);
+    if (hipMalloc(&sink, 64 * 4) != hipSuccess) { (void)hipFree(buf); set_err("hipMalloc failed"); return -1; }
+    int rc = 0;
+    float t = 0.0f;
+    const dim3 grid((unsigned)((n16 + SR_PER_WG - 1) / SR_PER_WG));
+    if (hipMemsetAsync(buf, 1, n16 * 16, s->st) != hipSuccess) rc = -1;
+    if (!rc) hipLaunchKernelGGL(k_stream_read, grid, dim3(WG), 0, s->st, (const uint4 *)buf, n16, sink);   // warm-up
+    if (!rc && (hipEventRecord(s->ev0, s->st) != hipSuccess)) rc = -1;
+    for (int r = 0; r < reps && !rc; r++)
+        hipLaunchKernelGGL(k_stream_read, grid, dim3(WG), 0, s->st, (const uint4 *)buf, n16, sink);
+    if (!rc && (hipEventRecord(s->ev1, s->st) != hipSuccess || hipEventSynchronize(s->ev1) != hipSuccess ||
+                hipEventElapsedTime(&t, s->ev0, s->ev1) != hipSuccess || hipGetLastError() != hipSuccess))
+        rc = -1;
+    (void)hipStreamSynchronize(s->st);
+    (void)hipFree(buf);
+    (void)hipFree(sink);
+    if (rc || t <= 0.0f) { set_err("measure_read_bw: launch or timing failed"); return -1; }
+    *gbs = (float)((double)n16 * 16 * reps / (t * 1e-3) / 1e9);
+    return 0;
+}
+
 extern "C" int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms) {
     if (pos < 0 || pos >= s->ctx || reps <= 0) { set_err("time_kernel: bad arguments"); return -1; }
     s->tokpos_h[0] = 0;

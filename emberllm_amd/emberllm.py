@@ -114,6 +114,13 @@ class Engine:
             raise RuntimeError(_native.last_error())
         return ms.value
 
+    def measure_read_bw(self, nbytes=1 << 30, reps=10):
+        """Measured streaming read bandwidth of the GPU in GB/s."""
+        gbs = ctypes.c_float()
+        if self.lib.ehip_measure_read_bw(self.dev, int(nbytes), int(reps), ctypes.byref(gbs)) != 0:
+            raise RuntimeError(_native.last_error())
+        return gbs.value
+
     def close(self):
         if getattr(self, "st", None):
             self.lib.ember_state_free(self.st)

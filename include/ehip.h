@@ -125,11 +125,19 @@ int ehip_decode_fusion(const EhipState *s);
 int ehip_time_decode(EhipState *s, int pos0, int steps, float *ms_per_step);
 /* Time `reps` back-to-back launches of one decode-step kernel on the
  * state's stream with HIP events, at position pos; writes average ms.
- * kernel: 0 = the split-K attention chunk kernel (without its merge),
- * 1 = lm_head matvec, 2 = fused w1|w3 matvec.  Launches of kernels 0 and 2
- * walk through the layers, so each streams its own cache rows or weights
- * from HBM as in a decode step. */
+ * kernel: 0 = the split-K attention kernel (with its in-kernel chunk merge
+ * when ehip_decode_fusion reports one; the separate merge kernel is not
+ * timed), 1 = lm_head matvec, 2 = fused w1|w3 matvec.  Launches of kernels 0
+ * and 2 walk through the layers, so each streams its own cache rows or
+ * weights from HBM as in a decode step. */
 int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms_per_launch);
+/* The GPU's measured streaming read bandwidth: `reps` passes of a plain
+ * 16-byte-load kernel (32 KB per workgroup) over a fresh device buffer of
+ * `bytes` (1 MiB to 64 GiB), timed with HIP events on the state's stream;
+ * writes GB/s.  No counterpart in the reference: the measured peak that
+ * decode roofline fractions are also quoted against, beside the 8 TB/s
+ * datasheet figure. */
+int ehip_measure_read_bw(EhipState *s, uint64_t bytes, int reps, float *gb_per_s);
 
 #ifdef __cplusplus
 }

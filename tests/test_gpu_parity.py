@@ -321,3 +321,17 @@ def test_device_greedy_qwen3_shape(oracle_threads):
     res = _greedy_case("qwen3_06b", 16, 24, 12, ctx=48)
     ok = [r["agree"] or r["margin"] < 2 * r["max_abs"] for r in res]
     assert np.mean(ok) >= 0.99, res
+
+
+def test_measured_read_bandwidth():
+    """ehip_measure_read_bw: a plain streaming read over 256 MiB lands between
+    a tenth of and the datasheet's 8 TB/s, and a request below 1 MiB is an
+    error (the host rejects it before any launch)."""
+    say("measured read bandwidth")
+    e = emberllm.Engine(configs.model_path("t_llama"))
+    gbs = e.measure_read_bw(256 << 20, 4)
+    say(f"read bandwidth {gbs:.0f} GB/s")
+    assert 800.0 < gbs < 8000.0, gbs
+    with pytest.raises(RuntimeError):
+        e.measure_read_bw(1024, 1)
+    e.close()

@@ -198,23 +198,27 @@ __global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
 }
 
 // --------------------------------------------------------------------------
-// int8 MFMA GEMM.  Workgroup tile GM_U (units) x GM_T (tokens), four waves in
-// a 2 x 2 arrangement, each owning 2 x 2 MFMA tiles of 32 x 32.  K advances
-// GM_KB quant blocks per stage; stages are double-buffered in LDS (the next
-// stage's global loads are issued before the current stage's products).
+// int8 MFMA GEMM.  Workgroup tile GM_U (units) x TT (tokens, 128 or 64), four
+// waves in a 2 x 2 arrangement, each owning 2 x (TT / 64) MFMA tiles of
+// 32 x 32 (64-token tiles when 128 would leave CUs idle: the 1024-output wo
+// and w2 products of a 2048-token pass).  K advances GM_KB quant blocks per
+// stage; stages are double-buffered in LDS (the next stage's global loads are
+// issued before the current stage's products).
 // Output (i, j) of an MFMA tile sits in lane j + 32*((i/4)%2), accumulator
 // (i%4) + 4*(i/8); A fragments hold W[u][16h .. 16h+15] of one block, B
 // fragments X[t][16h .. 16h+15], h = lane / 32.
-constexpr int GM_U = 128, GM_T = 128, GM_KB = 2;
+constexpr int GM_U = 128, GM_KB = 2;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
-template <int DT, int EPI>
+template <int DT, int EPI, int TT>
 __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
+    constexpr int GM_T = TT, NY = TT / 64;            // tokens per tile, MFMA tiles per wave along tokens
     constexpr int WB = DT == DT_Q8 ? 32 : 16;          // weight bytes per row and block
     constexpr int WROW = GM_KB * WB, XROW = GM_KB * 32; // stage bytes per row
+    static_assert(TT == 64 || TT == 128, "token tile of 64 or 128");
     __shared__ __align__(16) uint8_t ws[2][GM_U * WROW];
     __shared__ __align__(16) int8_t xsm[2][GM_T * XROW];
     __shared__ float dws[2][GM_KB][GM_U], dxs[2][GM_KB][GM_T];
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
     const int j = lane & 31, h = lane >> 5;
     const int u0 = blockIdx.x * GM_U, t0 = blockIdx.y * GM_T;
     const int K = a.W.cols, nb = K / QB, nst = (nb + GM_KB - 1) / GM_KB;
-    const int wu = (wave & 1) * 64, wt = (wave >> 1) * 64;   // this wave's 64 x 64 corner
+    const int wu = (wave & 1) * 64, wt = (wave >> 1) * (TT / 2);   // this wave's 64 x TT/2 corner
 
     // global -> registers for one stage: weights (WROW bytes per row), codes, scales
     constexpr int WLD = GM_U * WROW / 16 / WG, XLD = GM_T * XROW / 16 / WG;
@@ -243,11 +247,12 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
             const int t = min(t0 + row, a.n - 1), blk = min(b0 + c / 32, nb - 1);
             xr[i] = *reinterpret_cast<const int4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
         }
-        {   // GM_KB * (GM_U + GM_T) = 512 scales: two per thread
+        {   // GM_KB * GM_U weight scales and GM_KB * GM_T activation scales: one
+            // and (at most) one per thread
             const int kb = tid / GM_U, r = tid % GM_U;
             const int blk = min(b0 + kb, nb - 1);
             dwr = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk]);
-            const int t = min(t0 + r, a.n - 1);
+            const int t = min(t0 + min(r, GM_T - 1), a.n - 1);
             dxr = a.dx[(size_t)t * nb + blk];
             xsr = DT == DT_Q4 ? a.xs[(size_t)t * nb + blk] : 0;
         }
@@ -259,15 +264,17 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
         for (int i = 0; i < XLD; i++) reinterpret_cast<int4 *>(xsm[buf])[tid + i * WG] = xr[i];
         const int kb = tid / GM_U, r = tid % GM_U;
         dws[buf][kb][r] = dwr;
-        dxs[buf][kb][r] = dxr;
-        sxs[buf][kb][r] = xsr;
+        if (r < GM_T) {
+            dxs[buf][kb][r] = dxr;
+            sxs[buf][kb][r] = xsr;
+        }
     };
 
-    float acc[2][2][16];
+    float acc[2][NY][16];
 #pragma unroll
     for (int x = 0; x < 2; x++)
 #pragma unroll
-        for (int y = 0; y < 2; y++)
+        for (int y = 0; y < NY; y++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[x][y][r] = 0.0f;
 
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int kb = 0; kb < GM_KB; kb++) {
             if (st * GM_KB + kb >= nb) break;
-            i32x4 af[2], bf[2];
+            i32x4 af[2], bf[NY];
 #pragma unroll
             for (int x = 0; x < 2; x++) {      // weight rows wu + 32x + j, k-half h
                 const uint8_t *src = ws[buf] + (size_t)(wu + 32 * x + j) * WROW + kb * WB;
@@ -293,12 +300,12 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
                 }
             }
 #pragma unroll
-            for (int y = 0; y < 2; y++)
+            for (int y = 0; y < NY; y++)
                 bf[y] = *reinterpret_cast<const i32x4 *>(xsm[buf] + (size_t)(wt + 32 * y + j) * XROW + kb * 32 + 16 * h);
 #pragma unroll
             for (int x = 0; x < 2; x++)
 #pragma unroll
-                for (int y = 0; y < 2; y++) {
+                for (int y = 0; y < NY; y++) {
                     i32x16 d = {};
                     d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[x], bf[y], d, 0, 0, 0);
                     const float dx = dxs[buf][kb][wt + 32 * y + j];
@@ -320,7 +327,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
     for (int x = 0; x < 2; x++)
 #pragma unroll
-        for (int y = 0; y < 2; y++) {
+        for (int y = 0; y < NY; y++) {
             const int t = t0 + wt + 32 * y + j;
             if (t >= a.n) continue;
 #pragma unroll
@@ -337,15 +344,18 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
     if (a.W.dtype == DT_Q8 || a.W.dtype == DT_Q4) {
-        dim3 g((a.units + GM_U - 1) / GM_U, (a.n + GM_T - 1) / GM_T);
-#define GMF(DT)                                                                                  \
-    if (a.W.dtype == DT) {                                                                       \
-        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE>), g, dim3(WG), 0, st, a); \
-        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID>), g, dim3(WG), 0, st, a); \
+        // 128-token tiles unless that leaves fewer workgroups than CUs
+        // (a 256-CU part); 64-token tiles then double the grid
+        const int gu = (a.units + GM_U - 1) / GM_U;
+        const bool t64 = (long)gu * ((a.n + 127) / 128) < 256;
+        dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
+#define GMF(DT, TT)                                                                              \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT>), g, dim3(WG), 0, st, a); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT>), g, dim3(WG), 0, st, a); \
         else return -1;                                                                          \
-        return 0;                                                                                \
-    }
-        GMF(DT_Q8) GMF(DT_Q4)
+        return 0;
+        if (a.W.dtype == DT_Q8) { if (t64) { GMF(DT_Q8, 64) } else { GMF(DT_Q8, 128) } }
+        if (t64) { GMF(DT_Q4, 64) } else { GMF(DT_Q4, 128) }
 #undef GMF
     }
     dim3 grid((a.units + TM - 1) / TM, (a.n + TN - 1) / TN);

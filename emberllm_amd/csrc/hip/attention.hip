@@ -13,13 +13,16 @@
 // LDS among many rows, in three kernels per layer:
 //   k_pf_scores   s[h][b][t] = (sum over d in order of q*k) / sqrt(hd), one
 //                 lane per key, each lane carrying up to 8 (token, head)
-//                 rows of its kv group; K tile and Q rows staged in LDS
-//   k_pf_softmax  per row: max, e_t = expf(s_t - max) (in place), the sum
-//                 taken in t order by one lane per row, 1/sum
+//                 rows of its kv group; K tile and Q rows staged in LDS; also
+//                 the maximum of each row over the tile's 64 keys
+//   k_pf_rowsum   per row, one lane: max = the maximum of its tile maxima,
+//                 then the sum in t order of e_t = expf(s_t - max), and 1/sum
 //                 (model.c:57-64)
 //   k_pf_pv       o[b][h][d] = sum over t in order of (e_t * (1/sum)) * v_t[d],
+//                 e_t recomputed while staging (expf gives the same value),
 //                 one thread per (row set, d); V tile and probabilities
 //                 staged in LDS
+// The score rows are written once and read twice (the sum, then P.V).
 // Roofline: VALU-bound, 2 * hd multiply-adds per (head, token, key) pair,
 // each as a separately rounded multiply and add like the reference's
 // -ffp-contract=off build.
@@ -95,78 +98,75 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
                 acc[i][h] = s;
             }
     }
-    const int t = kt0 + lane;
+    const int t = kt0 + lane, ntl = attn_prefill_tiles(a.ldk);
 #pragma unroll
     for (int i = 0; i < QW; i++) {
-        const int b = b0 + wave * QW + i;
-        if (b >= a.n_tok || t > a.pos_base + b) continue;
+        const int b = b0 + wave * QW + i;   // uniform over the wave
+        const bool rowok = b < a.n_tok && kt0 <= a.pos_base + b;
+        const bool ok = rowok && t <= a.pos_base + b;
 #pragma unroll
-        for (int h = 0; h < GM; h++)
-            if (h < G) a.scores[((size_t)(g * G + h) * a.n_tok + b) * a.ldk + t] = acc[i][h] * a.inv_sqrt;
+        for (int h = 0; h < GM; h++) {
+            if (h >= G) continue;
+            const size_t row = (size_t)(g * G + h) * a.n_tok + b;
+            const float sv = acc[i][h] * a.inv_sqrt;
+            if (ok) a.scores[row * a.ldk + t] = sv;
+            const float mx = wave_max(ok ? sv : -INFINITY);
+            if (lane == 0 && rowok) a.tmax[row * ntl + blockIdx.x] = mx;
+        }
     }
 }
 
-// grid (n_heads * n_tok / 64 rounded up); 64 rows per workgroup.  Every
-// loop issues a batch of independent loads before using any of them.
+// grid (n_heads * n_tok / 64 rounded up) of one wave, one lane per row (rows
+// of a wave are consecutive tokens of one head, so their lengths differ by at
+// most 63).  The sum keeps the reference's order, one position at a time;
+// the loads run SM_B float4s ahead of the adds, double-buffered.
 constexpr int SM_B = 8;
-__global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nrows = a.n_heads * a.n_tok;
-    const int r0 = blockIdx.x * 64;
-    // 1. each wave: max and exponentials of 16 rows, lanes across positions
-    for (int k = 0; k < 16; k++) {
-        const int r = r0 + wave * 16 + k;
-        if (r >= nrows) break;
-        const int b = r % a.n_tok, len = a.pos_base + b + 1;
-        float *row = a.scores + (size_t)r * a.ldk;
-        float mx = -INFINITY;
-        for (int t0 = 0; t0 < len; t0 += 64 * SM_B) {
-            float v[SM_B];
+__global__ __launch_bounds__(64) void k_pf_rowsum(AttnArgs a) {
+    const int lane = threadIdx.x, nrows = a.n_heads * a.n_tok;
+    const int r = min((int)blockIdx.x * 64 + lane, nrows - 1);
+    const int b = r % a.n_tok, len = a.pos_base + b + 1;
+    const int ntl = attn_prefill_tiles(a.ldk), nt = (len + PF_KT - 1) / PF_KT;
+    const float4 *tm = reinterpret_cast<const float4 *>(a.tmax + (size_t)r * ntl);
+    float mx = -INFINITY;
+    for (int k = 0; k < nt; k += 16) {
+        float4 v[4];
 #pragma unroll
-            for (int i = 0; i < SM_B; i++) v[i] = row[min(t0 + lane + 64 * i, len - 1)];
+        for (int i = 0; i < 4; i++) v[i] = tm[min(k / 4 + i, ntl / 4 - 1)];
 #pragma unroll
-            for (int i = 0; i < SM_B; i++) mx = fmaxf(mx, v[i]);
-        }
-        mx = wave_max(mx);
-        for (int t0 = 0; t0 < len; t0 += 64 * SM_B) {
-            float v[SM_B];
-#pragma unroll
-            for (int i = 0; i < SM_B; i++) v[i] = row[min(t0 + lane + 64 * i, len - 1)];
-#pragma unroll
-            for (int i = 0; i < SM_B; i++)
-                if (t0 + lane + 64 * i < len) row[t0 + lane + 64 * i] = expf(v[i] - mx);
+        for (int i = 0; i < 4; i++) {
+            const int k0 = k + 4 * i;
+            if (k0 < nt) mx = fmaxf(mx, v[i].x);
+            if (k0 + 1 < nt) mx = fmaxf(mx, v[i].y);
+            if (k0 + 2 < nt) mx = fmaxf(mx, v[i].z);
+            if (k0 + 3 < nt) mx = fmaxf(mx, v[i].w);
         }
     }
-    __syncthreads();
-    // 2. one lane per row: the sum in position order, then 1/sum; batches of
-    // SM_B float4 double-buffered so the loads run ahead of the adds
-    if (wave == 0) {
-        const int r = min(r0 + lane, nrows - 1);
-        const int b = r % a.n_tok, len = a.pos_base + b + 1;
-        const float *row = a.scores + (size_t)r * a.ldk;
-        const int last4 = a.ldk - 4;   // loads stay inside the row
-        float4 cur[SM_B], nxt[SM_B];
+    const float *row = a.scores + (size_t)r * a.ldk;
+    const int last4 = a.ldk - 4;   // loads stay inside the row
+    float4 cur[SM_B], nxt[SM_B];
 #pragma unroll
-        for (int i = 0; i < SM_B; i++) cur[i] = *reinterpret_cast<const float4 *>(row + min(4 * i, last4));
-        float sum = 0.0f;
-        for (int t0 = 0; t0 < len; t0 += 4 * SM_B) {
-            if (t0 + 4 * SM_B < len) {
+    for (int i = 0; i < SM_B; i++) cur[i] = *reinterpret_cast<const float4 *>(row + min(4 * i, last4));
+    float sum = 0.0f;
+    for (int t0 = 0; t0 < len; t0 += 4 * SM_B) {
+        if (t0 + 4 * SM_B < len) {
 #pragma unroll
-                for (int i = 0; i < SM_B; i++)
-                    nxt[i] = *reinterpret_cast<const float4 *>(row + min(t0 + 4 * SM_B + 4 * i, last4));
-            }
-#pragma unroll
-            for (int i = 0; i < SM_B; i++) {
-                const int t = t0 + 4 * i;
-                if (t < len) sum = sum + cur[i].x;
-                if (t + 1 < len) sum = sum + cur[i].y;
-                if (t + 2 < len) sum = sum + cur[i].z;
-                if (t + 3 < len) sum = sum + cur[i].w;
-            }
-#pragma unroll
-            for (int i = 0; i < SM_B; i++) cur[i] = nxt[i];
+            for (int i = 0; i < SM_B; i++)
+                nxt[i] = *reinterpret_cast<const float4 *>(row + min(t0 + 4 * SM_B + 4 * i, last4));
         }
-        if (r0 + lane < nrows) a.rowinv[r] = 1.0f / sum;
+#pragma unroll
+        for (int i = 0; i < SM_B; i++) {
+            const int t = t0 + 4 * i;
+            if (t < len) sum = sum + expf(cur[i].x - mx);
+            if (t + 1 < len) sum = sum + expf(cur[i].y - mx);
+            if (t + 2 < len) sum = sum + expf(cur[i].z - mx);
+            if (t + 3 < len) sum = sum + expf(cur[i].w - mx);
+        }
+#pragma unroll
+        for (int i = 0; i < SM_B; i++) cur[i] = nxt[i];
+    }
+    if ((int)blockIdx.x * 64 + lane < nrows) {
+        a.rowmax[r] = mx;
+        a.rowinv[r] = 1.0f / sum;
     }
 }
 
@@ -218,13 +218,13 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
                 const size_t row = (size_t)(g * G + h) * a.n_tok + b;
                 const int len = a.pos_base + b + 1;
                 if (t0 + c < len) {
-                    const float inv = a.rowinv[row];
-                    const float4 e = *reinterpret_cast<const float4 *>(a.scores + row * a.ldk + t0 + c);
+                    const float inv = a.rowinv[row], mx = a.rowmax[row];
+                    const float4 sv = *reinterpret_cast<const float4 *>(a.scores + row * a.ldk + t0 + c);
                     const int t = t0 + c;
-                    p.x = e.x * inv;
-                    p.y = t + 1 < len ? e.y * inv : 0.0f;
-                    p.z = t + 2 < len ? e.z * inv : 0.0f;
-                    p.w = t + 3 < len ? e.w * inv : 0.0f;
+                    p.x = expf(sv.x - mx) * inv;
+                    p.y = t + 1 < len ? expf(sv.y - mx) * inv : 0.0f;
+                    p.z = t + 2 < len ? expf(sv.z - mx) * inv : 0.0f;
+                    p.w = t + 3 < len ? expf(sv.w - mx) * inv : 0.0f;
                 }
             }
             *reinterpret_cast<float4 *>(&ps[r * PF_KT + c]) = p;
@@ -254,6 +254,116 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
         const int b = b0 + r / GM, h = r % GM;
         if (r >= R || b >= a.n_tok || h >= G) continue;
         a.out[(size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + d] = acc[k];
+    }
+}
+
+// P.V for head_dim 64 / 128, register-blocked: thread (dg, rs) accumulates
+// dims 4*dg .. 4*dg+3 of the RPS rows rs*RPS .. of the workgroup's 64 rows
+// (QT = 64 / GM tokens x GM heads), so each position costs one V float4 and
+// RPS/4 probability float4 reads from LDS for 8 * RPS multiplies and adds.
+// V is staged row-major (vs[t][d]); probabilities position-major
+// (ps[t][row]), computed while staging as expf(s - max) * (1/sum); the next
+// tile's global loads are issued before the current tile's products.  Every
+// (row, dim) sums its positions in order, multiply and add rounded apart;
+// positions past a row's length carry probability 0 (see k_pf_pv).
+template <int HD, int GM, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
+    constexpr int RW = 64, QT = RW / GM, DG = HD / 4, RSETS = WG / DG, RPS = RW / RSETS;
+    constexpr int VLD = PF_KT * HD / 4 / WG;        // V float4 loads per thread per tile
+    constexpr int SLD = RW * PF_KT / 4 / WG;        // score float4 loads per thread per tile
+    constexpr int PP = RW + 4;                      // ps row pitch
+    static_assert(RW % RSETS == 0 && RPS % 4 == 0 && WG % DG == 0, "layout");
+    __shared__ __align__(16) float vs[PF_KT * HD];
+    __shared__ __align__(16) float ps[PF_KT * PP];
+    const int tid = threadIdx.x, dg = tid % DG, rs = tid / DG;
+    const int G = a.n_heads / a.n_kv, g = blockIdx.y;
+    const int b0 = blockIdx.x * QT;
+    if (b0 >= a.n_tok) return;
+    const int blast = min(a.n_tok, b0 + QT) - 1;
+    const int tmax = a.pos_base + blast;                  // last key any row here needs
+    const size_t hoff = (size_t)g * HD;
+    // the one score row this thread stages (row = tid % RW in every tile)
+    const int srow = tid % RW, sb = b0 + srow / GM, sh = srow % GM;
+    const bool sok = sb < a.n_tok && sh < G;
+    const size_t sgrow = sok ? (size_t)(g * G + sh) * a.n_tok + sb : 0;
+    const int slen = sok ? a.pos_base + sb + 1 : 0;
+    const float smx = sok ? a.rowmax[sgrow] : 0.0f, sinv = sok ? a.rowinv[sgrow] : 0.0f;
+    const float *srowp = a.scores + sgrow * a.ldk;
+    const int last4 = a.ldk - 4;
+
+    float4 vr[VLD], sr[SLD];
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < VLD; i++) {
+            const int f = tid + i * WG, t = f / DG, c = (f % DG) * 4;
+            const size_t off = (size_t)min(t0 + t, tmax) * a.kv_dim + hoff + c;
+            if (F16) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
+                vr[i] = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
+            } else {
+                vr[i] = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.vc) + off);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < SLD; i++) {
+            const int c4 = (tid + i * WG) / RW;
+            sr[i] = *reinterpret_cast<const float4 *>(srowp + min(t0 + 4 * c4, last4));
+        }
+    };
+    auto stage = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < VLD; i++) {
+            const int f = tid + i * WG;
+            *reinterpret_cast<float4 *>(&vs[(f / DG) * HD + (f % DG) * 4]) = vr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < SLD; i++) {   // p = e * (1/sum), model.c:62-63
+            const int c4 = (tid + i * WG) / RW, t = t0 + 4 * c4;
+            const float4 e = sr[i];
+            ps[(4 * c4 + 0) * PP + srow] = t < slen ? expf(e.x - smx) * sinv : 0.0f;
+            ps[(4 * c4 + 1) * PP + srow] = t + 1 < slen ? expf(e.y - smx) * sinv : 0.0f;
+            ps[(4 * c4 + 2) * PP + srow] = t + 2 < slen ? expf(e.z - smx) * sinv : 0.0f;
+            ps[(4 * c4 + 3) * PP + srow] = t + 3 < slen ? expf(e.w - smx) * sinv : 0.0f;
+        }
+    };
+
+    float acc[RPS][4];
+#pragma unroll
+    for (int k = 0; k < RPS; k++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[k][e] = 0.0f;
+    load(0);
+    for (int t0 = 0; t0 <= tmax; t0 += PF_KT) {
+        __syncthreads();                   // the previous tile's products are done
+        stage(t0);
+        __syncthreads();
+        if (t0 + PF_KT <= tmax) load(t0 + PF_KT);
+        const float *vp = &vs[dg * 4];
+        const float *pp = &ps[rs * RPS];
+#pragma unroll 4
+        for (int t = 0; t < PF_KT; t++) {
+            const float4 v = *reinterpret_cast<const float4 *>(vp + t * HD);
+            float p[RPS];
+#pragma unroll
+            for (int k = 0; k < RPS; k += 4) {
+                const float4 q = *reinterpret_cast<const float4 *>(pp + t * PP + k);
+                p[k] = q.x; p[k + 1] = q.y; p[k + 2] = q.z; p[k + 3] = q.w;
+            }
+#pragma unroll
+            for (int k = 0; k < RPS; k++) {   // positions in order, multiply and add rounded apart
+                acc[k][0] = acc[k][0] + p[k] * v.x;
+                acc[k][1] = acc[k][1] + p[k] * v.y;
+                acc[k][2] = acc[k][2] + p[k] * v.z;
+                acc[k][3] = acc[k][3] + p[k] * v.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < RPS; k++) {
+        const int r = rs * RPS + k, b = b0 + r / GM, h = r % GM;
+        if (b >= a.n_tok || h >= G) continue;
+        *reinterpret_cast<float4 *>(a.out + (size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + dg * 4) =
+            make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
     }
 }
 
@@ -316,8 +426,13 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
     const int ktiles = (a.pos_base + a.n_tok + PF_KT - 1) / PF_KT;
     const int qtiles = (a.n_tok + QT - 1) / QT;
     hipLaunchKernelGGL((k_pf_scores<HD, GM, F16>), dim3(ktiles, qtiles, a.n_kv), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(k_pf_softmax, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL((k_pf_pv<HD, GM, F16>), dim3(qtiles, a.n_kv), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(k_pf_rowsum, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(64), 0, st, a);
+    if constexpr (HD == 64 || HD == 128) {
+        constexpr int QT2 = 64 / GM;
+        hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16>), dim3((a.n_tok + QT2 - 1) / QT2, a.n_kv), dim3(WG), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((k_pf_pv<HD, GM, F16>), dim3(qtiles, a.n_kv), dim3(WG), 0, st, a);
+    }
 }
 
 template <int HD, bool F16>
@@ -332,7 +447,8 @@ static int pf_pick_g(hipStream_t st, const AttnArgs &a) {
 }
 
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a) {
-    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || !a.scores || !a.rowinv) return -1;
+    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || !a.scores || !a.tmax || !a.rowmax || !a.rowinv)
+        return -1;
     if (a.ldk < a.pos_base + a.n_tok || a.ldk % 4) return -1;
     switch (a.hd) {
         case 48: return f16kv ? pf_pick_g<48, true>(st, a) : pf_pick_g<48, false>(st, a);

@@ -265,7 +265,9 @@ struct EhipState {
     // prefill scratch
     float *X, *QKV, *O, *H, *xf, *dxp;
     int8_t *qx; int *xsum, *ids_d;
-    float *pf_scores, *pf_rowinv;   // prefill attention scratch [n_heads][pf_chunk][ldk], [n_heads][pf_chunk]
+    // prefill attention scratch: scores [n_heads][pf_chunk][ldk], tile maxima
+    // [n_heads][pf_chunk][attn_prefill_tiles(ldk)], row max and 1/sum [n_heads][pf_chunk]
+    float *pf_scores, *pf_tmax, *pf_rowmax, *pf_rowinv;
     int pf_chunk;       // tokens per prefill pass
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
@@ -415,6 +417,8 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->ids_d = (int *)salloc(s, 4 * pfc)) &&
               (s->pf_scores = (float *)salloc(s, 4 * pfc * ldk_max * c.n_heads)) &&
               (s->pf_rowinv = (float *)salloc(s, 4 * pfc * c.n_heads)) &&
+              (s->pf_rowmax = (float *)salloc(s, 4 * pfc * c.n_heads)) &&
+              (s->pf_tmax = (float *)salloc(s, 4 * pfc * c.n_heads * (size_t)attn_prefill_tiles((int)ldk_max))) &&
               (s->am_val = (float *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->am_idx = (int *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true)) &&
@@ -790,7 +794,8 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             rc |= launch_qkpost(s->st, s->f16kv, p);
             at.q = s->QKV; at.q_stride = stride; at.pos_base = start + c0; at.n_tok = mt;
             at.out = s->O;
-            at.scores = s->pf_scores; at.rowinv = s->pf_rowinv; at.ldk = attn_prefill_ldk(start + c0, mt);
+            at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
+            at.ldk = attn_prefill_ldk(start + c0, mt);
             rc |= launch_attention(s->st, s->f16kv, at);
             QuantRowsArgs q2{};
             q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;

@@ -66,14 +66,18 @@ struct AttnArgs {
     // xm_err: set nonzero by a workgroup that finds itself on another XCD.
     int *xm_cnt; const int *xm_xcc; int *xm_err;
     float *out;            // [n_tok][n_heads*hd]
-    // prefill scratch: scores, then probabilities, [n_heads][n_tok][ldk]
-    // (ldk >= pos_base + n_tok, a multiple of 4) and 1/sum per row [n_heads][n_tok]
-    float *scores, *rowinv;
+    // prefill scratch: scores [n_heads][n_tok][ldk] (ldk >= pos_base + n_tok,
+    // a multiple of 4); the maximum of each 64-key tile of a row,
+    // [n_heads][n_tok][attn_prefill_tiles(ldk)]; per row the maximum and
+    // 1/sum of the exponentials [n_heads][n_tok]
+    float *scores, *tmax, *rowmax, *rowinv;
     int ldk;
 };
 // prefill: q rows already normed and rotated, k/v already in the cache
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
 inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }
+// tile-maximum slots per prefill score row (64-key tiles, padded to 4)
+__host__ __device__ inline int attn_prefill_tiles(int ldk) { return ((ldk + 63) / 64 + 3) & ~3; }
 // decode (one token, fused QK-norm / RoPE / KV store) over a grid of
 // (n_kv, max_chunks) workgroups, max_chunks = attn_decode_chunks(...).
 // Without xm_cnt the merge is a second kernel; with_merge = false leaves it

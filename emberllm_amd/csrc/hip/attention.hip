@@ -15,8 +15,9 @@
 //                 lane per key, each lane carrying up to 8 (token, head)
 //                 rows of its kv group; K tile and Q rows staged in LDS; also
 //                 the maximum of each row over the tile's 64 keys
-//   k_pf_rowsum   per row, one lane: max = the maximum of its tile maxima,
-//                 then the sum in t order of e_t = expf(s_t - max), and 1/sum
+//   k_pf_rowsum   per row: max = the maximum of its tile maxima; the
+//                 exponentials e_t = expf(s_t - max) computed by the whole
+//                 workgroup, then added in t order by one lane per row; 1/sum
 //                 (model.c:57-64)
 //   k_pf_pv       o[b][h][d] = sum over t in order of (e_t * (1/sum)) * v_t[d],
 //                 e_t recomputed while staging (expf gives the same value),
@@ -116,57 +117,89 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
     }
 }
 
-// grid (n_heads * n_tok / 64 rounded up) of one wave, one lane per row (rows
-// of a wave are consecutive tokens of one head, so their lengths differ by at
-// most 63).  The sum keeps the reference's order, one position at a time;
-// the loads run SM_B float4s ahead of the adds, double-buffered.
-constexpr int SM_B = 8;
-__global__ __launch_bounds__(64) void k_pf_rowsum(AttnArgs a) {
-    const int lane = threadIdx.x, nrows = a.n_heads * a.n_tok;
-    const int r = min((int)blockIdx.x * 64 + lane, nrows - 1);
-    const int b = r % a.n_tok, len = a.pos_base + b + 1;
-    const int ntl = attn_prefill_tiles(a.ldk), nt = (len + PF_KT - 1) / PF_KT;
-    const float4 *tm = reinterpret_cast<const float4 *>(a.tmax + (size_t)r * ntl);
-    float mx = -INFINITY;
-    for (int k = 0; k < nt; k += 16) {
+// grid (n_heads * n_tok / 64 rounded up), 64 rows per workgroup (rows of one
+// head, consecutive tokens, so their lengths differ by at most 63).  The four
+// waves compute the exponentials of a 64-position tile of all 64 rows into
+// LDS (double-buffered); wave 0 then adds each row's tile in position order,
+// one lane per row, while the next tile is computed.  Positions past a row's
+// length contribute +0, which leaves the (positive) sum unchanged, so the sum
+// is the reference's sequential one.
+constexpr int RS_P = PF_KT + 4;   // es row pitch
+__global__ __launch_bounds__(WG) void k_pf_rowsum(AttnArgs a) {
+    __shared__ __align__(16) float es[2][64 * RS_P];
+    __shared__ float smx[64];
+    __shared__ int slen[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nrows = a.n_heads * a.n_tok, r0 = blockIdx.x * 64;
+    const int ntl = attn_prefill_tiles(a.ldk);
+    if (wave == 0) {   // row maximum = the maximum of the row's tile maxima
+        const int r = min(r0 + lane, nrows - 1);
+        const int b = r % a.n_tok, len = a.pos_base + b + 1, nt = (len + PF_KT - 1) / PF_KT;
+        const float4 *tm = reinterpret_cast<const float4 *>(a.tmax + (size_t)r * ntl);
+        float mx = -INFINITY;
+        for (int k = 0; k < nt; k += 16) {
+            float4 v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = tm[min(k / 4 + i, ntl / 4 - 1)];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int k0 = k + 4 * i;
+                if (k0 < nt) mx = fmaxf(mx, v[i].x);
+                if (k0 + 1 < nt) mx = fmaxf(mx, v[i].y);
+                if (k0 + 2 < nt) mx = fmaxf(mx, v[i].z);
+                if (k0 + 3 < nt) mx = fmaxf(mx, v[i].w);
+            }
+        }
+        smx[lane] = mx;
+        slen[lane] = r0 + lane < nrows ? len : 0;
+    }
+    __syncthreads();
+    int maxlen = 0;
+#pragma unroll 4
+    for (int i = 0; i < 64; i++) maxlen = max(maxlen, slen[i]);
+    const int nk = (maxlen + PF_KT - 1) / PF_KT;
+    // exponentials of tile k: thread -> row tid / 4, positions 16 * (tid % 4) ..
+    const int er = tid / 4, eseg = (tid % 4) * 16;
+    const float emx = smx[er];
+    const int elen = slen[er];
+    const float *erow = a.scores + (size_t)min(r0 + er, nrows - 1) * a.ldk;
+    const int last4 = a.ldk - 4;
+    auto stage = [&](int k, int buf) {
         float4 v[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = tm[min(k / 4 + i, ntl / 4 - 1)];
+        for (int i = 0; i < 4; i++) v[i] = *reinterpret_cast<const float4 *>(erow + min(k * PF_KT + eseg + 4 * i, last4));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int k0 = k + 4 * i;
-            if (k0 < nt) mx = fmaxf(mx, v[i].x);
-            if (k0 + 1 < nt) mx = fmaxf(mx, v[i].y);
-            if (k0 + 2 < nt) mx = fmaxf(mx, v[i].z);
-            if (k0 + 3 < nt) mx = fmaxf(mx, v[i].w);
+            const int t = k * PF_KT + eseg + 4 * i;
+            float4 e;
+            e.x = t < elen ? expf(v[i].x - emx) : 0.0f;
+            e.y = t + 1 < elen ? expf(v[i].y - emx) : 0.0f;
+            e.z = t + 2 < elen ? expf(v[i].z - emx) : 0.0f;
+            e.w = t + 3 < elen ? expf(v[i].w - emx) : 0.0f;
+            *reinterpret_cast<float4 *>(&es[buf][er * RS_P + eseg + 4 * i]) = e;
         }
-    }
-    const float *row = a.scores + (size_t)r * a.ldk;
-    const int last4 = a.ldk - 4;   // loads stay inside the row
-    float4 cur[SM_B], nxt[SM_B];
-#pragma unroll
-    for (int i = 0; i < SM_B; i++) cur[i] = *reinterpret_cast<const float4 *>(row + min(4 * i, last4));
+    };
     float sum = 0.0f;
-    for (int t0 = 0; t0 < len; t0 += 4 * SM_B) {
-        if (t0 + 4 * SM_B < len) {
-#pragma unroll
-            for (int i = 0; i < SM_B; i++)
-                nxt[i] = *reinterpret_cast<const float4 *>(row + min(t0 + 4 * SM_B + 4 * i, last4));
+    if (nk > 0) stage(0, 0);
+    __syncthreads();
+    for (int k = 0; k < nk; k++) {
+        if (k + 1 < nk) stage(k + 1, (k + 1) & 1);
+        if (wave == 0) {
+            const float *er0 = &es[k & 1][lane * RS_P];
+#pragma unroll 4
+            for (int j = 0; j < PF_KT; j += 4) {
+                const float4 e = *reinterpret_cast<const float4 *>(er0 + j);
+                sum = sum + e.x;
+                sum = sum + e.y;
+                sum = sum + e.z;
+                sum = sum + e.w;
+            }
         }
-#pragma unroll
-        for (int i = 0; i < SM_B; i++) {
-            const int t = t0 + 4 * i;
-            if (t < len) sum = sum + expf(cur[i].x - mx);
-            if (t + 1 < len) sum = sum + expf(cur[i].y - mx);
-            if (t + 2 < len) sum = sum + expf(cur[i].z - mx);
-            if (t + 3 < len) sum = sum + expf(cur[i].w - mx);
-        }
-#pragma unroll
-        for (int i = 0; i < SM_B; i++) cur[i] = nxt[i];
+        __syncthreads();
     }
-    if ((int)blockIdx.x * 64 + lane < nrows) {
-        a.rowmax[r] = mx;
-        a.rowinv[r] = 1.0f / sum;
+    if (wave == 0 && r0 + lane < nrows) {
+        a.rowmax[r0 + lane] = smx[lane];
+        a.rowinv[r0 + lane] = 1.0f / sum;
     }
 }
 
@@ -277,7 +310,11 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     __shared__ __align__(16) float ps[PF_KT * PP];
     const int tid = threadIdx.x, dg = tid % DG, rs = tid / DG;
     const int G = a.n_heads / a.n_kv, g = blockIdx.y;
-    const int b0 = blockIdx.x * QT;
+    // causal rows get longer with the token: the upper half of the kv groups
+    // takes the token tiles in reverse, so the two workgroups that share a CU
+    // (linear ids w and w + 256 with 8 kv groups) pair a long tile with a short one
+    const int xt = g >= (int)gridDim.y / 2 ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int b0 = xt * QT;
     if (b0 >= a.n_tok) return;
     const int blast = min(a.n_tok, b0 + QT) - 1;
     const int tmax = a.pos_base + blast;                  // last key any row here needs
@@ -426,7 +463,7 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
     const int ktiles = (a.pos_base + a.n_tok + PF_KT - 1) / PF_KT;
     const int qtiles = (a.n_tok + QT - 1) / QT;
     hipLaunchKernelGGL((k_pf_scores<HD, GM, F16>), dim3(ktiles, qtiles, a.n_kv), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(k_pf_rowsum, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(k_pf_rowsum, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(WG), 0, st, a);
     if constexpr (HD == 64 || HD == 128) {
         constexpr int QT2 = 64 / GM;
         hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16>), dim3((a.n_tok + QT2 - 1) / QT2, a.n_kv), dim3(WG), 0, st, a);

@@ -349,6 +349,12 @@ static int xm_probe(EhipState *s) {
     for (int g = 0; g < nkv && ok; g++)
         for (int y = 1; y < gy && ok; y++) ok = h[(size_t)y * nkv + g] == h[g];
     if (!ok) return 0;
+    // EHIP_XMERGE_TEST_SKEW=k records every kv head's XCD as k further on
+    // (test hook): each workgroup's own check then fails, so the error path
+    // can be exercised while the kernels run exactly as usual
+    const int skew = env_int("EHIP_XMERGE_TEST_SKEW", 0);
+    if (skew)
+        for (int g = 0; g < nkv; g++) h[g] = (h[g] + skew) & 7;
     HCHK(hipMemcpy(s->xm_xcc, h.data(), 4 * (size_t)nkv, hipMemcpyHostToDevice), -1);
     s->xm_on = true;
     return 0;

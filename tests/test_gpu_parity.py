@@ -335,3 +335,31 @@ def test_measured_read_bandwidth():
     with pytest.raises(RuntimeError):
         e.measure_read_bw(1024, 1)
     e.close()
+
+
+def test_xcd_check_reports_misplaced_workgroups(monkeypatch):
+    """The in-kernel merge relies on every workgroup of a kv head running on
+    the XCD the state's probe recorded; each workgroup checks that and raises
+    a flag the host turns into an error.  EHIP_XMERGE_TEST_SKEW records the
+    wrong XCDs (the kernels themselves run as usual), so the device loop must
+    fail with the placement error instead of returning tokens."""
+    monkeypatch.setenv("EHIP_XMERGE_TEST_SKEW", "3")
+    name = "qwen3_06b"
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    say("XCD placement check: forced mismatch")
+    eng = emberllm.Engine(path, ctx=64)
+    if not eng.decode_fusion() & 1:
+        eng.close()
+        pytest.skip("this GPU does not place a kv head's workgroups on one XCD; the merge runs as a second kernel")
+    ids = np.arange(8) * 97 % V
+    tok0 = int(np.argmax(eng.prefill(ids)))
+    with pytest.raises(RuntimeError, match="another XCD"):
+        eng.generate_greedy(tok0, len(ids), 4)
+    eng.close()
+    monkeypatch.delenv("EHIP_XMERGE_TEST_SKEW")
+    e2 = emberllm.Engine(path, ctx=64)   # without the skew the same loop runs
+    e2.prefill(ids)
+    toks, _ = e2.generate_greedy(tok0, len(ids), 4)
+    assert len(toks) == 4
+    e2.close()

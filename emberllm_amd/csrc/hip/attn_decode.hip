@@ -12,7 +12,9 @@
 // workgroups read whole cache rows.  Rows [0, pos] of each kv head are split
 // into equal chunks, one per workgroup of that head; with max_chunks =
 // ATT_DEC_WPC * #CUs / n_kv every CU streams the same share whatever the position (a CU
-// holding one more chunk than the others would set the kernel's length).  A
+// holding one more chunk than the others would set the kernel's length).
+// Chunks hold at least ATT_DEC_RMIN rows: at short contexts a few chunks
+// (and a short merge) beat many chunks of two or three rows.  A
 // workgroup serves all kv_mul query heads of its kv head from the same K/V
 // rows, so each cache row is read once per step.  Lane (rw, j) of a wave holds
 // 16-byte piece j of row rw of each wave load:
@@ -138,8 +140,9 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     const int G = a.n_heads / a.n_kv;
     const int pos = a.tokpos[1];
     // rows [0, pos] split into equal chunks over the grid's max_chunks
-    // workgroups of this kv head (two per CU over all kv heads)
-    const int R = (pos + 1 + a.max_chunks - 1) / a.max_chunks;
+    // workgroups of this kv head (two per CU over all kv heads), at least
+    // ATT_DEC_RMIN rows each
+    const int R = dec_chunk_rows(pos, a.max_chunks);
     const int nc = (pos + 1 + R - 1) / R;
     if (c >= nc) return;
     const int t0 = c * R, t1 = min(pos + 1, t0 + R);
@@ -459,7 +462,7 @@ __global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a) {
     __shared__ float red[NWAVE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
     const int pos = a.tokpos[1];
-    const int R = (pos + 1 + a.max_chunks - 1) / a.max_chunks;
+    const int R = dec_chunk_rows(pos, a.max_chunks);
     const int nc = (pos + 1 + R - 1) / R;
     if (nc == 1) return;   // the attention kernel wrote the output
     float2 *sml = reinterpret_cast<float2 *>(dyn);

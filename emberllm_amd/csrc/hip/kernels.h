@@ -90,6 +90,14 @@ constexpr int ATT_DEC_NL = 5;       // K and V pieces per thread per batch in th
 constexpr int ATT_DEC_NW = 4;       // waves per decode attention workgroup
 constexpr int ATT_DEC_WPC = 2;      // decode attention workgroups per CU
 constexpr int ATT_DEC_CR = 160;     // positions per decode attention workgroup before more are added
+constexpr int ATT_DEC_RMIN = 32;    // positions per decode attention chunk at least (short contexts)
+// rows per chunk of the decode attention at position pos: (pos + 1) spread
+// over the grid's max_chunks workgroups of a kv head, but at least
+// ATT_DEC_RMIN, so short contexts use a few chunks and a short merge
+__host__ __device__ inline int dec_chunk_rows(int pos, int max_chunks) {
+    const int r = (pos + 1 + max_chunks - 1) / max_chunks;
+    return r > ATT_DEC_RMIN ? r : ATT_DEC_RMIN;
+}
 constexpr int XM_CNT_STRIDE = 32;   // ints between arrival counters (one 128-byte line each)
 // out[y * gx + x] = the XCD that workgroup (x, y) of a (gx, gy) grid ran on
 int launch_xcc_probe(hipStream_t st, int gx, int gy, int *out);

@@ -348,17 +348,17 @@ def test_xcd_check_reports_misplaced_workgroups(monkeypatch):
     path = configs.model_path(name, threads=16)
     V = configs.ALL[name]["vocab_size"]
     say("XCD placement check: forced mismatch")
-    eng = emberllm.Engine(path, ctx=64)
+    eng = emberllm.Engine(path, ctx=160)
     if not eng.decode_fusion() & 1:
         eng.close()
         pytest.skip("this GPU does not place a kv head's workgroups on one XCD; the merge runs as a second kernel")
-    ids = np.arange(8) * 97 % V
+    ids = np.arange(100) * 97 % V   # several chunks per kv head, so the merge (and its check) runs
     tok0 = int(np.argmax(eng.prefill(ids)))
     with pytest.raises(RuntimeError, match="another XCD"):
         eng.generate_greedy(tok0, len(ids), 4)
     eng.close()
     monkeypatch.delenv("EHIP_XMERGE_TEST_SKEW")
-    e2 = emberllm.Engine(path, ctx=64)   # without the skew the same loop runs
+    e2 = emberllm.Engine(path, ctx=160)   # without the skew the same loop runs
     e2.prefill(ids)
     toks, _ = e2.generate_greedy(tok0, len(ids), 4)
     assert len(toks) == 4

@@ -138,23 +138,16 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = blockIdx.x, c = blockIdx.y;   // kv heads vary fastest: neighbours read whole cache rows
     const int G = a.n_heads / a.n_kv;
-    const int pos = a.tokpos[1];
-    // rows [0, pos] split into equal chunks over the grid's max_chunks
-    // workgroups of this kv head (two per CU over all kv heads), at least
-    // ATT_DEC_RMIN rows each
-    const int R = dec_chunk_rows(pos, a.max_chunks);
-    const int nc = (pos + 1 + R - 1) / R;
-    if (c >= nc) return;
-    const int t0 = c * R, t1 = min(pos + 1, t0 + R);
     const int xcc_want = XM ? a.xm_xcc[g] : 0;
     const int j = lane % LPR, rw = lane / LPR;
     const bool pj = j < P;
     const int jc = pj ? j : P - 1;   // clamped piece index for loads
     const int qd = a.n_heads * HD;
     const size_t hoff = (size_t)g * HD;
-    const bool neox = a.rope_style == ROPE_NEOX;
-
-    // ---- 1. loads --------------------------------------------------------
+    // ---- 1. loads: the token's q heads / k / v pieces and the QK-norm
+    // weights first (they do not depend on the position, so their round trip
+    // overlaps the one that reads it), then the position-dependent RoPE row
+    // and the first K/V batch ------------------------------------------------
     float qv[GM][PE], kn[PE], vn[PE], qw[PE], kw[PE];
     float2 cs[PE];
 #pragma unroll
@@ -166,6 +159,16 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
         load_floats<PE>(qw, a.q_norm + jc * PE);
         load_floats<PE>(kw, a.k_norm + jc * PE);
     }
+    const int pos = a.tokpos[1];
+    // rows [0, pos] split into equal chunks over the grid's max_chunks
+    // workgroups of this kv head (two per CU over all kv heads), at least
+    // ATT_DEC_RMIN rows each
+    const int R = dec_chunk_rows(pos, a.max_chunks);
+    const int nc = (pos + 1 + R - 1) / R;
+    if (c >= nc) return;
+    const int t0 = c * R, t1 = min(pos + 1, t0 + R);
+    const bool neox = a.rope_style == ROPE_NEOX;
+
     {
         const float2 *rp = a.rope + (size_t)pos * (HD / 2);
         const int i0 = neox ? (jc % (P / 2)) * PE : jc * (PE / 2);

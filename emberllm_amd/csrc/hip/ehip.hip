@@ -276,7 +276,7 @@ struct EhipState {
     // device sampler: xorshift64* state, history ring, candidates; the
     // sampling decode graph is captured for one parameter set
     unsigned long long *smp_rng; int *smp_meta, *smp_hist; int smp_hist_cap;
-    float *smp_pmax, *smp_psum, *smp_cval; int *smp_cidx;
+    float *smp_psum, *smp_cval; int *smp_cidx, *smp_cnt;
     StepGraph smp[2];   // device sampling loop: 1 step, GEN_UNROLL steps
     SampleParams smp_graph_p; int smp_graph_cap;
     hipEvent_t ev0, ev1;
@@ -430,7 +430,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true)) &&
               (s->smp_rng = (unsigned long long *)salloc(s, 8)) &&
               (s->smp_meta = (int *)salloc(s, 8, true)) &&
-              (s->smp_pmax = (float *)salloc(s, 4 * SAMPLE_GRID)) &&
+              (s->smp_cnt = (int *)salloc(s, 4 * 2 * SAMPLE_GRID, true)) &&
               (s->smp_psum = (float *)salloc(s, 4 * SAMPLE_GRID)) &&
               (s->smp_cval = (float *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX)) &&
               (s->smp_cidx = (int *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX));
@@ -707,7 +707,7 @@ static SampleArgs sample_args(EhipState *s, const SampleParams &p, int cap, int 
     SampleArgs a{};
     a.logits = s->logits_d; a.n = n; a.p = p;
     a.rng = s->smp_rng; a.hist = cap > 0 ? s->smp_hist : nullptr; a.hist_meta = s->smp_meta; a.hist_cap = cap;
-    a.pmax = s->smp_pmax; a.psum = s->smp_psum; a.cval = s->smp_cval; a.cidx = s->smp_cidx;
+    a.psum = s->smp_psum; a.scnt = s->smp_cnt; a.cval = s->smp_cval; a.cidx = s->smp_cidx;
     a.am_val = s->am_val; a.am_idx = s->am_idx;
     a.tokpos = s->tokpos_d; a.out = s->gen_tok; a.cap = s->ctx;
     return a;
@@ -746,9 +746,22 @@ extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, Embe
     s->tokpos_h[3] = 0;
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
     HCHK(hipStreamSynchronize(s->st), -1);
+    SampleArgs sa = sample_args(s, p, cap, V);
+    // the lm_head's per-workgroup winners serve as the sampler's per-part
+    // maxima unless penalties change the logits afterwards
+    const bool parts = p.temperature > 0.0f && !sample_penalized(sa) && s->m->head.dtype != DT_F32;
     auto enq = [&]() -> int {
-        if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
-        if (launch_sample(s->st, sample_args(s, p, cap, V))) { set_err("sampler launch failed"); return -1; }
+        if (parts) {
+            if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
+            MatvecArgs h = head_args(s, s->x);
+            h.am_val = s->am_val; h.am_idx = s->am_idx;
+            sa.nparts = launch_matvec_parts(s->st, PRO_NORM, h);
+            if (sa.nparts <= 0) { set_err("lm_head launch failed"); return -1; }
+        } else if (enq_decode(s)) {
+            set_err("a decode kernel could not be launched for this shape");
+            return -1;
+        }
+        if (launch_sample(s->st, sa)) { set_err("sampler launch failed"); return -1; }
         return 0;
     };
     if (!same_params(p, s->smp_graph_p) || cap != s->smp_graph_cap) {   // graphs hold the parameters

@@ -37,6 +37,9 @@ struct MatvecArgs {
 };
 constexpr int MATVEC_MAX_GRID = 2048;
 int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
+// EPI_STORE with am_val/am_idx set and no merge: returns the number of
+// per-workgroup winners written (the sampler's per-part maxima), or -1.
+int launch_matvec_parts(hipStream_t st, int pro, const MatvecArgs &a);
 
 // ------------------------------------------------------------- attention --
 // GQA attention against the cache.  Prefill: causal attention of n_tok query
@@ -173,11 +176,16 @@ struct SampleArgs {
     unsigned long long *rng;         // device xorshift64* state
     int *hist, *hist_meta;           // ring [hist_cap]; {hist_len, hist_pos}
     int hist_cap;
-    float *pmax, *psum;              // [SAMPLE_GRID]
-    float *cval; int *cidx;          // [SAMPLE_GRID][SAMPLE_TOPK_MAX] candidates
-    float *am_val; int *am_idx;      // argmax partials (greedy)
+    float *psum;                     // [SAMPLE_GRID] slice sums of e
+    int *scnt;                       // [SAMPLE_GRID] tokens per slice, then the arrival counter (zeroed)
+    float *cval; int *cidx;          // [SAMPLE_GRID][SAMPLE_TOPK_MAX] tokens passed on
+    float *am_val; int *am_idx;      // per-part maxima (the greedy winners)
+    int nparts;                      // > 0: am_val already holds that many for these logits
     int *tokpos; int *out; int cap;  // as ArgmaxArgs
 };
 int launch_sample(hipStream_t st, const SampleArgs &a);
+// Whether launch_sample applies penalties (which change the logits after the
+// per-part maxima were taken).
+bool sample_penalized(const SampleArgs &a);
 
 }  // namespace ehip

@@ -419,4 +419,12 @@ int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a) {
     return 0;
 }
 
+int launch_matvec_parts(hipStream_t st, int pro, const MatvecArgs &a) {
+    const int K = a.W.cols;
+    if (K % QB != 0 || K <= 0 || a.units <= 0 || !a.am_val || a.W.dtype == DT_F32) return -1;
+    if (pro == PRO_NORM) return pick_dt<PRO_NORM, EPI_STORE>(st, a);
+    if (pro == PRO_EMBED_NORM) return pick_dt<PRO_EMBED_NORM, EPI_STORE>(st, a);
+    return -1;
+}
+
 }  // namespace ehip

@@ -118,6 +118,23 @@ int launch_argmax(hipStream_t st, const ArgmaxArgs &a) {
 // of index order, so a probability can differ from the reference's in its
 // last bit; a draw could then differ only when it lands within that of a
 // cumulative boundary.
+//
+// After the logits (and the penalties), one kernel of SAMPLE_GRID workgroups,
+// one slice of the vocabulary each (k_samp_fused):
+//   1. M = max logit / T, from per-part maxima that come with the logits (the
+//      lm_head's per-workgroup winners, or k_argmax_part's); e = expf(l/T - M)
+//      over the slice and the slice's sum of e in a fixed order;
+//   2. a bound e_lo from K = min(n, top_k) distinct tokens (the K largest of
+//      128 group maxima of those winners) that every token among the first K
+//      of the final order reaches (samp_bound); the slice passes on only its
+//      tokens with e >= e_lo, typically a few, at most SAMP_CAP;
+//   3. the last workgroup to arrive (an arrival counter) forms S = the sum of
+//      the slice sums in a fixed tree order, p = e / S for the passed tokens,
+//      ranks them by (p desc, index asc) — by counting when there are at
+//      most WG of them, else with a bitonic network — and draws.  If a slice
+//      had more than SAMP_CAP tokens to pass (flat or degenerate logits), it
+//      streams the whole vocabulary through the network instead, keeping the
+//      running first 64: exact, and slower.
 
 // penalties (sample.c:76-96).  Each token's updates depend only on its own
 // occurrences, so the lane holding a token's first occurrence in history
@@ -145,6 +162,12 @@ __global__ __launch_bounds__(WG) void k_samp_pen(SampleArgs a) {
 }
 
 constexpr int SAMP_E = SAMPLE_SLICE_MAX / WG;   // slice elements per thread
+constexpr int SAMP_CAP = 4 * WG / SAMPLE_GRID;   // tokens a slice may pass on
+constexpr int SAMP_PARTS = 8;                    // per-part maxima per thread
+static_assert(SAMPLE_GRID % 64 == 0 && SAMPLE_GRID <= WG, "one thread per slice in the final workgroup");
+static_assert(SAMP_CAP % 4 == 0 && SAMP_CAP <= SAMPLE_TOPK_MAX && SAMPLE_GRID * SAMP_CAP == 4 * WG,
+              "passed-on slots: 4 per thread");
+static_assert(MATVEC_MAX_GRID <= SAMP_PARTS * WG && ARGMAX_MAX_BLOCKS <= SAMP_PARTS * WG, "per-part maxima");
 
 __device__ __forceinline__ void samp_slice(int n, int &lo, int &hi) {
     const int per = (n + SAMPLE_GRID - 1) / SAMPLE_GRID;
@@ -152,330 +175,388 @@ __device__ __forceinline__ void samp_slice(int n, int &lo, int &hi) {
     hi = min(n, lo + per);
 }
 
-// logits /= T, slice maximum.  Every load is issued before the first use.
-__global__ __launch_bounds__(WG) void k_samp_a(SampleArgs a) {
-    __shared__ float red[NWAVE];
-    int lo, hi;
-    samp_slice(a.n, lo, hi);
-    float l[SAMP_E];
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        const int i = lo + (int)threadIdx.x + k * WG;
-        l[k] = i < hi ? a.logits[i] : 0.0f;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        const int i = lo + (int)threadIdx.x + k * WG;
-        if (i < hi) {
-            const float v = l[k] / a.p.temperature;
-            a.logits[i] = v;
-            mx = fmaxf(mx, v);
-        }
-    }
-    mx = wave_max(mx);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float m = red[0];
-        for (int w = 1; w < NWAVE; w++) m = fmaxf(m, red[w]);
-        a.pmax[blockIdx.x] = m;
-    }
-}
-
-// e = expf(l - max) in place, slice sum
-__global__ __launch_bounds__(WG) void k_samp_b(SampleArgs a) {
-    __shared__ float red[NWAVE];
-    int lo, hi;
-    samp_slice(a.n, lo, hi);
-    float l[SAMP_E];
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        const int i = lo + (int)threadIdx.x + k * WG;
-        l[k] = i < hi ? a.logits[i] : 0.0f;
-    }
-    float M = -INFINITY;
-    for (int w = 0; w < SAMPLE_GRID; w++) M = fmaxf(M, a.pmax[w]);
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        const int i = lo + (int)threadIdx.x + k * WG;
-        if (i < hi) {
-            const float e = expf(l[k] - M);
-            a.logits[i] = e;
-            s += e;
-        }
-    }
-    const float t = block_sum(s, red);
-    if (threadIdx.x == 0) a.psum[blockIdx.x] = t;
-}
+// e of a logit: the reference's division by the temperature, then expf of the
+// difference to the maximum (sample.c:129-134).
+__device__ __forceinline__ float samp_e(float l, float T, float M) { return expf(l / T - M); }
 
 // (p desc, index asc): the order of the reference's stable sort
 __device__ __forceinline__ bool samp_before(float pa, int ia, float pb, int ib) {
     return pa > pb || (pa == pb && ia < ib);
 }
 
-// Unsigned key with the order of the float (for the non-NaN values here).
-__device__ __forceinline__ unsigned samp_key(float p) {
-    const unsigned b = __float_as_uint(p);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-struct SelLds {
-    alignas(16) unsigned hist[512];
-    int cnt[SAMP_E * NWAVE];
-    int sel[3];
-};
-
-// Radix selection of the K-th largest key among the valid ones (1 <= K <=
-// their count), from the top in digits of 9 (sign and exponent), 8, 8 and 7
-// bits, stopping once the bin holding the K-th key is taken whole.  On
-// return the keys with (key & M) > P are taken (K - R of them) and R of the
-// C keys with (key & M) == P complete the K: all of them when C == R, else
-// (M == ~0, exactly equal keys) the first R in index order.
-__device__ __forceinline__ void radix_select(const unsigned (&key)[SAMP_E], const bool (&val)[SAMP_E], int K,
-                                             SelLds &s, unsigned &P, unsigned &M, int &R, int &C) {
-    P = 0; M = 0; R = K; C = 0;
-#pragma unroll 1
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = pass == 0 ? 23 : pass == 1 ? 15 : pass == 2 ? 7 : 0;
-        const int bits = pass == 0 ? 9 : pass == 3 ? 7 : 8;
-        const unsigned dmask = (1u << bits) - 1u;
-        s.hist[threadIdx.x] = 0;
-        s.hist[threadIdx.x + WG] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < SAMP_E; k++)
-            if (val[k] && (key[k] & M) == P) atomicAdd(&s.hist[(key[k] >> shift) & dmask], 1u);
-        __syncthreads();
-        if (threadIdx.x < 64) {
-            // lane l holds bins 8l..8l+7; find the bin where the count from the top reaches R
-            const int l = threadIdx.x;
-            const uint4 h0 = reinterpret_cast<const uint4 *>(s.hist)[2 * l];
-            const uint4 h1 = reinterpret_cast<const uint4 *>(s.hist)[2 * l + 1];
-            const unsigned hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-            unsigned own = 0;
-#pragma unroll
-            for (int b = 0; b < 8; b++) own += hb[b];
-            unsigned suf = own;   // count in lanes >= l
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const unsigned t = __shfl_down(suf, off);
-                if (l + off < 64) suf += t;
-            }
-            const unsigned r = (unsigned)R;
-            unsigned c = suf - own;   // count above this lane's bins
-            if (c < r && r <= suf) {
-                int sb = 0;
-                unsigned sc = 0, sh = 0;
-                bool found = false;
-#pragma unroll
-                for (int b = 7; b >= 0; b--) {
-                    if (!found && c + hb[b] >= r) { found = true; sb = b; sc = c; sh = hb[b]; }
-                    c += hb[b];
-                }
-                s.sel[0] = 8 * l + sb;
-                s.sel[1] = (int)sc;
-                s.sel[2] = (int)sh;
-            }
-        }
-        __syncthreads();
-        P |= (unsigned)s.sel[0] << shift;
-        M |= dmask << shift;
-        R -= s.sel[1];
-        C = s.sel[2];
-        if (C == R) break;   // the whole bin is taken: no further digits needed
-    }
-}
-
-// Rank of each flagged element among the flagged ones in index order, where
-// thread t holds elements t + k*WG (k = 0..SAMP_E-1); *total gets their count.
-__device__ __forceinline__ void block_rank(const bool (&f)[SAMP_E], int (&rank)[SAMP_E], int &total, SelLds &s) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const unsigned long long below = (1ull << lane) - 1ull;
-    __syncthreads();   // s.cnt may still be read by a previous call
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        const unsigned long long b = __ballot(f[k]);
-        rank[k] = __popcll(b & below);
-        if (lane == 0) s.cnt[k * NWAVE + w] = __popcll(b);
-    }
-    __syncthreads();
-    int base = 0;
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        int row = 0, pre = 0;
-#pragma unroll
-        for (int v = 0; v < NWAVE; v++) {
-            const int c = s.cnt[k * NWAVE + v];
-            pre += v < w ? c : 0;
-            row += c;
-        }
-        rank[k] += base + pre;
-        base += row;
-    }
-    total = base;
-}
-
-// Which of the held elements belong to the first K in samp_before order
-// (keys from samp_key, distinct indices increasing with position).
-__device__ __forceinline__ void samp_top(const unsigned (&key)[SAMP_E], const bool (&val)[SAMP_E], int K,
-                                         bool (&take)[SAMP_E], SelLds &s) {
-    unsigned P, M;
-    int R, C;
-    radix_select(key, val, K, s, P, M, R, C);
-    bool tie[SAMP_E];
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        take[k] = val[k] && (key[k] & M) > P;
-        tie[k] = val[k] && (key[k] & M) == P;
-    }
-    if (C == R) {
-#pragma unroll
-        for (int k = 0; k < SAMP_E; k++) take[k] = take[k] || tie[k];
-    } else {   // equal probabilities: the smaller indices come first
-        int rk[SAMP_E], nt;
-        block_rank(tie, rk, nt, s);
-#pragma unroll
-        for (int k = 0; k < SAMP_E; k++) take[k] = take[k] || (tie[k] && rk[k] < R);
-    }
-}
-
-// p = e / sum; the slice's first SAMPLE_TOPK_MAX candidates in samp_before
-// order, written in index order (which k_samp_d's tie ranking relies on).
-__global__ __launch_bounds__(WG) void k_samp_c(SampleArgs a) {
-    __shared__ SelLds s;
-    __shared__ float S;
-    int lo, hi;
-    samp_slice(a.n, lo, hi);
-    float e[SAMP_E];
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        const int i = lo + (int)threadIdx.x + k * WG;
-        e[k] = i < hi ? a.logits[i] : 0.0f;
-    }
-    if (threadIdx.x == 0) {
-        float t = 0.0f;
-        for (int w = 0; w < SAMPLE_GRID; w++) t += a.psum[w];
-        S = t;
-    }
-    __syncthreads();
-    float p[SAMP_E];
-    unsigned key[SAMP_E];
-    bool val[SAMP_E], take[SAMP_E];
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        val[k] = lo + (int)threadIdx.x + k * WG < hi;
-        p[k] = e[k] / S;
-        key[k] = samp_key(p[k]);
-        take[k] = false;
-    }
-    const int K = min(hi - lo, SAMPLE_TOPK_MAX);
-    if (K > 0) samp_top(key, val, K, take, s);
-    int pos[SAMP_E], nt;
-    block_rank(take, pos, nt, s);
-    float *cv = a.cval + blockIdx.x * SAMPLE_TOPK_MAX;
-    int *ci = a.cidx + blockIdx.x * SAMPLE_TOPK_MAX;
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++)
-        if (take[k] && pos[k] < SAMPLE_TOPK_MAX) {
-            cv[pos[k]] = p[k];
-            ci[pos[k]] = lo + (int)threadIdx.x + k * WG;
-        }
-    for (int j = nt + (int)threadIdx.x; j < SAMPLE_TOPK_MAX; j += WG) { cv[j] = -1.0f; ci[j] = INT_MAX; }
-}
-
-__device__ __forceinline__ void samp_emit(const SampleArgs &a, int tok) {
-    if (a.hist && a.hist_cap > 0) {   // ember_sampler_accept
-        const int pos = a.hist_meta[1];
-        a.hist[pos] = tok;
-        a.hist_meta[1] = (pos + 1) % a.hist_cap;
-        if (a.hist_meta[0] < a.hist_cap) a.hist_meta[0] += 1;
-    }
-    a.tokpos[0] = tok;
-    a.tokpos[1] += 1;
-    const int k = a.tokpos[2];
-    if (k < a.cap) a.out[k] = tok;
-    a.tokpos[2] = k + 1;
+// 64-bit key whose unsigned order is samp_before's for p >= 0 (p = e / S,
+// never negative): p's bits above, the complement of the index below.
+__device__ __forceinline__ unsigned long long samp_key(float p, int ix) {
+    return ((unsigned long long)__float_as_uint(p) << 32) | (unsigned)~ix;
 }
 
 __device__ __forceinline__ float lane_f(float v, int i) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
 
-// The first min(n, top_k) of all candidates, then top-k / min-p / top-p and
-// the draw (sample.c:136-175).  Candidate position order is index order.
-// The final 64 are sorted by one wave (bitonic network over lanes); the
-// cumulative sums are taken sequentially in sorted order as the reference's
-// loops take them.
-__global__ __launch_bounds__(WG) void k_samp_d(SampleArgs a) {
-    constexpr int NC = SAMPLE_GRID * SAMPLE_TOPK_MAX;
-    static_assert(NC == SAMP_E * WG, "candidate count");
-    __shared__ SelLds s;
-    __shared__ float tp[SAMPLE_TOPK_MAX];
-    __shared__ int ti[SAMPLE_TOPK_MAX];
-    float p[SAMP_E];
-    int id[SAMP_E];
-    unsigned key[SAMP_E];
-    bool val[SAMP_E], take[SAMP_E];
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        p[k] = a.cval[threadIdx.x + k * WG];
-        id[k] = a.cidx[threadIdx.x + k * WG];
-    }
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++) {
-        val[k] = id[k] >= 0 && id[k] < a.n;
-        key[k] = samp_key(p[k]);
-    }
-    const int K = min(a.n, a.p.top_k);   // 1..SAMPLE_TOPK_MAX, checked at launch
-    samp_top(key, val, K, take, s);
-    int pos[SAMP_E], nt;
-    block_rank(take, pos, nt, s);
-#pragma unroll
-    for (int k = 0; k < SAMP_E; k++)
-        if (take[k] && pos[k] < SAMPLE_TOPK_MAX) { tp[pos[k]] = p[k]; ti[pos[k]] = id[k]; }
-    for (int j = nt + (int)threadIdx.x; j < SAMPLE_TOPK_MAX; j += WG) { tp[j] = -1.0f; ti[j] = INT_MAX; }
+// Why e_lo bounds the first K.  Let C be K distinct tokens and eps the least
+// e among them.  p = fl(e / S) is monotone in e, so at least K tokens have
+// p >= fl(eps / S): the K-th largest p is >= fl(eps / S), and so is the p of
+// every token x among the first K.  Either e_x >= eps, or fl(e_x / S) ==
+// fl(eps / S), i.e. e_x / S and eps / S round to the same float: then
+// eps - e_x <= S ulp(fl(eps / S)) < eps 2^-22 + S 2^-149, with S <= n <= 2^18
+// (every e <= 1).  e_lo = eps - eps 2^-20 - 2^-128 lies below both cases.
+// C is the K largest (in e) of the 128 group maxima, group j holding the
+// per-part maxima j, j + 128, ...: distinct parts, distinct tokens.  A part
+// with no finite winner contributes -inf (e = 0), which only lowers eps.
+// eps, the K-th largest of the 128 e values, is the largest e that at least
+// K of them reach.  Thread t < 128 holds group t's e.  Every thread returns
+// e_lo (0 when NaNs leave no such e).
+__device__ __forceinline__ float samp_bound(float g, int K, float T, float M, float *ge, float *red) {
+    const int t = threadIdx.x;
+    const float e = samp_e(g, T, M);
+    if (t < 128) ge[t] = e;
     __syncthreads();
-    if (threadIdx.x >= 64) return;
-    const int lane = threadIdx.x;
-    float v = tp[lane];
-    int ix = ti[lane];
+    float x = 0.0f;
+    if (t < 128) {
+        int cnt = 0;
 #pragma unroll
-    for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const float pv = __shfl_xor(v, j);
-            const int pi = __shfl_xor(ix, j);
-            const bool want_first = ((lane & j) == 0) == ((lane & k) == 0);
-            if (want_first ? samp_before(pv, pi, v, ix) : samp_before(v, ix, pv, pi)) { v = pv; ix = pi; }
+        for (int q = 0; q < 128; q += 4) {
+            const float4 o = *reinterpret_cast<const float4 *>(ge + q);
+            cnt += (o.x >= e ? 1 : 0) + (o.y >= e ? 1 : 0) + (o.z >= e ? 1 : 0) + (o.w >= e ? 1 : 0);
         }
-    int m = min(nt, K);
+        x = cnt >= K ? e : 0.0f;
+    }
+    x = wave_max(x);
+    if ((t & 63) == 0) red[t >> 6] = x;
+    __syncthreads();
+    x = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    return x - x * 0x1p-20f - 0x1p-128f;
+}
+
+// One compare-exchange of the bitonic network at position e (partner e ^ j):
+// keep the earlier of the pair in samp_before order where the k-block runs
+// forward and e is the lower position, or runs backward and e is the upper.
+__device__ __forceinline__ void bit_cx(float &v, int &ix, float pv, int pi, int e, int j, int k) {
+    const bool first = ((e & j) == 0) == ((e & k) == 0);
+    if (first ? samp_before(pv, pi, v, ix) : samp_before(v, ix, pv, pi)) { v = pv; ix = pi; }
+}
+
+// The in-thread stage j = J of the network: pairs (i, i | J) with (i & J) == 0.
+template <int PER, int J>
+__device__ __forceinline__ void bit_local(float (&v)[PER], int (&ix)[PER], int k) {
+    if constexpr (J < PER) {
+        const int e0 = PER * (int)threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            if (i & J) continue;
+            const float va = v[i], vb = v[i | J];
+            const int ia = ix[i], ib = ix[i | J];
+            bit_cx(v[i], ix[i], vb, ib, e0 + i, J, k);
+            bit_cx(v[i | J], ix[i | J], va, ia, e0 + (i | J), J, k);
+        }
+    }
+}
+
+// Sorts the PER * WG (p, index) pairs held by the workgroup, pair PER*t + i in
+// thread t, into samp_before order.  Partners in the same thread exchange in
+// registers, in the same wave through lane shuffles, otherwise through LDS
+// (lp, li: PER * WG entries).  The network is fixed: NaNs cannot stall it.
+template <int PER>
+__device__ __forceinline__ void bitonic_sort(float (&v)[PER], int (&ix)[PER], float *lp, int *li) {
+    constexpr int N = PER * WG;
+    const int t = threadIdx.x;
+#pragma unroll 1
+    for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll 1
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j < PER) {
+                if (j == 1) bit_local<PER, 1>(v, ix, k);
+                else bit_local<PER, 2>(v, ix, k);
+            } else if (j < 64 * PER) {
+                const int lm = j / PER;
+#pragma unroll
+                for (int i = 0; i < PER; i++) {
+                    const float pv = __shfl_xor(v[i], lm);
+                    const int pi = __shfl_xor(ix[i], lm);
+                    bit_cx(v[i], ix[i], pv, pi, PER * t + i, j, k);
+                }
+            } else {
+                __syncthreads();   // earlier readers of lp/li are done
+#pragma unroll
+                for (int i = 0; i < PER; i++) { lp[PER * t + i] = v[i]; li[PER * t + i] = ix[i]; }
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < PER; i++) {
+                    const int e = PER * t + i;
+                    bit_cx(v[i], ix[i], lp[e ^ j], li[e ^ j], e, j, k);
+                }
+            }
+        }
+    }
+}
+
+// The device state the draw reads and advances, loaded early by one thread.
+struct SampState {
+    unsigned long long rng;
+    int pos, ngen, hlen, hpos;
+};
+
+__device__ __forceinline__ SampState samp_state_load(const SampleArgs &a) {
+    SampState q;
+    q.rng = a.rng[0];
+    q.pos = a.tokpos[1];
+    q.ngen = a.tokpos[2];
+    const bool h = a.hist && a.hist_cap > 0;
+    q.hlen = h ? a.hist_meta[0] : 0;
+    q.hpos = h ? a.hist_meta[1] : 0;
+    return q;
+}
+
+// ember_sampler_accept and the decode loop's {token, pos + 1, n + 1}
+__device__ __forceinline__ void samp_emit(const SampleArgs &a, const SampState &q, int tok) {
+    if (a.hist && a.hist_cap > 0) {
+        a.hist[q.hpos] = tok;
+        a.hist_meta[1] = (q.hpos + 1) % a.hist_cap;
+        if (q.hlen < a.hist_cap) a.hist_meta[0] = q.hlen + 1;
+    }
+    a.tokpos[0] = tok;
+    a.tokpos[1] = q.pos + 1;
+    if (q.ngen < a.cap) a.out[q.ngen] = tok;
+    a.tokpos[2] = q.ngen + 1;
+}
+
+// Kernel arguments are loaded where first used; pinning them at the start
+// issues all their scalar loads together instead of one miss per phase.
+#define SAMP_PIN(x) asm volatile("" ::"s"(x))
+
+// Launched with SAMPLE_GRID workgroups; a.nparts per-part maxima in a.am_val.
+__global__ __launch_bounds__(WG) void k_samp_fused(SampleArgs a) {
+    __shared__ float red[NWAVE], red2[NWAVE];
+    __shared__ float gm[NWAVE][64];
+    __shared__ int sh_nk;
+    __shared__ float lp[4 * WG];
+    __shared__ int li[4 * WG];
+    __shared__ unsigned long long lk[WG];
+    __shared__ float fp[SAMPLE_TOPK_MAX];
+    __shared__ int fi[SAMPLE_TOPK_MAX];
+    __shared__ int sh_last;
+    __shared__ int scn[SAMPLE_GRID], pre[SAMPLE_GRID];
+    __shared__ float wsum[SAMPLE_GRID / 64];
+    __shared__ int wcnt[SAMPLE_GRID / 64];
+    __shared__ bool wovf[SAMPLE_GRID / 64];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    SAMP_PIN(a.logits); SAMP_PIN(a.am_val); SAMP_PIN(a.cval); SAMP_PIN(a.cidx); SAMP_PIN(a.psum);
+    SAMP_PIN(a.scnt); SAMP_PIN(a.rng); SAMP_PIN(a.tokpos); SAMP_PIN(a.out); SAMP_PIN(a.hist);
+    SAMP_PIN(a.hist_meta); SAMP_PIN(a.n); SAMP_PIN(a.nparts); SAMP_PIN(a.cap); SAMP_PIN(a.hist_cap);
+    SAMP_PIN(a.p.temperature); SAMP_PIN(a.p.top_k); SAMP_PIN(a.p.top_p); SAMP_PIN(a.p.min_p);
+    const float T = a.p.temperature;
+    const int K = min(a.n, a.p.top_k);   // 1..SAMPLE_TOPK_MAX, checked at launch
+    int lo, hi;
+    samp_slice(a.n, lo, hi);
+
+    // ---- 1. loads: the per-part maxima and the slice's logits --------------
+    // (indices clamped into range, so every load is unconditional)
+    float pm[SAMP_PARTS], l[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_PARTS; k++) pm[k] = a.am_val[min(tid + k * WG, a.nparts - 1)];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) l[k] = a.logits[min(lo + tid + k * WG, a.n - 1)];
+#pragma unroll
+    for (int k = 0; k < SAMP_PARTS; k++)
+        if (tid + k * WG >= a.nparts) pm[k] = -INFINITY;
+
+    // ---- 2. M and the bound (every wave computes both) ---------------------
+    float g = pm[0];   // this thread's parts all fall in group tid % 128
+#pragma unroll
+    for (int k = 1; k < SAMP_PARTS; k++) g = fmaxf(g, pm[k]);
+    gm[w][lane] = g;
+    __syncthreads();
+    const float ga = fmaxf(gm[0][lane], gm[2][lane]), gb = fmaxf(gm[1][lane], gm[3][lane]);
+    // max(l) / T == max(l / T): correctly rounded division is monotone
+    const float M = wave_max(fmaxf(ga, gb)) / T;
+    if (tid == 0) sh_nk = 0;   // samp_bound's barriers order this before the counting
+    const float e_lo = samp_bound(w & 1 ? gb : ga, K, T, M, lp, red);   // thread t: group t % 128
+
+    // ---- 3. e, the slice sum, the tokens passed on --------------------------
+    // A token passed on takes the next slot of an LDS counter: the order
+    // within a slice does not matter, the final ranking breaks ties by index.
+    float *cv = a.cval + blockIdx.x * SAMP_CAP;
+    int *ci = a.cidx + blockIdx.x * SAMP_CAP;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + tid + k * WG;
+        if (k * WG < hi - lo && i < hi) {   // the first test is uniform
+            const float e = samp_e(l[k], T, M);
+            s += e;
+            if (e >= e_lo) {
+                const int slot = atomicAdd(&sh_nk, 1);
+                if (slot < SAMP_CAP) { cv[slot] = e; ci[slot] = i; }
+            }
+        }
+    }
+    s = wave_sum(s);
+    if (lane == 0) red2[w] = s;
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWAVE; i++) t += red2[i];
+        a.psum[blockIdx.x] = t;
+        a.scnt[blockIdx.x] = sh_nk;
+    }
+
+    // ---- 4. arrival: the last workgroup carries on --------------------------
+    // Every wave's stores have completed before the release (which writes the
+    // L2 back for the other XCDs); the acquire invalidates this CU's caches.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(a.scnt + SAMPLE_GRID, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        sh_last = old == SAMPLE_GRID - 1;
+    }
+    __syncthreads();
+    if (!sh_last) return;
+    if (tid == 0) __hip_atomic_store(a.scnt + SAMPLE_GRID, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- 5. one round trip: counts, sums and every passed-on slot ----------
+    // thread t < SAMPLE_GRID: slice t's count and sum; slots 4 tid .. 4 tid + 3
+    int c = 0;
+    float ps = 0.0f;
+    if (tid < SAMPLE_GRID) { c = a.scnt[tid]; ps = a.psum[tid]; }
+    const float4 cv4 = reinterpret_cast<const float4 *>(a.cval)[tid];
+    const int4 ci4 = reinterpret_cast<const int4 *>(a.cidx)[tid];
+    SampState st{};
+    if (tid == 0) st = samp_state_load(a);   // used by the draw only
+    if (tid < SAMPLE_GRID) {
+        const float ws = wave_sum(ps);
+        int incl = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int u = __shfl_up(incl, off);
+            if (lane >= off) incl += u;
+        }
+        scn[tid] = c;
+        pre[tid] = incl - c;   // within this wave of slices
+        const bool ovf = __ballot(c > SAMP_CAP) != 0;
+        if (lane == 63) { wsum[w] = ws; wcnt[w] = incl; wovf[w] = ovf; }
+    }
+    if (tid < 64) { fp[tid] = -1.0f; fi[tid] = INT_MAX; }
+    __syncthreads();
+    float S = wsum[0];   // a fixed tree order over the slices
+    int total = wcnt[0];
+    bool ovf = wovf[0];
+#pragma unroll
+    for (int v = 1; v < SAMPLE_GRID / 64; v++) { S += wsum[v]; total += wcnt[v]; ovf = ovf || wovf[v]; }
+    const int mode = (ovf || total < K) ? 2 : total <= WG ? 0 : total <= 4 * WG ? 1 : 2;
+
+    // ---- 6. the first 64 in samp_before order into fp/fi --------------------
+    if (mode != 2) {   // compact the passed tokens to [0, total)
+        constexpr int TPS = SAMP_CAP / 4;   // threads per slice
+        const int sl = tid / TPS, c = scn[sl];
+        int b = pre[sl];
+#pragma unroll
+        for (int v = 0; v < SAMPLE_GRID / 64 - 1; v++) b += v < sl / 64 ? wcnt[v] : 0;
+        const float cv[4] = { cv4.x, cv4.y, cv4.z, cv4.w };
+        const int cx[4] = { ci4.x, ci4.y, ci4.z, ci4.w };
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * (tid % TPS) + i;
+            if (r < c) {
+                const float pv = cv[i] / S;
+                if (mode == 0) lk[b + r] = samp_key(pv, cx[i]);
+                else { lp[b + r] = pv; li[b + r] = cx[i]; }
+            }
+        }
+        __syncthreads();
+    }
+    if (mode == 0) {   // rank by counting: distinct indices make the ranks distinct
+        if (tid < total) {
+            const unsigned long long my = lk[tid];
+            int rank = 0;
+#pragma unroll 8
+            for (int q = 0; q < total; q++) rank += lk[q] > my ? 1 : 0;
+            if (rank < SAMPLE_TOPK_MAX) {
+                fp[rank] = __uint_as_float((unsigned)(my >> 32));
+                fi[rank] = (int)~(unsigned)my;
+            }
+        }
+    } else if (mode == 1) {
+        float v4[4];
+        int i4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = 4 * tid + i;
+            v4[i] = q < total ? lp[q] : -1.0f;
+            i4[i] = q < total ? li[q] : INT_MAX;
+        }
+        bitonic_sort<4>(v4, i4, lp, li);
+        if (tid < SAMPLE_TOPK_MAX / 4) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) { fp[4 * tid + i] = v4[i]; fi[4 * tid + i] = i4[i]; }
+        }
+    } else {
+        // the whole vocabulary, 4 * WG - 64 logits at a time beside the running 64
+        constexpr int STEP = 4 * WG - SAMPLE_TOPK_MAX;
+#pragma unroll 1
+        for (int base = 0; base < a.n; base += STEP) {
+            float v4[4];
+            int i4[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = 4 * tid + i;
+                if (q < SAMPLE_TOPK_MAX) {
+                    v4[i] = fp[q];
+                    i4[i] = fi[q];
+                } else {
+                    const int x = base + q - SAMPLE_TOPK_MAX;
+                    v4[i] = x < a.n ? samp_e(a.logits[x], T, M) / S : -1.0f;
+                    i4[i] = x < a.n ? x : INT_MAX;
+                }
+            }
+            bitonic_sort<4>(v4, i4, lp, li);
+            __syncthreads();   // every read of fp/fi above is done
+            if (tid < SAMPLE_TOPK_MAX / 4) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) { fp[4 * tid + i] = v4[i]; fi[4 * tid + i] = i4[i]; }
+            }
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    if (tid >= 64) return;
+
+    // ---- 7. min-p, top-p and the draw (sample.c:141-175) --------------------
+    const float v = fp[lane];
+    const int ix = fi[lane];
+    int m = K;   // the first K are real tokens on every path above
     if (a.p.min_p > 0.0f && a.p.min_p < 1.0f) {
         const float thresh = a.p.min_p * lane_f(v, 0);
         const unsigned long long drop = __ballot(lane >= 1 && lane < m && !(v >= thresh));
         if (drop) m = __builtin_ctzll(drop);
     }
-    float cum = 0.0f, c = 0.0f;   // cum = sum of the sorted p[0..lane], in order
+    float cum = 0.0f;   // sum of the sorted p[0..lane], in order (adding +0 after it changes nothing)
 #pragma unroll
-    for (int i = 0; i < 64; i++) {
-        c += lane_f(v, i);
-        if (lane == i) cum = c;
+    for (int q = 0; q < 64; q += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(fp + q);
+        cum += q <= lane ? f.x : 0.0f;
+        cum += q + 1 <= lane ? f.y : 0.0f;
+        cum += q + 2 <= lane ? f.z : 0.0f;
+        cum += q + 3 <= lane ? f.w : 0.0f;
     }
     if (a.p.top_p > 0.0f && a.p.top_p < 1.0f) {
         const unsigned long long hit = __ballot(lane < m && cum >= a.p.top_p);
         if (hit) m = __builtin_ctzll(hit) + 1;
     }
-    const float cutoff = __shfl(cum, m - 1);
-    unsigned long long x = a.rng[0];   // xorshift64* (sample.c:98-105)
+    const float cutoff = lane_f(cum, m - 1);
+    // xorshift64* (sample.c:98-107) on the state lane 0 loaded
+    const unsigned xh = (unsigned)__builtin_amdgcn_readlane((int)(st.rng >> 32), 0),
+                   xl = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)st.rng, 0);
+    unsigned long long x = ((unsigned long long)xh << 32) | xl;
     x ^= x >> 12; x ^= x << 25; x ^= x >> 27;
     const unsigned int u = (unsigned int)((x * 0x2545F4914F6CDD1DULL) >> 32);
     const float r = (float)(u >> 8) / 16777216.0f * cutoff;
     const unsigned long long in = __ballot(lane < m && r < cum);
-    const int chosen = __shfl(ix, in ? __builtin_ctzll(in) : m - 1);
+    const int chosen = __builtin_amdgcn_readlane(ix, in ? __builtin_ctzll(in) : m - 1);
     if (lane == 0) {
         a.rng[0] = x;
-        samp_emit(a, chosen);
+        samp_emit(a, st, chosen);
     }
 }
 
@@ -493,10 +574,14 @@ __global__ void k_samp_greedy_emit(SampleArgs a) {
     }
 }
 
+bool sample_penalized(const SampleArgs &a) {
+    return a.hist && a.hist_cap > 0 &&
+        (a.p.repeat_penalty != 1.0f || a.p.frequency_penalty != 0.0f || a.p.presence_penalty != 0.0f);
+}
+
 int launch_sample(hipStream_t st, const SampleArgs &a) {
     if (a.n <= 0 || (a.n + SAMPLE_GRID - 1) / SAMPLE_GRID > SAMPLE_SLICE_MAX) return -1;
-    const bool pen = a.hist && a.hist_cap > 0 &&
-        (a.p.repeat_penalty != 1.0f || a.p.frequency_penalty != 0.0f || a.p.presence_penalty != 0.0f);
+    const bool pen = sample_penalized(a);
     if (pen) hipLaunchKernelGGL(k_samp_pen, dim3(1), dim3(WG), 0, st, a);
     if (a.p.temperature <= 0.0f) {
         ArgmaxArgs g{};
@@ -507,10 +592,17 @@ int launch_sample(hipStream_t st, const SampleArgs &a) {
         return 0;
     }
     if (a.p.top_k < 1 || a.p.top_k > SAMPLE_TOPK_MAX) return -1;
-    hipLaunchKernelGGL(k_samp_a, dim3(SAMPLE_GRID), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(k_samp_b, dim3(SAMPLE_GRID), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(k_samp_c, dim3(SAMPLE_GRID), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(k_samp_d, dim3(1), dim3(WG), 0, st, a);
+    SampleArgs b = a;
+    if (pen || b.nparts <= 0) {   // per-part maxima of the logits as they now are
+        ArgmaxArgs g{};
+        g.logits = a.logits; g.n = a.n; g.pval = a.am_val; g.pidx = a.am_idx;
+        const int nb = (a.n + ARGMAX_PER_THREAD * WG - 1) / (ARGMAX_PER_THREAD * WG);
+        if (nb > ARGMAX_MAX_BLOCKS) return -1;
+        hipLaunchKernelGGL(k_argmax_part, dim3(nb), dim3(WG), 0, st, g);
+        b.nparts = nb;
+    }
+    if (b.nparts > SAMP_PARTS * WG) return -1;
+    hipLaunchKernelGGL(k_samp_fused, dim3(SAMPLE_GRID), dim3(WG), 0, st, b);
     return 0;
 }
 

@@ -93,16 +93,50 @@ def test_device_sampler_matches_host_on_vocab_logits(params):
     eng.close()
 
 
-def test_generate_sampled_equals_host_loop():
-    """ehip_generate_sampled = the generate loop of forward + ember_sample."""
+@pytest.mark.parametrize("kind", ["flat", "two-level", "quantized", "one-hot", "spread-ties"])
+def test_device_sampler_degenerate_logits(kind):
+    """Flat and heavily tied logits: many tokens share the bound, which sends
+    the sampler down its whole-vocabulary path; "spread-ties" (514 tokens tied
+    at the top, about 8 per slice) takes its bitonic sort of up to 1024."""
+    V = 151936
+    say(f"vocab {V}: {kind} logits")
+    eng = emberllm.Engine(small_model(V))
+    rng = np.random.default_rng(5)
+    a = sampler(0.9, 0.95, 50, 31)
+    b = sampler(0.9, 0.95, 50, 31)
+    for step in range(4):
+        if kind == "flat":
+            lg = np.full(V, 0.25, np.float32)
+        elif kind == "two-level":
+            lg = np.where(rng.random(V) < 0.01, 1.0, 0.0).astype(np.float32)
+        elif kind == "quantized":
+            lg = (np.round(rng.normal(0, 2, V) * 2) / 2).astype(np.float32)
+        elif kind == "spread-ties":
+            lg = rng.normal(0, 1, V).astype(np.float32)
+            lg[::296] = 10.0
+        else:
+            lg = np.full(V, -50.0, np.float32)
+            lg[rng.integers(0, V)] = 50.0
+        x = lg.copy()
+        host = lib().ember_sample(ctypes.byref(b), x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), V)
+        dev = eng.sample(lg, a)
+        assert dev == host and a.rng_state == b.rng_state, (kind, step, dev, host)
+    eng.close()
+
+
+@pytest.mark.parametrize("penalties", [True, False], ids=["penalties", "plain"])
+def test_generate_sampled_equals_host_loop(penalties):
+    """ehip_generate_sampled = the generate loop of forward + ember_sample.
+    Without penalties the lm_head's per-workgroup winners feed the sampler."""
     path = configs.model_path("t_qwen3")
-    say("device sampling loop vs host loop")
+    say(f"device sampling loop vs host loop, penalties {penalties}")
     a, b = emberllm.Engine(path), emberllm.Engine(path)
     ids = np.array([3, 77, 12, 500, 9], dtype=np.int32)
     a.prefill(ids)
     lg = b.prefill(ids)
-    sa = sampler(0.8, 0.9, 40, 4242, rp=1.1, last_n=16)
-    sb = sampler(0.8, 0.9, 40, 4242, rp=1.1, last_n=16)
+    pen = dict(rp=1.1, last_n=16) if penalties else {}
+    sa = sampler(0.8, 0.9, 40, 4242, **pen)
+    sb = sampler(0.8, 0.9, 40, 4242, **pen)
     for t in ids:
         lib().ember_sampler_accept(ctypes.byref(sa), int(t))
         lib().ember_sampler_accept(ctypes.byref(sb), int(t))

@@ -173,6 +173,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill and kernel timings")
+    ap.add_argument("--sampled-only", action="store_true",
+                    help="profiling aid: fill the cache to --depth, run only the device sampling loop "
+                         "(T 0.8, top-k 40, top-p 0.9) and print its rate; no JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 64 MiB device-to-device 8 times (a kernel of known traffic, for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -236,6 +239,21 @@ def main():
     log(f"prefill pp{depth} {out[f'prefill_tok_s_pp{depth}']:.1f} tok/s")
     tok0 = int(np.argmax(lg))
 
+    def sampled_rate():
+        smp = _native.EmberSampler()
+        lib.ember_sampler_init(ctypes.byref(smp), 0.8, 0.9, 40, 1234)
+        eng.generate_sampled(tok0, depth, W, smp)
+        _, mss = eng.generate_sampled(tok0, depth, K, smp)
+        lib.ember_sampler_free(ctypes.byref(smp))
+        rate = K / (mss / 1e3)
+        log(f"decode @{depth} sampled (T 0.8, top-k 40, top-p 0.9): {rate:.1f} tok/s")
+        return rate
+
+    if args.sampled_only:
+        sampled_rate()
+        eng.close()
+        return
+
     # ---- decode at depth: device-resident greedy loop --------------------
     eng.generate_greedy(tok0, depth, W)             # warmup (also builds the graph)
     wall = time.perf_counter()
@@ -293,13 +311,7 @@ def main():
         log(f"decode @128: {out['decode_tok_s_depth128']:.1f} tok/s")
 
         # ---- sampled decode at depth (T 0.8, top-k 40, top-p 0.9) ---------
-        smp = _native.EmberSampler()
-        lib.ember_sampler_init(ctypes.byref(smp), 0.8, 0.9, 40, 1234)
-        eng.generate_sampled(tok0, depth, W, smp)
-        _, mss = eng.generate_sampled(tok0, depth, K, smp)
-        lib.ember_sampler_free(ctypes.byref(smp))
-        out["decode_tok_s_sampled"] = K / (mss / 1e3)
-        log(f"decode @{depth} sampled (T 0.8, top-k 40, top-p 0.9): {out['decode_tok_s_sampled']:.1f} tok/s")
+        out["decode_tok_s_sampled"] = sampled_rate()
     eng.close()
 
     cpu = None

@@ -84,6 +84,7 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
         for (int h = 0; h < GM; h++) acc[i][h] = 0.0f;
     const float *kr = &ks[lane * KP];
     const float *qw = &qs[wave * QW * GM * HD];
+#pragma unroll(HD > 64 ? 1 : 4)   // full unrolling at HD 64 spilled registers
     for (int d = 0; d < HD; d += 4) {
         const float4 kf = *reinterpret_cast<const float4 *>(kr + d);
 #pragma unroll
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     const float *srowp = a.scores + sgrow * a.ldk;
     const int last4 = a.ldk - 4;
 
-    float4 vr[VLD], sr[SLD];
+    f32x4 vr[VLD], sr[SLD];
     auto load = [&](int t0) {
 #pragma unroll
         for (int i = 0; i < VLD; i++) {
@@ -336,27 +337,27 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
             const size_t off = (size_t)min(t0 + t, tmax) * a.kv_dim + hoff + c;
             if (F16) {
                 const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
-                vr[i] = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
+                vr[i] = f32x4{h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16)};
             } else {
-                vr[i] = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.vc) + off);
+                vr[i] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.vc) + off);
             }
         }
 #pragma unroll
         for (int i = 0; i < SLD; i++) {
             const int c4 = (tid + i * WG) / RW;
-            sr[i] = *reinterpret_cast<const float4 *>(srowp + min(t0 + 4 * c4, last4));
+            sr[i] = *reinterpret_cast<const f32x4 *>(srowp + min(t0 + 4 * c4, last4));
         }
     };
     auto stage = [&](int t0) {
 #pragma unroll
         for (int i = 0; i < VLD; i++) {
             const int f = tid + i * WG;
-            *reinterpret_cast<float4 *>(&vs[(f / DG) * HD + (f % DG) * 4]) = vr[i];
+            *reinterpret_cast<f32x4 *>(&vs[(f / DG) * HD + (f % DG) * 4]) = vr[i];
         }
 #pragma unroll
         for (int i = 0; i < SLD; i++) {   // p = e * (1/sum), model.c:62-63
             const int c4 = (tid + i * WG) / RW, t = t0 + 4 * c4;
-            const float4 e = sr[i];
+            const f32x4 e = sr[i];
             ps[(4 * c4 + 0) * PP + srow] = t < slen ? expf(e.x - smx) * sinv : 0.0f;
             ps[(4 * c4 + 1) * PP + srow] = t + 1 < slen ? expf(e.y - smx) * sinv : 0.0f;
             ps[(4 * c4 + 2) * PP + srow] = t + 2 < slen ? expf(e.z - smx) * sinv : 0.0f;

@@ -19,6 +19,10 @@ enum { DT_F32 = 0, DT_Q8 = 1, DT_Q4 = 2 };
 enum { ROPE_INTERLEAVED = 0, ROPE_NEOX = 1 };
 constexpr int QB = 32;      // weights per quant block
 constexpr int WG = 256;     // threads per workgroup (4 wave64)
+// Native 4-float vector.  Arrays of HIP's float4 struct that a lambda fills
+// and another reads can stay in scratch memory; arrays of this type are kept
+// in registers.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int NWAVE = WG / 64;
 
 struct DMat {

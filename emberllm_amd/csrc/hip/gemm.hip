@@ -201,20 +201,23 @@ __global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
 // int8 MFMA GEMM.  Workgroup tile GM_U (units) x TT (tokens, 128 or 64), four
 // waves in a 2 x 2 arrangement, each owning 2 x (TT / 64) MFMA tiles of
 // 32 x 32 (64-token tiles when 128 would leave CUs idle: the 1024-output wo
-// and w2 products of a 2048-token pass).  K advances GM_KB quant blocks per
+// and w2 products of a 2048-token pass).  K advances KB quant blocks per
 // stage; stages are double-buffered in LDS (the next stage's global loads are
-// issued before the current stage's products).
+// issued before the current stage's products).  KB = 2 (measured against 8,
+// which was slower at every prompt length once no stage registers sat in
+// scratch memory).
 // Output (i, j) of an MFMA tile sits in lane j + 32*((i/4)%2), accumulator
 // (i%4) + 4*(i/8); A fragments hold W[u][16h .. 16h+15] of one block, B
 // fragments X[t][16h .. 16h+15], h = lane / 32.
-constexpr int GM_U = 128, GM_KB = 2;
+constexpr int GM_U = 128;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
-template <int DT, int EPI, int TT>
+template <int DT, int EPI, int TT, int KB>
 __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
+    constexpr int GM_KB = KB;
     constexpr int GM_T = TT, NY = TT / 64;            // tokens per tile, MFMA tiles per wave along tokens
     constexpr int WB = DT == DT_Q8 ? 32 : 16;          // weight bytes per row and block
     constexpr int WROW = GM_KB * WB, XROW = GM_KB * 32; // stage bytes per row
@@ -231,42 +234,55 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 
     // global -> registers for one stage: weights (WROW bytes per row), codes, scales
     constexpr int WLD = GM_U * WROW / 16 / WG, XLD = GM_T * XROW / 16 / WG;
-    int4 wr[WLD], xr[XLD];
-    float dwr, dxr; int xsr;
-    auto load = [&](int st) {
+    constexpr int NDW = GM_KB * GM_U / WG, NDX = (GM_KB * GM_T + WG - 1) / WG;   // scales per thread
+    static_assert(GM_KB * GM_U % WG == 0, "weight scales per thread");
+    i32x4 wr[WLD], xr[XLD];   // native vectors: HIP's int4 struct kept these in scratch
+    float dwr[NDW], dxr[NDX]; int xsr[NDX];
+    auto load = [&](int st) __attribute__((always_inline)) {
         const int b0 = st * GM_KB;
 #pragma unroll
         for (int i = 0; i < WLD; i++) {
             const int f = tid + i * WG, row = f / (WROW / 16), c = (f % (WROW / 16)) * 16;
             const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
-            wr[i] = *reinterpret_cast<const int4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
+            wr[i] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
         }
 #pragma unroll
         for (int i = 0; i < XLD; i++) {
             const int f = tid + i * WG, row = f / (XROW / 16), c = (f % (XROW / 16)) * 16;
             const int t = min(t0 + row, a.n - 1), blk = min(b0 + c / 32, nb - 1);
-            xr[i] = *reinterpret_cast<const int4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
+            xr[i] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
         }
-        {   // GM_KB * GM_U weight scales and GM_KB * GM_T activation scales: one
-            // and (at most) one per thread
-            const int kb = tid / GM_U, r = tid % GM_U;
-            const int blk = min(b0 + kb, nb - 1);
-            dwr = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk]);
-            const int t = min(t0 + min(r, GM_T - 1), a.n - 1);
-            dxr = a.dx[(size_t)t * nb + blk];
-            xsr = DT == DT_Q4 ? a.xs[(size_t)t * nb + blk] : 0;
+        // GM_KB * GM_U weight scales and GM_KB * GM_T activation scales
+#pragma unroll
+        for (int i = 0; i < NDW; i++) {
+            const int f = tid + i * WG, kb = f / GM_U, r = f % GM_U;
+            dwr[i] = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + min(b0 + kb, nb - 1)]);
+        }
+#pragma unroll
+        for (int i = 0; i < NDX; i++) {
+            const int f = min(tid + i * WG, GM_KB * GM_T - 1), kb = f / GM_T, r = f % GM_T;
+            const int t = min(t0 + r, a.n - 1), blk = min(b0 + kb, nb - 1);
+            dxr[i] = a.dx[(size_t)t * nb + blk];
+            xsr[i] = DT == DT_Q4 ? a.xs[(size_t)t * nb + blk] : 0;
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < WLD; i++) reinterpret_cast<int4 *>(ws[buf])[tid + i * WG] = wr[i];
+        for (int i = 0; i < WLD; i++) reinterpret_cast<i32x4 *>(ws[buf])[tid + i * WG] = wr[i];
 #pragma unroll
-        for (int i = 0; i < XLD; i++) reinterpret_cast<int4 *>(xsm[buf])[tid + i * WG] = xr[i];
-        const int kb = tid / GM_U, r = tid % GM_U;
-        dws[buf][kb][r] = dwr;
-        if (r < GM_T) {
-            dxs[buf][kb][r] = dxr;
-            sxs[buf][kb][r] = xsr;
+        for (int i = 0; i < XLD; i++) reinterpret_cast<i32x4 *>(xsm[buf])[tid + i * WG] = xr[i];
+#pragma unroll
+        for (int i = 0; i < NDW; i++) {
+            const int f = tid + i * WG;
+            dws[buf][f / GM_U][f % GM_U] = dwr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NDX; i++) {
+            const int f = tid + i * WG;
+            if (f < GM_KB * GM_T) {
+                dxs[buf][f / GM_T][f % GM_T] = dxr[i];
+                sxs[buf][f / GM_T][f % GM_T] = xsr[i];
+            }
         }
     };
 
@@ -341,18 +357,152 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
         }
 }
 
+// --------------------------------------------------------------------------
+// Short prompts: the 128-unit tiles above leave most CUs idle (a 128-token
+// wo or w2 product is 16 workgroups), and the reference's block order keeps
+// K in one workgroup.  This variant takes 32 units x 32 tokens per workgroup,
+// one 16 x 16 v_mfma_i32_16x16x32_i8 tile per wave and quant block, and
+// GS_KB = 16 blocks per double-buffered stage so a short K needs few global
+// round trips.  Fragments of the 16 x 16 x 32 product: lane l holds
+// A[l % 16][8 (l / 16) .. +7] (eight int8 of a weight row),
+// B[8 (l / 16) .. +7][l % 16] (of a token row), and outputs
+// D[4 (l / 16) + r][l % 16], r = 0..3.  The epilogue is the same
+// sum += ((float)isum * dw) * dx in block order.
+constexpr int GS_U = 32, GS_T = 32, GS_KB = 16;
+
+template <int DT, int EPI>
+__global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
+    constexpr int WB = DT == DT_Q8 ? 32 : 16;                 // weight bytes per row and block
+    constexpr int WROW = GS_KB * WB, XROW = GS_KB * 32;        // stage bytes per row
+    constexpr int WP = WROW + 16, XP = XROW + 16;              // LDS row pitches
+    constexpr int WLD = GS_U * WROW / 16 / WG, XLD = GS_T * XROW / 16 / WG;
+    constexpr int NSC = GS_KB * GS_U / WG;                     // scales of each kind per thread
+    static_assert(GS_U == GS_T && GS_KB * GS_U % WG == 0 && WLD >= 1 && XLD >= 1, "layout");
+    __shared__ __align__(16) uint8_t ws[2][GS_U * WP];
+    __shared__ __align__(16) int8_t xsm[2][GS_T * XP];
+    __shared__ float dws[2][GS_KB][GS_U], dxs[2][GS_KB][GS_T];
+    __shared__ int sxs[2][GS_KB][GS_T];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int fr = lane & 15, fg = lane >> 4;
+    const int u0 = blockIdx.x * GS_U, t0 = blockIdx.y * GS_T;
+    const int K = a.W.cols, nb = K / QB, nst = (nb + GS_KB - 1) / GS_KB;
+    const int wu = (wave & 1) * 16, wt = (wave >> 1) * 16;
+
+    i32x4 wr[WLD], xr[XLD];
+    float dwr[NSC], dxr[NSC];
+    int xsr[NSC];
+    auto load = [&](int st) {
+        const int b0 = st * GS_KB;
+#pragma unroll
+        for (int i = 0; i < WLD; i++) {
+            const int f = tid + i * WG, row = f / (WROW / 16), c = (f % (WROW / 16)) * 16;
+            const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
+            wr[i] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
+        }
+#pragma unroll
+        for (int i = 0; i < XLD; i++) {
+            const int f = tid + i * WG, row = f / (XROW / 16), c = (f % (XROW / 16)) * 16;
+            const int t = min(t0 + row, a.n - 1), blk = min(b0 + c / 32, nb - 1);
+            xr[i] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
+        }
+#pragma unroll
+        for (int i = 0; i < NSC; i++) {
+            const int f = tid + i * WG, kb = f / GS_U, r = f % GS_U, blk = min(b0 + kb, nb - 1);
+            const int t = min(t0 + r, a.n - 1);
+            dwr[i] = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk]);
+            dxr[i] = a.dx[(size_t)t * nb + blk];
+            xsr[i] = DT == DT_Q4 ? a.xs[(size_t)t * nb + blk] : 0;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < WLD; i++) {
+            const int f = tid + i * WG;
+            *reinterpret_cast<i32x4 *>(ws[buf] + (f / (WROW / 16)) * WP + (f % (WROW / 16)) * 16) = wr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < XLD; i++) {
+            const int f = tid + i * WG;
+            *reinterpret_cast<i32x4 *>(xsm[buf] + (f / (XROW / 16)) * XP + (f % (XROW / 16)) * 16) = xr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NSC; i++) {
+            const int f = tid + i * WG;
+            dws[buf][f / GS_U][f % GS_U] = dwr[i];
+            dxs[buf][f / GS_T][f % GS_T] = dxr[i];
+            sxs[buf][f / GS_T][f % GS_T] = xsr[i];
+        }
+    };
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int st = 0; st < nst; st++) {
+        const int buf = st & 1;
+        if (st + 1 < nst) load(st + 1);
+#pragma unroll 4
+        for (int kb = 0; kb < GS_KB; kb++) {
+            if (st * GS_KB + kb >= nb) break;
+            const uint8_t *wp = ws[buf] + (wu + fr) * WP + kb * WB;
+            long af;
+            if (DT == DT_Q8) {
+                af = *reinterpret_cast<const long *>(wp + 8 * fg);
+            } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
+                const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
+                af = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
+            }
+            const long bf = *reinterpret_cast<const long *>(xsm[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
+            const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, i32x4{0, 0, 0, 0}, 0, 0, 0);
+            const float dx = dxs[buf][kb][wt + fr];
+            const int xsum = DT == DT_Q4 ? sxs[buf][kb][wt + fr] : 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
+                acc[r] += ((float)isum * dws[buf][kb][wu + 4 * fg + r]) * dx;
+            }
+        }
+        __syncthreads();
+        if (st + 1 < nst) {
+            store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+    const int t = t0 + wt + fr;
+    if (t >= a.n) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int u = u0 + wu + 4 * fg + r;
+        if (u >= a.units) continue;
+        float *o = a.out + (size_t)t * a.out_stride + u;
+        if (EPI == EPI_STORE) *o = a.bias ? acc[r] + a.bias[u] : acc[r];
+        else *o += acc[r];
+    }
+}
+
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
     if (a.W.dtype == DT_Q8 || a.W.dtype == DT_Q4) {
         // 128-token tiles unless that leaves fewer workgroups than CUs
         // (a 256-CU part); 64-token tiles then double the grid
         const int gu = (a.units + GM_U - 1) / GM_U;
+        if ((long)gu * ((a.n + 63) / 64) < 256) {   // short prompt: 32 x 32 tiles
+            const dim3 gs((a.units + GS_U - 1) / GS_U, (a.n + GS_T - 1) / GS_T);
+#define GSF(DT)                                                                                          \
+            if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE>), gs, dim3(WG), 0, st, a); \
+            else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID>), gs, dim3(WG), 0, st, a); \
+            else return -1;                                                                              \
+            return 0;
+            if (a.W.dtype == DT_Q8) { GSF(DT_Q8) }
+            GSF(DT_Q4)
+#undef GSF
+        }
         const bool t64 = (long)gu * ((a.n + 127) / 128) < 256;
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
-#define GMF(DT, TT)                                                                              \
-        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT>), g, dim3(WG), 0, st, a); \
-        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT>), g, dim3(WG), 0, st, a); \
-        else return -1;                                                                          \
+#define GMF(DT, TT)                                                                                     \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2>), g, dim3(WG), 0, st, a); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2>), g, dim3(WG), 0, st, a); \
+        else return -1;                                                                                 \
         return 0;
         if (a.W.dtype == DT_Q8) { if (t64) { GMF(DT_Q8, 64) } else { GMF(DT_Q8, 128) } }
         if (t64) { GMF(DT_Q4, 64) } else { GMF(DT_Q4, 128) }

@@ -24,9 +24,11 @@ __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
     __shared__ float red[NWAVE];
     const int K = a.cols, nb = K / QB, b = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the row loops are unrolled so a thread's global loads are issued together
     float ss = 0.0f;
     if (a.ids) {
         const int tok = a.ids[b];
+#pragma unroll 4
         for (int i = tid; i < K; i += WG) {
             float v;
             if (a.emb.dtype == DT_F32) v = reinterpret_cast<const float *>(a.emb.q)[(size_t)tok * K + i];
@@ -37,6 +39,7 @@ __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
         }
     } else if (a.swiglu) {
         const float *row = a.x + (size_t)b * a.x_stride;
+#pragma unroll 4
         for (int i = tid; i < K; i += WG) {
             const float g = row[i];
             const float v = g / (1.0f + expf(-g)) * row[K + i];
@@ -44,11 +47,13 @@ __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
         }
     } else {
         const float *row = a.x + (size_t)b * a.x_stride;
+#pragma unroll 4
         for (int i = tid; i < K; i += WG) { const float v = row[i]; xs[i] = v; ss += v * v; }
     }
     if (a.norm_w) {
         const float tot = block_sum(ss, red);
         const float scale = 1.0f / sqrtf(tot / (float)K + a.eps);
+#pragma unroll 4
         for (int i = tid; i < K; i += WG) xs[i] = xs[i] * scale * a.norm_w[i];
     }
     __syncthreads();

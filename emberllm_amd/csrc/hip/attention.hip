@@ -292,7 +292,8 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
 }
 
 // P.V for head_dim 64 / 128, register-blocked: thread (dg, rs) accumulates
-// dims 4*dg .. 4*dg+3 of the RPS rows rs*RPS .. of the workgroup's 64 rows
+// dims 4*dg .. 4*dg+3 (of the HD / DS dims blockIdx.z covers: DS > 1 splits
+// a head over workgroups for short prompts) of the RPS rows rs*RPS .. of the workgroup's 64 rows
 // (QT = 64 / GM tokens x GM heads), so each position costs one V float4 and
 // RPS/4 probability float4 reads from LDS for 8 * RPS multiplies and adds.
 // V is staged row-major (vs[t][d]); probabilities position-major
@@ -300,14 +301,15 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
 // tile's global loads are issued before the current tile's products.  Every
 // (row, dim) sums its positions in order, multiply and add rounded apart;
 // positions past a row's length carry probability 0 (see k_pf_pv).
-template <int HD, int GM, bool F16>
+template <int HD, int GM, bool F16, int DS>
 __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
-    constexpr int RW = 64, QT = RW / GM, DG = HD / 4, RSETS = WG / DG, RPS = RW / RSETS;
-    constexpr int VLD = PF_KT * HD / 4 / WG;        // V float4 loads per thread per tile
+    constexpr int HDS = HD / DS;                    // this workgroup's dims: blockIdx.z * HDS ..
+    constexpr int RW = 64, QT = RW / GM, DG = HDS / 4, RSETS = WG / DG, RPS = RW / RSETS;
+    constexpr int VLD = PF_KT * HDS / 4 / WG;       // V float4 loads per thread per tile
     constexpr int SLD = RW * PF_KT / 4 / WG;        // score float4 loads per thread per tile
     constexpr int PP = RW + 4;                      // ps row pitch
-    static_assert(RW % RSETS == 0 && RPS % 4 == 0 && WG % DG == 0, "layout");
-    __shared__ __align__(16) float vs[PF_KT * HD];
+    static_assert(RW % RSETS == 0 && RPS % 2 == 0 && WG % DG == 0 && VLD >= 1, "layout");
+    __shared__ __align__(16) float vs[PF_KT * HDS];
     __shared__ __align__(16) float ps[PF_KT * PP];
     const int tid = threadIdx.x, dg = tid % DG, rs = tid / DG;
     const int G = a.n_heads / a.n_kv, g = blockIdx.y;
@@ -319,7 +321,7 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     if (b0 >= a.n_tok) return;
     const int blast = min(a.n_tok, b0 + QT) - 1;
     const int tmax = a.pos_base + blast;                  // last key any row here needs
-    const size_t hoff = (size_t)g * HD;
+    const size_t hoff = (size_t)g * HD + (size_t)blockIdx.z * HDS;
     // the one score row this thread stages (row = tid % RW in every tile)
     const int srow = tid % RW, sb = b0 + srow / GM, sh = srow % GM;
     const bool sok = sb < a.n_tok && sh < G;
@@ -352,7 +354,7 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < VLD; i++) {
             const int f = tid + i * WG;
-            *reinterpret_cast<f32x4 *>(&vs[(f / DG) * HD + (f % DG) * 4]) = vr[i];
+            *reinterpret_cast<f32x4 *>(&vs[(f / DG) * HDS + (f % DG) * 4]) = vr[i];
         }
 #pragma unroll
         for (int i = 0; i < SLD; i++) {   // p = e * (1/sum), model.c:62-63
@@ -380,12 +382,20 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
         const float *pp = &ps[rs * RPS];
 #pragma unroll 4
         for (int t = 0; t < PF_KT; t++) {
-            const float4 v = *reinterpret_cast<const float4 *>(vp + t * HD);
+            const float4 v = *reinterpret_cast<const float4 *>(vp + t * HDS);
             float p[RPS];
+            if constexpr (RPS % 4 == 0) {
 #pragma unroll
-            for (int k = 0; k < RPS; k += 4) {
-                const float4 q = *reinterpret_cast<const float4 *>(pp + t * PP + k);
-                p[k] = q.x; p[k + 1] = q.y; p[k + 2] = q.z; p[k + 3] = q.w;
+                for (int k = 0; k < RPS; k += 4) {
+                    const float4 q = *reinterpret_cast<const float4 *>(pp + t * PP + k);
+                    p[k] = q.x; p[k + 1] = q.y; p[k + 2] = q.z; p[k + 3] = q.w;
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < RPS; k += 2) {
+                    const float2 q = *reinterpret_cast<const float2 *>(pp + t * PP + k);
+                    p[k] = q.x; p[k + 1] = q.y;
+                }
             }
 #pragma unroll
             for (int k = 0; k < RPS; k++) {   // positions in order, multiply and add rounded apart
@@ -400,7 +410,7 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     for (int k = 0; k < RPS; k++) {
         const int r = rs * RPS + k, b = b0 + r / GM, h = r % GM;
         if (b >= a.n_tok || h >= G) continue;
-        *reinterpret_cast<float4 *>(a.out + (size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + dg * 4) =
+        *reinterpret_cast<float4 *>(a.out + (size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + blockIdx.z * HDS + dg * 4) =
             make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
     }
 }
@@ -466,8 +476,15 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
     hipLaunchKernelGGL((k_pf_scores<HD, GM, F16>), dim3(ktiles, qtiles, a.n_kv), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(k_pf_rowsum, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(WG), 0, st, a);
     if constexpr (HD == 64 || HD == 128) {
-        constexpr int QT2 = 64 / GM;
-        hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16>), dim3((a.n_tok + QT2 - 1) / QT2, a.n_kv), dim3(WG), 0, st, a);
+        // short prompts: split the head dims over workgroups (32 per
+        // workgroup) so the grid covers more CUs; each (row, dim) still sums
+        // its positions in order
+        constexpr int QT2 = 64 / GM, DSPLIT = HD / 32;
+        const dim3 g2((a.n_tok + QT2 - 1) / QT2, a.n_kv);
+        if ((long)g2.x * g2.y < 256)
+            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, DSPLIT>), dim3(g2.x, g2.y, DSPLIT), dim3(WG), 0, st, a);
+        else
+            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, 1>), g2, dim3(WG), 0, st, a);
     } else {
         hipLaunchKernelGGL((k_pf_pv<HD, GM, F16>), dim3(qtiles, a.n_kv), dim3(WG), 0, st, a);
     }

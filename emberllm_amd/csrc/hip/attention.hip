@@ -57,9 +57,9 @@ __device__ __forceinline__ void stage_rows(float *dst, int pitch, const void *ca
 
 // grid (key tiles, token tiles of 4*QW, kv groups); wave w carries tokens
 // b0 + w*QW .. + QW-1 and the group's heads; lane = key
-template <int HD, int GM, bool F16>
+template <int HD, int GM, bool F16, int QW>
 __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
-    constexpr int QW = PfRows<GM>::QW, QT = 4 * QW, KP = HD + 4;
+    constexpr int QT = 4 * QW, KP = HD + 4;   // QW token rows per wave
     __shared__ __align__(16) float ks[PF_KT * KP];
     __shared__ __align__(16) float qs[QT * GM * HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -473,7 +473,11 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
     constexpr int QT = 4 * PfRows<GM>::QW;
     const int ktiles = (a.pos_base + a.n_tok + PF_KT - 1) / PF_KT;
     const int qtiles = (a.n_tok + QT - 1) / QT;
-    hipLaunchKernelGGL((k_pf_scores<HD, GM, F16>), dim3(ktiles, qtiles, a.n_kv), dim3(WG), 0, st, a);
+    // short prompts: one token row per wave for four times the workgroups
+    if (PfRows<GM>::QW > 1 && (long)ktiles * qtiles * a.n_kv < 1024)
+        hipLaunchKernelGGL((k_pf_scores<HD, GM, F16, 1>), dim3(ktiles, (a.n_tok + 3) / 4, a.n_kv), dim3(WG), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_pf_scores<HD, GM, F16, PfRows<GM>::QW>), dim3(ktiles, qtiles, a.n_kv), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(k_pf_rowsum, dim3((a.n_heads * a.n_tok + 63) / 64), dim3(WG), 0, st, a);
     if constexpr (HD == 64 || HD == 128) {
         // short prompts: split the head dims over workgroups (32 per

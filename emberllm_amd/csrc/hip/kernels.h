@@ -171,7 +171,7 @@ struct SampleParams {
 };
 constexpr int SAMPLE_TOPK_MAX = 64, SAMPLE_GRID = 64, SAMPLE_SLICE_MAX = 4096;
 struct SampleArgs {
-    float *logits; int n;            // device logits, overwritten as the reference does
+    float *logits; int n;            // device logits (penalties update them in place, as the reference does)
     SampleParams p;
     unsigned long long *rng;         // device xorshift64* state
     int *hist, *hist_meta;           // ring [hist_cap]; {hist_len, hist_pos}

@@ -491,7 +491,10 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         // 128-token tiles unless that leaves fewer workgroups than CUs
         // (a 256-CU part); 64-token tiles then double the grid
         const int gu = (a.units + GM_U - 1) / GM_U;
-        if ((long)gu * ((a.n + 63) / 64) < 256) {   // short prompt: 32 x 32 tiles
+        // 32 x 32 tiles for short prompts, and for the narrow (<= 1024-output)
+        // wo / w2 products up to 4 x that grid (pp2048 +2%, pp4096 +1.5%)
+        const long g64 = (long)gu * ((a.n + 63) / 64);
+        if (g64 < 256 || (a.units <= 1024 && g64 < 1024)) {
             const dim3 gs((a.units + GS_U - 1) / GS_U, (a.n + GS_T - 1) / GS_T);
 #define GSF(DT)                                                                                          \
             if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE>), gs, dim3(WG), 0, st, a); \

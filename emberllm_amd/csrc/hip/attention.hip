@@ -485,7 +485,7 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
         // its positions in order
         constexpr int QT2 = 64 / GM, DSPLIT = HD / 32;
         const dim3 g2((a.n_tok + QT2 - 1) / QT2, a.n_kv);
-        if ((long)g2.x * g2.y < 256)
+        if ((long)g2.x * g2.y < 1024)   // measured: up to pp2048 for 8 kv heads
             hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, DSPLIT>), dim3(g2.x, g2.y, DSPLIT), dim3(WG), 0, st, a);
         else
             hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, 1>), g2, dim3(WG), 0, st, a);

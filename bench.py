@@ -20,7 +20,8 @@ reported, never as `value`:
   decode_tok_s_sampled  the device loop with the full sampler (temperature
                         0.8, top-k 40, top-p 0.9, fixed seed) at the same depth
   prefill_tok_s_pp128 / _pp4096   ember_prefill at position 0 (mean of 5
-                        after 1 warmup, src/main.c:251-266)
+                        after 1 warmup, src/main.c:251-266); the last
+                        pp4096 run leaves the cache filled for the decode
   roofline              the dominant kernel (split-K attention of one layer
                         at depth 4096): algorithmic bytes per launch over
                         its average duration (HIP events, isolated launches
@@ -214,29 +215,27 @@ def main():
 
     # ---- prefill --------------------------------------------------------
     def prefill_rate(n, reps=5, warm=1):
+        """The reference bench's prefill protocol (src/main.c:251-266): one
+        untimed run, then the mean of `reps` timed ones; returns (mean, sd,
+        last logits)."""
         ids = rng.integers(0, V, n).astype(np.int32)
         rates = []
         for r in range(warm + reps):
             t = time.perf_counter()
-            eng.prefill(ids)
+            lg = eng.prefill(ids)
             dt = time.perf_counter() - t
             if r >= warm:
                 rates.append(n / dt)
-        return float(np.mean(rates)), float(np.std(rates, ddof=1) if len(rates) > 1 else 0.0)
+        return float(np.mean(rates)), float(np.std(rates, ddof=1) if len(rates) > 1 else 0.0), lg
 
     if not args.decode_only:
-        out["prefill_tok_s_pp128"], out["prefill_tok_s_pp128_sd"] = prefill_rate(128)
+        out["prefill_tok_s_pp128"], out["prefill_tok_s_pp128_sd"], _ = prefill_rate(128)
         log(f"prefill pp128 {out['prefill_tok_s_pp128']:.1f} tok/s")
-    # fill the cache to `depth` (also timed: pp<depth>)
-    ids = rng.integers(0, V, depth).astype(np.int32)
-    reps = 1 if args.decode_only else 3
-    rates = []
-    for _ in range(reps):
-        t = time.perf_counter()
-        lg = eng.prefill(ids)
-        rates.append(depth / (time.perf_counter() - t))
-    out[f"prefill_tok_s_pp{depth}"] = float(np.max(rates[1:] if len(rates) > 1 else rates))
-    log(f"prefill pp{depth} {out[f'prefill_tok_s_pp{depth}']:.1f} tok/s")
+    # fill the cache to `depth` (also timed: pp<depth>, mean of 5 after 1 warmup)
+    key = f"prefill_tok_s_pp{depth}"
+    out[key], out[key + "_sd"], lg = prefill_rate(depth, reps=1 if args.decode_only else 5,
+                                                  warm=0 if args.decode_only else 1)
+    log(f"prefill pp{depth} {out[key]:.1f} tok/s")
     tok0 = int(np.argmax(lg))
 
     def sampled_rate():
@@ -255,7 +254,8 @@ def main():
         return
 
     # ---- decode at depth: device-resident greedy loop --------------------
-    eng.generate_greedy(tok0, depth, W)             # warmup (also builds the graph)
+    eng.generate_greedy(tok0, depth, W)             # warmup (graph capture happens before the
+                                                    # timed region of every call)
     wall = time.perf_counter()
     toks, ms = eng.generate_greedy(tok0, depth, K)  # synchronises before and after
     wall = time.perf_counter() - wall

@@ -126,6 +126,11 @@ PROTOTYPES = {
     "ehip_set_graph_mode": (ctypes.c_int, [_P, ctypes.c_int]),
     "ehip_decode_fusion": (ctypes.c_int, [_P]),
     "ehip_debug_buffer": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_uint64]),
+    "ehip_debug_capture": (ctypes.c_int, [_P, ctypes.c_int]),
+    "ehip_debug_read": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_uint64]),
+    "ehip_debug_capture_prefill": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int]),
+    "ehip_debug_read_prefill": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_uint64, _IP, _IP]),
+    "ehip_prefill_pass_tokens": (ctypes.c_int, [_P]),
     "ehip_time_decode": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _FP]),
     "ehip_generate_greedy": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _IP, _FP]),
     "ehip_sample": (ctypes.c_int, [_P, _FP, ctypes.c_int, ctypes.POINTER(EmberSampler), _IP]),

@@ -53,7 +53,16 @@ TINY = {
     "t_g7": _cfg(128, 256, 2, 7, 1, 64, 384, 320, 1e6, 1e-6, N, bias=1),
 }
 
-ALL = dict(REAL, **TINY)
+# Qwen3-0.6B width and heads with 2 layers and a small vocabulary: reaches the
+# prefill GEMM tiles of the real shape (64- and 128-token MFMA tiles) and a
+# second 2048-token prefill pass while the oracle stays fast.
+WIDE = {
+    "w_qwen3": _cfg(1024, 3072, 2, 16, 8, 128, 4096, 4608, 1e6, 1e-6, N, qk_norm=1),
+    "w_qwen3_q4": _cfg(1024, 3072, 2, 16, 8, 128, 4096, 4608, 1e6, 1e-6, N, qk_norm=1,
+                       dtype=_native.DT_Q4_0),
+}
+
+ALL = dict(REAL, **TINY, **WIDE)
 
 
 def synth_config(cfg, threads=0):

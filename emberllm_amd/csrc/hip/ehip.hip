@@ -280,8 +280,17 @@ struct EhipState {
     StepGraph smp[2];   // device sampling loop: 1 step, GEN_UNROLL steps
     SampleParams smp_graph_p; int smp_graph_cap;
     hipEvent_t ev0, ev1;
+    // per-layer capture of the decode step's intermediate vectors
+    // (ehip_debug_capture): layer, or -1; one device buffer per DBG_* slot
+    int dbg_layer = -1;
+    float *dbg[6] = {};
+    // the same for one layer of one prefill pass (ehip_debug_capture_prefill)
+    int pdbg_layer = -1, pdbg_pass = 0, pdbg_n = 0, pdbg_pos = 0;
+    float *pdbg[6] = {};
     std::vector<void *> allocs;
 };
+// slots of ehip_debug_capture
+enum { DBG_XIN = 0, DBG_QKV = 1, DBG_O = 2, DBG_XMID = 3, DBG_H = 4, DBG_XOUT = 5 };
 
 template <class F>
 static int graph_capture(EhipState *s, StepGraph &sg, int steps, F enq) {
@@ -370,12 +379,18 @@ static int xm_reset(EhipState *s) {
     return 0;
 }
 
-static int xm_check(EhipState *s, int flag) {
-    if (!flag) return 0;
-    xm_reset(s);
-    set_err("decode attention: a workgroup ran on another XCD than the state's probe found; its chunk merge "
-            "is invalid (set EHIP_XMERGE=0 to merge with a second kernel)");
-    return -1;
+static void drop_step_graphs(EhipState *s);
+
+// The fused merge found a workgroup off the XCD its kv head was recorded on,
+// so that launch's merge (and every result after it) is invalid.  Switch the
+// state to the two-kernel merge for good: clear the counters and the flag,
+// and drop the captured graphs, which hold the fused kernel.  The caller
+// re-runs the work from its start, which rewrites the KV rows it wrote.
+static int xm_fallback(EhipState *s) {
+    if (xm_reset(s)) return -1;
+    s->xm_on = false;
+    drop_step_graphs(s);
+    return 0;
 }
 
 extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
@@ -524,20 +539,33 @@ static int enq_layers(EhipState *s) {
     const EhipModel *m = s->m;
     const EhipConfig &c = m->cfg;
     const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    // copies of the captured layer's vectors into the debug slots
+    auto snap = [&](int l, int slot, const float *src, int n) -> int {
+        if (l != s->dbg_layer) return 0;
+        HCHK(hipMemcpyAsync(s->dbg[slot], src, 4 * (size_t)n, hipMemcpyDeviceToDevice, s->st), -1);
+        return 0;
+    };
     for (int l = 0; l < c.n_layers; l++) {
         const DevLayer &y = m->layers[l];
         MatvecArgs a{};
         a.W = y.qkv; a.units = qd + 2 * kvd; a.in = s->x; a.norm_w = y.attn_norm; a.eps = c.norm_eps;
         a.tokpos = s->tokpos_d; a.emb = m->emb; a.x_out = s->x; a.out = s->qkv; a.bias = y.bias_qkv;
+        if (l > 0 && snap(l, DBG_XIN, s->x, c.dim)) return -1;
         if (launch_matvec(s->st, l == 0 ? PRO_EMBED_NORM : PRO_NORM, EPI_STORE, a)) return -1;
+        if (l == 0 && snap(l, DBG_XIN, s->x, c.dim)) return -1;   // the embedding row it gathered
+        if (snap(l, DBG_QKV, s->qkv, qd + 2 * kvd)) return -1;
         if (enq_attn_decode(s, l)) return -1;
+        if (snap(l, DBG_O, s->o, qd)) return -1;
         MatvecArgs b{};
         b.W = y.wo; b.units = c.dim; b.in = s->o; b.out = s->x;
         if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, b)) return -1;
+        if (snap(l, DBG_XMID, s->x, c.dim)) return -1;
         if (enq_w13(s, l)) return -1;
+        if (snap(l, DBG_H, s->h, c.hidden_dim)) return -1;
         MatvecArgs d{};
         d.W = y.w2; d.units = c.dim; d.in = s->h; d.out = s->x;
         if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, d)) return -1;
+        if (snap(l, DBG_XOUT, s->x, c.dim)) return -1;
     }
     return 0;
 }
@@ -577,19 +605,26 @@ static int run_step(EhipState *s) {
 extern "C" float *ehip_forward(EhipState *s, int tok, int pos) {
     s->tokpos_h[0] = tok;
     s->tokpos_h[1] = pos;
-    if (run_step(s)) return nullptr;
-    HCHK(hipStreamSynchronize(s->st), nullptr);
-    int flag;
-    memcpy(&flag, s->logits_h + s->m->cfg.vocab_size, 4);
-    if (xm_check(s, flag)) return nullptr;
-    return s->logits_h;
+    for (int attempt = 0; attempt < 2; attempt++) {
+        if (run_step(s)) return nullptr;
+        HCHK(hipStreamSynchronize(s->st), nullptr);
+        int flag;
+        memcpy(&flag, s->logits_h + s->m->cfg.vocab_size, 4);
+        if (!flag) return s->logits_h;
+        if (!s->xm_on || xm_fallback(s)) break;   // re-run the step on the two-kernel schedule
+    }
+    set_err("decode attention: the chunk merge reported an error on the two-kernel schedule");
+    return nullptr;
 }
 
-// The error flag after a device-held loop.
+// The error flag after a device-held loop: 0 clear, 1 raised (and the state
+// switched to the two-kernel schedule: re-run the loop), -1 failure.
 static int xm_flag(EhipState *s) {
     int flag = 0;
     HCHK(hipMemcpy(&flag, s->xm_err, 4, hipMemcpyDeviceToHost), -1);
-    return xm_check(s, flag);
+    if (!flag) return 0;
+    if (!s->xm_on) { set_err("decode attention: the chunk merge reported an error on the two-kernel schedule"); return -1; }
+    return xm_fallback(s) ? -1 : 1;
 }
 
 // One step of the device-resident greedy loop: the decode launches, then the
@@ -612,8 +647,19 @@ static int enq_gen_step(EhipState *s) {
     return 0;
 }
 
-// Enqueue n steps of a device loop: graphs of GEN_UNROLL steps, then single
-// steps (each captured on first use), or plain launches without graphs.
+// A device loop of n steps replays graphs of GEN_UNROLL steps, then single
+// steps.  prepare_steps captures and instantiates the graphs the loop will
+// replay (once per state and parameter set), so that run_steps, which the
+// callers bracket with their timing events, only launches them; without
+// graphs run_steps enqueues the plain launches.
+template <class F>
+static int prepare_steps(EhipState *s, StepGraph (&gr)[2], int n, F enq) {
+    if (!s->graph_mode) return 0;
+    if (n / GEN_UNROLL && !gr[1].x && graph_capture(s, gr[1], GEN_UNROLL, enq)) return -1;
+    if (n % GEN_UNROLL && !gr[0].x && graph_capture(s, gr[0], 1, enq)) return -1;
+    return 0;
+}
+
 template <class F>
 static int run_steps(EhipState *s, StepGraph (&gr)[2], int n, F enq) {
     if (!s->graph_mode) {
@@ -622,25 +668,36 @@ static int run_steps(EhipState *s, StepGraph (&gr)[2], int n, F enq) {
         return 0;
     }
     const int big = n / GEN_UNROLL, small = n % GEN_UNROLL;
-    if (big && !gr[1].x && graph_capture(s, gr[1], GEN_UNROLL, enq)) return -1;
-    if (small && !gr[0].x && graph_capture(s, gr[0], 1, enq)) return -1;
+    if ((big && !gr[1].x) || (small && !gr[0].x)) { set_err("device loop: graphs not prepared"); return -1; }
     for (int i = 0; i < big; i++) HCHK(hipGraphLaunch(gr[1].x, s->st), -1);
     for (int i = 0; i < small; i++) HCHK(hipGraphLaunch(gr[0].x, s->st), -1);
     return 0;
 }
 
+static int generate_greedy_once(EhipState *s, int tok, int pos, int n, int *out_tokens, float *ms);
+
 extern "C" int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *out_tokens, float *ms) {
     const int V = s->m->cfg.vocab_size;
     if (n <= 0 || pos < 0 || (long)pos + n > s->ctx) { set_err("generate: positions %d..%d exceed the context of %d", pos, pos + n - 1, s->ctx); return -1; }
     if (tok < 0 || tok >= V) { set_err("generate: token id %d out of range [0,%d)", tok, V); return -1; }
+    int rc = generate_greedy_once(s, tok, pos, n, out_tokens, ms);
+    if (rc == 1) rc = generate_greedy_once(s, tok, pos, n, out_tokens, ms);   // after the schedule fallback
+    return rc == 0 ? 0 : -1;
+}
+
+// One run of the greedy loop: 0, 1 when the fused merge's check fired (the
+// state has switched schedules; nothing was returned), or -1.
+static int generate_greedy_once(EhipState *s, int tok, int pos, int n, int *out_tokens, float *ms) {
     s->tokpos_h[0] = tok;
     s->tokpos_h[1] = pos;
     s->tokpos_h[2] = 0;
     s->tokpos_h[3] = 0;
+    auto enq = [&]() { return enq_gen_step(s); };
+    if (prepare_steps(s, s->gen, n, enq)) return -1;
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
     HCHK(hipStreamSynchronize(s->st), -1);
     HCHK(hipEventRecord(s->ev0, s->st), -1);
-    if (run_steps(s, s->gen, n, [&]() { return enq_gen_step(s); })) return -1;
+    if (run_steps(s, s->gen, n, enq)) return -1;
     HCHK(hipEventRecord(s->ev1, s->st), -1);
     HCHK(hipEventSynchronize(s->ev1), -1);
     if (ms) {
@@ -648,7 +705,8 @@ extern "C" int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *
         HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
         *ms = t;
     }
-    if (xm_flag(s)) return -1;
+    const int f = xm_flag(s);
+    if (f) return f;
     if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
     return 0;
 }
@@ -731,12 +789,25 @@ extern "C" int ehip_sample(EhipState *s, const float *logits, int n, EmberSample
     return 0;
 }
 
+static int generate_sampled_once(EhipState *s, int tok, int pos, int n, EmberSampler *smp, int *out_tokens,
+                                 float *ms);
+
 extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, EmberSampler *smp, int *out_tokens,
                                      float *ms) {
     const int V = s->m->cfg.vocab_size;
     if (n <= 0 || pos < 0 || (long)pos + n > s->ctx) { set_err("generate: positions %d..%d exceed the context of %d", pos, pos + n - 1, s->ctx); return -1; }
     if (tok < 0 || tok >= V) { set_err("generate: token id %d out of range [0,%d)", tok, V); return -1; }
     if (!sampler_supported(smp)) { set_err("device sampler: top_k %d outside [1,%d]", smp->top_k, SAMPLE_TOPK_MAX); return -1; }
+    // the host sampler is updated only after a run whose merge check passed,
+    // so a re-run after the schedule fallback starts from the same state
+    int rc = generate_sampled_once(s, tok, pos, n, smp, out_tokens, ms);
+    if (rc == 1) rc = generate_sampled_once(s, tok, pos, n, smp, out_tokens, ms);
+    return rc == 0 ? 0 : -1;
+}
+
+static int generate_sampled_once(EhipState *s, int tok, int pos, int n, EmberSampler *smp, int *out_tokens,
+                                 float *ms) {
+    const int V = s->m->cfg.vocab_size;
     if (sampler_upload(s, smp)) return -1;
     const SampleParams p = sampler_params(smp);
     const int cap = smp->history ? smp->hist_cap : 0;
@@ -769,6 +840,8 @@ extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, Embe
         s->smp_graph_p = p;
         s->smp_graph_cap = cap;
     }
+    if (prepare_steps(s, s->smp, n, enq)) return -1;
+    HCHK(hipStreamSynchronize(s->st), -1);
     HCHK(hipEventRecord(s->ev0, s->st), -1);
     if (run_steps(s, s->smp, n, enq)) return -1;
     HCHK(hipEventRecord(s->ev1, s->st), -1);
@@ -778,8 +851,9 @@ extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, Embe
         HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
         *ms = t;
     }
+    const int f = xm_flag(s);
+    if (f) return f;
     if (sampler_download(s, smp)) return -1;
-    if (xm_flag(s)) return -1;
     if (out_tokens) HCHK(hipMemcpy(out_tokens, s->gen_tok, 4 * (size_t)n, hipMemcpyDeviceToHost), -1);
     return 0;
 }
@@ -799,11 +873,23 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             q.norm_w = y.attn_norm; q.eps = c.norm_eps;
             if (l == 0) { q.ids = s->ids_d; q.emb = m->emb; q.x_out = s->X; }
             q.xf = m->any_f32 ? s->xf : nullptr; q.qx = s->qx; q.dx = s->dxp; q.xs = s->xsum;
+            // copies of the captured layer's tensors of this pass
+            const bool snap = l == s->pdbg_layer && c0 / s->pf_chunk == s->pdbg_pass;
+            auto psnap = [&](int slot, const float *src, int stride, int width) -> int {
+                if (!snap) return 0;
+                HCHK(hipMemcpy2DAsync(s->pdbg[slot], 4 * (size_t)width, src, 4 * (size_t)stride, 4 * (size_t)width,
+                                      mt, hipMemcpyDeviceToDevice, s->st), -1);
+                return 0;
+            };
+            if (snap) { s->pdbg_n = mt; s->pdbg_pos = start + c0; }
+            if (l > 0 && psnap(DBG_XIN, s->X, c.dim, c.dim)) return nullptr;
             int rc = launch_quant_rows(s->st, q);
+            if (l == 0 && psnap(DBG_XIN, s->X, c.dim, c.dim)) return nullptr;   // the embedded rows
             GemmArgs g{};
             g.W = y.qkv; g.units = stride; g.n = mt; g.qx = s->qx; g.dx = s->dxp; g.xs = s->xsum; g.xf = q.xf;
             g.out = s->QKV; g.out_stride = stride; g.bias = y.bias_qkv;
             rc |= launch_gemm(s->st, EPI_STORE, g);
+            if (psnap(DBG_QKV, s->QKV, stride, stride)) return nullptr;
             QkPostArgs p{};
             p.qkv = s->QKV; p.stride = stride; p.q_norm = y.q_norm; p.k_norm = y.k_norm;
             p.rope = s->rope; p.eps = c.norm_eps; p.rope_style = c.rope_style;
@@ -816,6 +902,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
             at.ldk = attn_prefill_ldk(start + c0, mt);
             rc |= launch_attention(s->st, s->f16kv, at);
+            if (psnap(DBG_O, s->O, qd, qd)) return nullptr;
             QuantRowsArgs q2{};
             q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;
             q2.xf = q.xf; q2.qx = s->qx; q2.dx = s->dxp; q2.xs = s->xsum;
@@ -824,6 +911,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             g2.W = y.wo; g2.units = c.dim; g2.n = mt; g2.qx = s->qx; g2.dx = s->dxp; g2.xs = s->xsum;
             g2.xf = q.xf; g2.out = s->X; g2.out_stride = c.dim;
             rc |= launch_gemm(s->st, EPI_RESID, g2);
+            if (psnap(DBG_XMID, s->X, c.dim, c.dim)) return nullptr;
             QuantRowsArgs q3 = q;
             q3.ids = nullptr; q3.norm_w = y.ffn_norm;
             rc |= launch_quant_rows(s->st, q3);
@@ -831,6 +919,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             g3.W = y.w13; g3.units = 2 * hid; g3.n = mt; g3.qx = s->qx; g3.dx = s->dxp; g3.xs = s->xsum;
             g3.xf = q.xf; g3.out = s->H; g3.out_stride = 2 * hid;
             rc |= launch_gemm(s->st, EPI_STORE, g3);
+            if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return nullptr;
             QuantRowsArgs q4{};
             q4.x = s->H; q4.x_stride = 2 * hid; q4.cols = hid; q4.n = mt; q4.swiglu = 1;
             q4.xf = q.xf; q4.qx = s->qx; q4.dx = s->dxp; q4.xs = s->xsum;
@@ -839,6 +928,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             g4.W = y.w2; g4.units = c.dim; g4.n = mt; g4.qx = s->qx; g4.dx = s->dxp; g4.xs = s->xsum;
             g4.xf = q.xf; g4.out = s->X; g4.out_stride = c.dim;
             rc |= launch_gemm(s->st, EPI_RESID, g4);
+            if (psnap(DBG_XOUT, s->X, c.dim, c.dim)) return nullptr;
             if (rc) { set_err("a prefill kernel could not be launched for this shape"); return nullptr; }
         }
         if (c0 + mt == n) {
@@ -882,6 +972,80 @@ extern "C" int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t b
     HCHK(hipMemcpy(host, src[which], bytes, hipMemcpyDeviceToHost), -1);
     return 0;
 }
+
+static void drop_step_graphs(EhipState *s) {
+    (void)hipStreamSynchronize(s->st);
+    if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    s->gexec = nullptr;
+    s->graph = nullptr;
+    for (StepGraph &g : s->gen) graph_free(g);
+    for (StepGraph &g : s->smp) graph_free(g);
+}
+
+extern "C" int ehip_debug_capture(EhipState *s, int layer) {
+    const EhipConfig &c = s->m->cfg;
+    if (layer < -1 || layer >= c.n_layers) { set_err("debug_capture: layer %d out of range", layer); return -1; }
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const size_t len[6] = { (size_t)c.dim, (size_t)(qd + 2 * kvd), (size_t)qd, (size_t)c.dim,
+                            (size_t)c.hidden_dim, (size_t)c.dim };
+    for (int i = 0; i < 6 && layer >= 0; i++)
+        if (!s->dbg[i] && !(s->dbg[i] = (float *)salloc(s, 4 * len[i], true))) {
+            set_err("debug_capture: allocation failed");
+            return -1;
+        }
+    drop_step_graphs(s);   // captured graphs hold the previous choice
+    s->dbg_layer = layer;
+    return 0;
+}
+
+extern "C" int ehip_debug_read(EhipState *s, int slot, void *host, uint64_t bytes) {
+    const EhipConfig &c = s->m->cfg;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const uint64_t len[6] = { 4ull * c.dim, 4ull * (qd + 2 * kvd), 4ull * qd, 4ull * c.dim,
+                              4ull * c.hidden_dim, 4ull * c.dim };
+    if (slot < 0 || slot > 5 || !s->dbg[slot] || bytes > len[slot]) { set_err("debug_read: bad request"); return -1; }
+    HCHK(hipStreamSynchronize(s->st), -1);
+    HCHK(hipMemcpy(host, s->dbg[slot], bytes, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
+// widths of the prefill capture slots (per token)
+static void pdbg_widths(const EhipConfig &c, size_t w[6]) {
+    const size_t qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+    w[DBG_XIN] = c.dim; w[DBG_QKV] = qd + 2 * kvd; w[DBG_O] = qd;
+    w[DBG_XMID] = c.dim; w[DBG_H] = 2 * (size_t)c.hidden_dim; w[DBG_XOUT] = c.dim;
+}
+
+extern "C" int ehip_debug_capture_prefill(EhipState *s, int layer, int pass) {
+    const EhipConfig &c = s->m->cfg;
+    if (layer < -1 || layer >= c.n_layers || pass < 0) { set_err("debug_capture_prefill: bad layer or pass"); return -1; }
+    size_t w[6];
+    pdbg_widths(c, w);
+    for (int i = 0; i < 6 && layer >= 0; i++)
+        if (!s->pdbg[i] && !(s->pdbg[i] = (float *)salloc(s, 4 * w[i] * (size_t)s->pf_chunk, true))) {
+            set_err("debug_capture_prefill: allocation failed");
+            return -1;
+        }
+    s->pdbg_layer = layer;
+    s->pdbg_pass = pass;
+    s->pdbg_n = 0;
+    return 0;
+}
+
+extern "C" int ehip_debug_read_prefill(EhipState *s, int slot, void *host, uint64_t bytes, int *n_tok, int *pos0) {
+    size_t w[6];
+    pdbg_widths(s->m->cfg, w);
+    if (slot < 0 || slot > 5 || !s->pdbg[slot]) { set_err("debug_read_prefill: bad request"); return -1; }
+    if (n_tok) *n_tok = s->pdbg_n;
+    if (pos0) *pos0 = s->pdbg_pos;
+    if (bytes > 4 * w[slot] * (size_t)s->pdbg_n) { set_err("debug_read_prefill: %llu bytes requested", (unsigned long long)bytes); return -1; }
+    HCHK(hipStreamSynchronize(s->st), -1);
+    if (bytes) HCHK(hipMemcpy(host, s->pdbg[slot], bytes, hipMemcpyDeviceToHost), -1);
+    return 0;
+}
+
+extern "C" int ehip_prefill_pass_tokens(const EhipState *s) { return s->pf_chunk; }
 
 extern "C" int ehip_decode_fusion(const EhipState *s) {
     return s->xm_on ? 1 : 0;

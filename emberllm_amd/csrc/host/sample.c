@@ -16,72 +16,87 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* seed 0 selects this fixed nonzero state (a zero xorshift state stays zero) */
+#define RNG_ZERO_SEED 0x9E3779B97F4A7C15ULL
+
 void ember_sampler_init(EmberSampler *s, float temp, float top_p, int top_k, uint64_t seed) {
-    s->temperature = temp;
-    s->top_p = top_p;
-    s->top_k = top_k;
-    s->min_p = 0.0f;
-    s->repeat_penalty = 1.0f;
-    s->presence_penalty = 0.0f;
-    s->frequency_penalty = 0.0f;
-    s->repeat_last_n = 0;
-    s->rng_state = seed ? seed : 0x9E3779B97F4A7C15ULL;
-    s->history = NULL;
-    s->hist_cap = s->hist_len = s->hist_pos = 0;
+    /* every penalty starts at its no-op value; no history ring */
+    const EmberSampler fresh = {
+        .temperature = temp,
+        .top_p = top_p,
+        .top_k = top_k,
+        .repeat_penalty = 1.0f,
+        .rng_state = seed != 0 ? seed : RNG_ZERO_SEED,
+    };
+    *s = fresh;
+}
+
+/* Give the history ring `cap` slots (cap <= 0 releases it) and empty it. */
+static void ring_resize(EmberSampler *s, int cap) {
+    if (cap <= 0) {
+        free(s->history);
+        s->history = NULL;
+        s->hist_cap = 0;
+    } else if (cap != s->hist_cap) {
+        s->history = ember_xrealloc(s->history, sizeof(int) * (size_t)cap, "sampler history ring");
+        s->hist_cap = cap;
+    }
+    s->hist_len = 0;
+    s->hist_pos = 0;
 }
 
 void ember_sampler_set_penalties(EmberSampler *s, float repeat_penalty, int repeat_last_n,
                                  float presence_penalty, float frequency_penalty, float min_p) {
     s->repeat_penalty = repeat_penalty;
+    s->repeat_last_n = repeat_last_n;
     s->presence_penalty = presence_penalty;
     s->frequency_penalty = frequency_penalty;
     s->min_p = min_p;
-    s->repeat_last_n = repeat_last_n;
-    const int keep = repeat_last_n > 0 &&
-        (repeat_penalty != 1.0f || presence_penalty != 0.0f || frequency_penalty != 0.0f);
-    if (!keep) {
-        free(s->history);
-        s->history = NULL;
-        s->hist_cap = 0;
-    } else if (s->hist_cap != repeat_last_n) {
-        s->history = ember_xrealloc(s->history, sizeof(int) * (size_t)repeat_last_n, "sampler history");
-        s->hist_cap = repeat_last_n;
-    }
-    s->hist_len = s->hist_pos = 0;
+    /* a ring is kept only when some penalty would read it */
+    const int reads_history = repeat_penalty != 1.0f || presence_penalty != 0.0f || frequency_penalty != 0.0f;
+    ring_resize(s, reads_history ? repeat_last_n : 0);
 }
 
 void ember_sampler_accept(EmberSampler *s, int token) {
-    if (!s->history || s->hist_cap == 0) return;
+    if (s->history == NULL || s->hist_cap <= 0) return;
     s->history[s->hist_pos] = token;
-    s->hist_pos = (s->hist_pos + 1) % s->hist_cap;
-    if (s->hist_len < s->hist_cap) s->hist_len++;
+    s->hist_pos = s->hist_pos + 1 < s->hist_cap ? s->hist_pos + 1 : 0;
+    if (s->hist_len < s->hist_cap) s->hist_len += 1;
 }
 
-void ember_sampler_reset(EmberSampler *s) { s->hist_len = s->hist_pos = 0; }
+void ember_sampler_reset(EmberSampler *s) {
+    s->hist_len = 0;
+    s->hist_pos = 0;
+}
 
 void ember_sampler_free(EmberSampler *s) {
-    if (!s) return;
-    free(s->history);
-    s->history = NULL;
-    s->hist_cap = s->hist_len = s->hist_pos = 0;
+    if (s != NULL) ring_resize(s, 0);
 }
 
-/* repetition / presence once per distinct token, frequency per occurrence */
+/* Penalties over the ring's hist_len valid entries (src/sample.c:76-96).
+ * Each distinct in-range token t is handled once, at its first entry: the
+ * repetition penalty (divide a positive logit, multiply a negative one) and
+ * the presence penalty, then the frequency penalty subtracted once per entry
+ * holding t.  Per logit that is the reference's sequence of operations, so
+ * the results are bit-identical; different logits are independent. */
 static void penalize(EmberSampler *s, float *logits, int n) {
-    if (!s->history || s->hist_len == 0) return;
     const int rep = s->repeat_penalty != 1.0f, pres = s->presence_penalty != 0.0f,
               freq = s->frequency_penalty != 0.0f;
-    if (!rep && !pres && !freq) return;
-    for (int i = 0; i < s->hist_len; i++) {
-        const int t = s->history[i];
+    if (s->history == NULL || s->hist_len <= 0 || !(rep || pres || freq)) return;
+    const int *h = s->history, len = s->hist_len;
+    for (int i = 0; i < len; i++) {
+        const int t = h[i];
         if (t < 0 || t >= n) continue;
-        int repeat = 0;
-        for (int j = 0; j < i && !repeat; j++) repeat = s->history[j] == t;
-        if (!repeat) {
-            if (rep) logits[t] = logits[t] > 0.0f ? logits[t] / s->repeat_penalty : logits[t] * s->repeat_penalty;
-            if (pres) logits[t] -= s->presence_penalty;
-        }
-        if (freq) logits[t] -= s->frequency_penalty;
+        int seen = 0;
+        for (int j = 0; j < i && !seen; j++) seen = h[j] == t;
+        if (seen) continue;
+        float v = logits[t];
+        if (rep) v = v > 0.0f ? v / s->repeat_penalty : v * s->repeat_penalty;
+        if (pres) v -= s->presence_penalty;
+        if (freq)
+            for (int k = i; k < len; k++)
+                if (h[k] == t) v -= s->frequency_penalty;
+        logits[t] = v;
     }
 }
 

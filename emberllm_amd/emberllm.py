@@ -1,18 +1,15 @@
-"""Python binding over libember.so with the reference binding's API.
+"""numpy-level view of libember.so for the tests and the benchmark.
 
-``Ember`` keeps the class surface of bindings/python/emberllm.py:112-201
-(constructor arguments, ``encode``, ``decode``, ``generate``,
-``generate_str``, ``close``, context management); it samples through the
-library's ember_sample rather than in Python.
-``Engine`` is the numpy-level view used by the tests and the benchmark.
+``Engine`` holds one loaded model and one device state and returns numpy
+arrays; besides the ember.h calls it reaches the device layer's loops and
+measurement hooks (ehip.h).  Applications keep using the reference's own
+ctypes binding (bindings/python/emberllm.py), which loads this library
+unchanged through EMBER_LIB.
 """
 import ctypes
 import numpy as np
 
 from . import _native
-
-_libc = ctypes.CDLL(None)
-_libc.free.argtypes = [ctypes.c_void_p]
 
 
 class Engine:
@@ -62,6 +59,44 @@ class Engine:
         if self.lib.ehip_debug_buffer(self.dev, which, out.ctypes.data, out.nbytes) != 0:
             raise RuntimeError(_native.last_error())
         return out
+
+    def debug_capture(self, layer):
+        """Record `layer`'s intermediate vectors in the following decode steps
+        (-1 stops); see ehip_debug_capture."""
+        if self.lib.ehip_debug_capture(self.dev, int(layer)) != 0:
+            raise RuntimeError(_native.last_error())
+
+    def debug_read(self, slot):
+        """One recorded vector (ehip_debug_capture slot 0..5) as float32."""
+        h = self.header
+        qd, kvd = h.n_heads * h.head_dim, h.n_kv_heads * h.head_dim
+        n = (h.dim, qd + 2 * kvd, qd, h.dim, h.hidden_dim, h.dim)[slot]
+        out = np.empty(n, dtype=np.float32)
+        if self.lib.ehip_debug_read(self.dev, int(slot), out.ctypes.data, out.nbytes) != 0:
+            raise RuntimeError(_native.last_error())
+        return out
+
+    def debug_capture_prefill(self, layer, pass_index=0):
+        """Record `layer` of prefill pass `pass_index` in the following
+        prefills (-1 stops); see ehip_debug_capture_prefill."""
+        if self.lib.ehip_debug_capture_prefill(self.dev, int(layer), int(pass_index)) != 0:
+            raise RuntimeError(_native.last_error())
+
+    def debug_read_prefill(self, slot):
+        """(rows [n_tok][width] float32, first position) of a recorded slot."""
+        h = self.header
+        qd, kvd = h.n_heads * h.head_dim, h.n_kv_heads * h.head_dim
+        width = (h.dim, qd + 2 * kvd, qd, h.dim, 2 * h.hidden_dim, h.dim)[slot]
+        n, p0 = ctypes.c_int(), ctypes.c_int()
+        if self.lib.ehip_debug_read_prefill(self.dev, int(slot), None, 0, ctypes.byref(n), ctypes.byref(p0)) != 0:
+            raise RuntimeError(_native.last_error())
+        out = np.empty((n.value, width), dtype=np.float32)
+        if self.lib.ehip_debug_read_prefill(self.dev, int(slot), out.ctypes.data, out.nbytes, None, None) != 0:
+            raise RuntimeError(_native.last_error())
+        return out, p0.value
+
+    def prefill_pass_tokens(self):
+        return self.lib.ehip_prefill_pass_tokens(self.dev)
 
     def set_graph(self, on):
         self.lib.ehip_set_graph_mode(self.dev, 1 if on else 0)
@@ -127,88 +162,6 @@ class Engine:
             self.st = None
         if getattr(self, "m", None):
             self.lib.ember_model_free(self.m)
-            self.m = None
-
-    def __enter__(self):
-        return self
-
-    def __exit__(self, *exc):
-        self.close()
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
-
-
-class Ember:
-    """A loaded model plus its tokenizer and one reusable run state."""
-
-    def __init__(self, path, ctx=0, kv_fp16=False):
-        self._lib = _native.lib()
-        self.m = self._lib.ember_model_load(path.encode())
-        if not self.m:
-            raise RuntimeError(f"failed to load model: {path}")
-        self.header = self._lib.ember_model_header(self.m).contents
-        self.tok = self._lib.ember_tokenizer_new(self.m)
-        self.st = self._lib.ember_state_new_ex(self.m, int(ctx), 1 if kv_fp16 else 0)
-        maxs = self.header.max_seq_len
-        self.ctx = maxs if ctx <= 0 or ctx > maxs else ctx
-
-    def encode(self, text, add_bos=True):
-        out = ctypes.POINTER(ctypes.c_int)()
-        n = self._lib.ember_encode(self.tok, text.encode(), 1 if add_bos else 0, ctypes.byref(out))
-        ids = [out[i] for i in range(n)]
-        _libc.free(ctypes.cast(out, ctypes.c_void_p))
-        return ids
-
-    def decode(self, prev, tok):
-        s = self._lib.ember_decode(self.tok, prev, tok)
-        return s.decode("utf-8", "replace") if s else ""
-
-    def generate(self, prompt, max_tokens=128, temperature=0.0, top_k=0, seed=None):
-        """Yield decoded text pieces one token at a time.
-
-        Sampling runs in the library (ember_sample) on the returned logits,
-        with top-p off; `seed` seeds its xorshift64* stream.
-        """
-        ids = self.encode(prompt)
-        if len(ids) >= self.ctx:
-            ids = ids[: self.ctx - 1]
-        arr = (ctypes.c_int * len(ids))(*ids)
-        smp = _native.EmberSampler()
-        self._lib.ember_sampler_init(ctypes.byref(smp), float(temperature), 1.0, int(top_k),
-                                     int(seed or 0) & 0xFFFFFFFFFFFFFFFF)
-        stops = {self.header.eos_token_id, self.header.eos_token_id2, self.header.bos_token_id}
-        logits = self._lib.ember_prefill(self.m, self.st, arr, len(ids), 0)
-        prev, pos = ids[-1], len(ids)
-        try:
-            for _ in range(max_tokens):
-                nxt = self._lib.ember_sample(ctypes.byref(smp), logits, self.header.vocab_size)
-                if nxt in stops:
-                    return
-                yield self.decode(prev, nxt)
-                prev = nxt
-                if pos >= self.ctx - 1:
-                    return
-                logits = self._lib.ember_forward(self.m, self.st, nxt, pos)
-                pos += 1
-        finally:
-            self._lib.ember_sampler_free(ctypes.byref(smp))
-
-    def generate_str(self, prompt, **kw):
-        return "".join(self.generate(prompt, **kw))
-
-    def close(self):
-        if getattr(self, "st", None):
-            self._lib.ember_state_free(self.st)
-            self.st = None
-        if getattr(self, "tok", None):
-            self._lib.ember_tokenizer_free(self.tok)
-            self.tok = None
-        if getattr(self, "m", None):
-            self._lib.ember_model_free(self.m)
             self.m = None
 
     def __enter__(self):

@@ -113,6 +113,29 @@ int ehip_kv_write(EhipState *s, int which, int layer, int n_pos, const void *hos
  * residual stream x [dim], 1 the last layer's raw q|k|v, 2 its attention
  * output [n_heads*hd], 3 its SwiGLU output [hidden], 4 logits [vocab]. */
 int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t bytes);
+/* Record one layer's intermediate vectors during every following decode
+ * step (ember_forward / ehip_forward and the device loops; layer -1 stops
+ * recording).  Slots, each fp32, as the layer computes them (the layer
+ * structure of src/model.c:374-409):
+ *   0 the residual stream entering the layer [dim] (layer 0: the embedding row)
+ *   1 the raw q|k|v product, bias added [n_heads*hd + 2*kv_dim]
+ *   2 the attention output [n_heads*hd]
+ *   3 the residual after wo [dim]
+ *   4 the SwiGLU output [hidden]
+ *   5 the residual after w2 [dim]
+ * No counterpart in the reference: a test hook for checking each decode
+ * kernel at full model shapes against a recomputation on the same inputs.
+ * Changing the layer drops the state's captured step graphs. */
+int ehip_debug_capture(EhipState *s, int layer);
+int ehip_debug_read(EhipState *s, int slot, void *host, uint64_t bytes);
+/* The same for prefill: record `layer` of prefill pass `pass` (passes cover
+ * ehip_prefill_pass_tokens() tokens each) in the following ehip_prefill
+ * calls, as [n_tok][width] fp32 rows; slot 4 holds the w1|w3 product before
+ * SwiGLU ([n_tok][2*hidden], the w1 rows first).  ehip_debug_read_prefill
+ * also returns the pass's token count and first position. */
+int ehip_debug_capture_prefill(EhipState *s, int layer, int pass);
+int ehip_debug_read_prefill(EhipState *s, int slot, void *host, uint64_t bytes, int *n_tok, int *pos0);
+int ehip_prefill_pass_tokens(const EhipState *s);
 /* 0: eager launches, 1: one hipGraph per decode step (default). */
 int ehip_set_graph_mode(EhipState *s, int mode);
 /* How the state's decode step is scheduled: bit 0 = the attention kernel

@@ -345,6 +345,8 @@ struct OrcState {
     float *x, *xb, *xb2, *hb, *hb2, *q, *k, *v, *att, *logits;
     void *kc, *vc;
     Q8Blk *xq;
+    int cap_layer;        /* orc_capture: layer whose vectors are copied out, or -1 */
+    float *cap[6];
 };
 
 OrcState *orc_state_new(OrcModel *m, int ctx_len, int kv_fp16) {
@@ -388,7 +390,18 @@ OrcState *orc_state_new(OrcModel *m, int ctx_len, int kv_fp16) {
     s->kc = calloc(1, kvb); s->vc = calloc(1, kvb);
     if (!s->kc || !s->vc || !s->logits) fatal("out of memory (kv)");
     s->xq = xalloc(sizeof(Q8Blk) * (size_t)(wide / QB + 1));
+    s->cap_layer = -1;
     return s;
+}
+
+void orc_capture(OrcState *s, int layer, float *const *slots) {
+    s->cap_layer = layer;
+    for (int i = 0; i < 6; i++) s->cap[i] = slots ? slots[i] : NULL;
+}
+
+/* copy n floats to capture slot i (row `row` of width n) when layer l is captured */
+static void cap_put(OrcState *s, int l, int i, size_t row, const float *src, size_t n) {
+    if (l == s->cap_layer && s->cap[i]) memcpy(s->cap[i] + row * n, src, 4 * n);
 }
 
 void orc_state_free(OrcState *s) {
@@ -507,6 +520,7 @@ float *orc_forward(OrcState *s, int tok, int pos) {
     embed(s, tok, s->x);
     for (int l = 0; l < s->L; l++) {
         Layer *y = &s->ly[l];
+        cap_put(s, l, 0, 0, s->x, (size_t)dim);
         norm(s->xb, s->x, y->an, dim, s->eps);
         matmul_b(s->q, s->xb, y->wq.p, y->wq.dt, dim, qd, 1, s->xq);
         matmul_b(s->k, s->xb, y->wk.p, y->wk.dt, dim, kvd, 1, s->xq);
@@ -514,6 +528,11 @@ float *orc_forward(OrcState *s, int tok, int pos) {
         if (y->bq) add_vec(s->q, y->bq, qd);
         if (y->bk) add_vec(s->k, y->bk, kvd);
         if (y->bv) add_vec(s->v, y->bv, kvd);
+        if (l == s->cap_layer && s->cap[1]) {   /* raw q|k|v */
+            memcpy(s->cap[1], s->q, 4 * (size_t)qd);
+            memcpy(s->cap[1] + qd, s->k, 4 * (size_t)kvd);
+            memcpy(s->cap[1] + qd + kvd, s->v, 4 * (size_t)kvd);
+        }
         if (s->qk && y->qn) {
             for (int h = 0; h < s->nh; h++) norm(s->q + h * hd, s->q + h * hd, y->qn, hd, s->eps);
             for (int h = 0; h < s->nkv; h++) norm(s->k + h * hd, s->k + h * hd, y->kn, hd, s->eps);
@@ -522,14 +541,18 @@ float *orc_forward(OrcState *s, int tok, int pos) {
         rotate(s->k, kvd, hd, pos, s->theta, s->rope_style);
         store_kv(s, l, pos, s->k, s->v);
         attend(s, s->q, s->xb, l, pos);
+        cap_put(s, l, 2, 0, s->xb, (size_t)qd);
         matmul_b(s->xb2, s->xb, y->wo.p, y->wo.dt, qd, dim, 1, s->xq);
         add_vec(s->x, s->xb2, dim);
+        cap_put(s, l, 3, 0, s->x, (size_t)dim);
         norm(s->xb, s->x, y->fn, dim, s->eps);
         matmul_b(s->hb, s->xb, y->w1.p, y->w1.dt, dim, s->hid, 1, s->xq);
         matmul_b(s->hb2, s->xb, y->w3.p, y->w3.dt, dim, s->hid, 1, s->xq);
         for (int i = 0; i < s->hid; i++) { float g = s->hb[i]; s->hb[i] = g / (1.0f + expf(-g)) * s->hb2[i]; }
+        cap_put(s, l, 4, 0, s->hb, (size_t)s->hid);
         matmul_b(s->xb, s->hb, y->w2.p, y->w2.dt, s->hid, dim, 1, s->xq);
         add_vec(s->x, s->xb, dim);
+        cap_put(s, l, 5, 0, s->x, (size_t)dim);
     }
     norm(s->x, s->x, s->fnorm, dim, s->eps);
     matmul_b(s->logits, s->x, s->head.p, s->head.dt, dim, s->V, 1, s->xq);
@@ -555,6 +578,7 @@ float *orc_prefill(OrcState *s, const int *ids, int n, int start) {
     }
     for (int l = 0; l < s->L; l++) {
         Layer *y = &s->ly[l];
+        for (int b = 0; b < n; b++) cap_put(s, l, 0, (size_t)b, X + (size_t)b * dim, (size_t)dim);
         for (int b = 0; b < n; b++) norm(Xn + (size_t)b * dim, X + (size_t)b * dim, y->an, dim, s->eps);
         matmul_b(Q, Xn, y->wq.p, y->wq.dt, dim, qd, n, sq);
         matmul_b(K, Xn, y->wk.p, y->wk.dt, dim, kvd, n, sq);
@@ -564,6 +588,13 @@ float *orc_prefill(OrcState *s, const int *ids, int n, int start) {
             if (y->bk) add_vec(K + (size_t)b * kvd, y->bk, kvd);
             if (y->bv) add_vec(Vv + (size_t)b * kvd, y->bv, kvd);
         }
+        if (l == s->cap_layer && s->cap[1])   /* raw q|k|v rows */
+            for (int b = 0; b < n; b++) {
+                float *r = s->cap[1] + (size_t)b * (qd + 2 * kvd);
+                memcpy(r, Q + (size_t)b * qd, 4 * (size_t)qd);
+                memcpy(r + qd, K + (size_t)b * kvd, 4 * (size_t)kvd);
+                memcpy(r + qd + kvd, Vv + (size_t)b * kvd, 4 * (size_t)kvd);
+            }
         for (int b = 0; b < n; b++) {
             float *qb = Q + (size_t)b * qd, *kb = K + (size_t)b * kvd;
             if (s->qk && y->qn) {
@@ -575,14 +606,22 @@ float *orc_prefill(OrcState *s, const int *ids, int n, int start) {
             store_kv(s, l, start + b, kb, Vv + (size_t)b * kvd);
         }
         for (int b = 0; b < n; b++) attend(s, Q + (size_t)b * qd, O + (size_t)b * qd, l, start + b);
+        for (int b = 0; b < n; b++) cap_put(s, l, 2, (size_t)b, O + (size_t)b * qd, (size_t)qd);
         matmul_b(T, O, y->wo.p, y->wo.dt, qd, dim, n, sq);
         for (size_t i = 0; i < N * dim; i++) X[i] += T[i];
+        for (int b = 0; b < n; b++) cap_put(s, l, 3, (size_t)b, X + (size_t)b * dim, (size_t)dim);
         for (int b = 0; b < n; b++) norm(Xn + (size_t)b * dim, X + (size_t)b * dim, y->fn, dim, s->eps);
         matmul_b(H1, Xn, y->w1.p, y->w1.dt, dim, hid, n, sq);
         matmul_b(H2, Xn, y->w3.p, y->w3.dt, dim, hid, n, sq);
+        if (l == s->cap_layer && s->cap[4])   /* w1 | w3 products before SwiGLU */
+            for (int b = 0; b < n; b++) {
+                memcpy(s->cap[4] + (size_t)b * 2 * hid, H1 + (size_t)b * hid, 4 * (size_t)hid);
+                memcpy(s->cap[4] + (size_t)b * 2 * hid + hid, H2 + (size_t)b * hid, 4 * (size_t)hid);
+            }
         for (size_t i = 0; i < N * hid; i++) { float g = H1[i]; H1[i] = g / (1.0f + expf(-g)) * H2[i]; }
         matmul_b(T, H1, y->w2.p, y->w2.dt, hid, dim, n, sq);
         for (size_t i = 0; i < N * dim; i++) X[i] += T[i];
+        for (int b = 0; b < n; b++) cap_put(s, l, 5, (size_t)b, X + (size_t)b * dim, (size_t)dim);
     }
     norm(s->x, X + (size_t)(n - 1) * dim, s->fnorm, dim, s->eps);
     matmul_b(s->logits, s->x, s->head.p, s->head.dt, dim, s->V, 1, s->xq);

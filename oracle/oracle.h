@@ -61,6 +61,14 @@ float    *orc_prefill(OrcState *s, const int *ids, int n, int start);
 /* raw KV cache access: which = 0 keys, 1 values; layout [L][ctx][kv_dim] of
  * fp32 or fp16 (per kv_fp16).  Used to hand a GPU-filled cache to the oracle. */
 void     *orc_kv_cache(OrcState *s, int which);
+/* Copy layer `layer`'s vectors out during the following orc_forward /
+ * orc_prefill calls (layer -1 or slots NULL: stop).  slots[i] (NULL to skip)
+ * receives per token, as [n][width] rows: 0 the residual entering the layer,
+ * 1 the raw q|k|v after bias, 2 the attention output, 3 the residual after
+ * wo, 4 the SwiGLU output (orc_forward) or the w1|w3 products before it
+ * ([n][2*hidden], orc_prefill), 5 the residual after w2.  The same slots as
+ * the GPU layer's debug capture, for checking the checker itself. */
+void      orc_capture(OrcState *s, int layer, float *const *slots);
 uint64_t  orc_kv_bytes(const OrcState *s);
 
 void orc_sampler_init(OrcSampler *s, float temp, float top_p, int top_k, uint64_t seed);

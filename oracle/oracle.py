@@ -51,6 +51,7 @@ _ORC = {
     "orc_forward": (_FP, [_P, ctypes.c_int, ctypes.c_int]),
     "orc_prefill": (_FP, [_P, _IP, ctypes.c_int, ctypes.c_int]),
     "orc_kv_cache": (_P, [_P, ctypes.c_int]),
+    "orc_capture": (None, [_P, ctypes.c_int, ctypes.POINTER(_FP)]),
     "orc_kv_bytes": (ctypes.c_uint64, [_P]),
     "orc_sampler_init": (None, [ctypes.POINTER(Sampler), ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_uint64]),
     "orc_sampler_set_penalties": (None, [ctypes.POINTER(Sampler), ctypes.c_float, ctypes.c_int,
@@ -142,7 +143,8 @@ class Oracle:
         self.ctx = self.L.orc_state_ctx(self.s)
         with open(path, "rb") as f:
             hdr = f.read(256)
-        self.vocab = int(np.frombuffer(hdr[16:48], dtype=np.int32)[6])
+        self._hdr = np.frombuffer(hdr[16:48], dtype=np.int32)
+        self.vocab = int(self._hdr[6])
 
     def forward(self, tok, pos):
         p = self.L.orc_forward(self.s, int(tok), int(pos))
@@ -152,6 +154,23 @@ class Oracle:
         a = np.ascontiguousarray(ids, dtype=np.int32)
         p = self.L.orc_prefill(self.s, intp(a), len(a), int(start))
         return np.ctypeslib.as_array(p, shape=(self.vocab,)).copy()
+
+    def capture(self, layer, n_tok=1, prefill=False):
+        """Record `layer`'s vectors in the following calls (orc_capture) into
+        numpy buffers for n_tok tokens; returns the list of six arrays (slot
+        4 holds the w1|w3 products when prefill is True).  layer -1 stops."""
+        hdr = self._hdr
+        dim, hid, nh, nkv, hd = (int(hdr[i]) for i in (0, 1, 3, 4, 5))
+        qd, kvd = nh * hd, nkv * hd
+        widths = (dim, qd + 2 * kvd, qd, dim, 2 * hid if prefill else hid, dim)
+        self._cap = [np.zeros((n_tok, w), dtype=np.float32) for w in widths]
+        if layer < 0:
+            self.L.orc_capture(self.s, -1, None)
+            return None
+        arr = (_FP * 6)(*[f32p(a) for a in self._cap])
+        self._cap_ptrs = arr
+        self.L.orc_capture(self.s, int(layer), arr)
+        return self._cap
 
     def kv_bytes(self):
         return int(self.L.orc_kv_bytes(self.s))

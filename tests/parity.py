@@ -1,29 +1,34 @@
-"""Tolerances and comparison helpers for GPU-vs-oracle parity.
+"""Tolerances and comparison helpers for end-to-end GPU-vs-oracle parity.
 
-The task's bar is per-step logits within 1e-2 max-abs and 1e-3 relative L2 of
-the reference CPU path, with >= 99% top-1 agreement under teacher forcing.
+The north-star bar is per-step logits within 1e-2 max-abs and 1e-3 relative
+L2 of the reference CPU path, with >= 99% top-1 agreement under teacher
+forcing.  It holds on the small variant models (rel-L2 ~4e-8) and does NOT
+hold end to end on the deep benchmark shapes, where the GPU path differs from
+the reference's deterministic build by ~1e-2 relative L2.
 
-The reference re-quantizes every matmul input to Q8_0 (kernels.c:210-213),
-which makes its forward pass discontinuous: a one-ulp change anywhere (a sum
-taken in another order) can move an fp16 block scale or an int8 code by one
-step, and that step cascades through the following layers.  The reference
-itself shows this: its optimized build (-O3 -ffast-math) deviates from its
-deterministic build (-O2 -fno-fast-math) by up to ~2e-2 relative L2 and ~6e-2
-max-abs on the benchmark shapes, on identical inputs (tests/golden/
-noise_floor.json, made by make_golden.py).  A single code flip, once it
-happens, perturbs the logits by ~1e-2 relative (t_gqa: 1.1e-2 between the
-two reference builds).  So for each teacher-forced case:
+Why: the reference re-quantizes every matmul input to Q8_0
+(src/kernels.c:210-213), which makes its forward pass discontinuous.  A
+one-ulp change anywhere (a sum taken in another order) can move an fp16 block
+scale or an int8 code by one step, and that step cascades through the
+following layers.  The reference itself shows this: its optimized build
+(-O3 -ffast-math) deviates from its deterministic build (-O2 -fno-fast-math)
+by ~1e-2 relative L2 and ~5e-2 max-abs on the benchmark shapes, on identical
+inputs (tests/golden/noise_floor.json, made by make_golden.py).  No
+implementation that sums in another order than the deterministic build can
+meet 1e-3 on those shapes; the GPU's kernels are instead held to 1e-6 of a
+float64 recomputation on their own inputs (tests/test_gpu_kernels.py).
 
-  * the task bar must hold at the median step:
+End-to-end runs are therefore held to the reference's own noise floor at
+the same model shape:
+  * at the median step:
         median rel-L2  <= max(1e-3, 1.5 x the reference builds' median)
         median max-abs <= max(1e-2, 1.5 x the reference builds' median)
-  * no step may exceed the cascade amplitude of one flip:
+  * at every step, within the cascade amplitude of one flip:
         max rel-L2  <= max(1e-2, 1.5 x the reference builds' maximum)
         max max-abs <= max(3e-2, 1.5 x the reference builds' maximum)
-  * top-1 agreement >= min(99%, the optimized reference's own agreement).
-
-A top-1 disagreement is excused when the oracle's top-2 margin is below twice
-that step's max-abs error (a near tie within the noise of the two paths).
+  * top-1 agreement >= min(99%, the optimized reference's own agreement),
+    where a disagreement is excused only when the oracle's top-2 margin is
+    below both twice that step's max-abs error and TIE_MARGIN (a near tie).
 """
 import json
 import os
@@ -35,6 +40,7 @@ REL_L2 = 1e-3
 FLIP_REL_L2 = 1e-2     # amplitude of one activation-code flip (relative L2)
 FLIP_MAX_ABS = 3e-2    # and its max-abs
 SLACK = 1.5
+TIE_MARGIN = 0.02      # largest top-2 logit gap a top-1 disagreement may be excused at
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
@@ -71,7 +77,7 @@ def check_run(results, case_id):
     assert all(r["finite"] for r in results), f"{case_id}: non-finite logits"
     rel = np.array([r["rel_l2"] for r in results])
     mab = np.array([r["max_abs"] for r in results])
-    ok = [r["agree"] or r["margin"] < 2 * r["max_abs"] for r in results]
+    ok = [r["agree"] or r["margin"] < min(2 * r["max_abs"], TIE_MARGIN) for r in results]
     summary = (f"{case_id}: rel-L2 median {np.median(rel):.2e} max {rel.max():.2e}; "
                f"max-abs median {np.median(mab):.2e} max {mab.max():.2e}; "
                f"top-1 {np.mean([r['agree'] for r in results]):.3f} "

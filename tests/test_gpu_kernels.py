@@ -1,0 +1,162 @@
+"""Kernel-level parity at full model shapes, through libember.so's C ABI.
+
+Every decode kernel (q|k|v matvec with its RMSNorm prologue, QK-norm / RoPE
+/ KV store, split-K attention and its merge, wo + residual, w1|w3 + SwiGLU,
+w2 + residual, final norm + lm_head) and every prefill kernel (row
+quantization, the int8 MFMA GEMMs in both tile sizes and the short-prompt
+GEMM, QK post-processing, the prefill attention) is captured on the GPU and
+recomputed in float64 from the model file on the GPU's own inputs
+(tests/kernel_check.py, itself pinned against the oracle on the CPU by
+tests/test_kernel_check.py).  Bound: 1e-6 of the sum of |terms| for
+products, 1e-5 of sum p|v| for attention, after resolving activation codes
+whose rounding an ulp decides.
+
+Workloads (the benchmark configurations): stories110M @128, SmolLM2 @1024,
+Qwen2.5-0.5B @256, Qwen3-0.6B Q8_0 @4096 (both decode-attention schedules),
+Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings; and a
+2-layer Qwen3-width model prefilling 2,300 tokens (one 2048-token pass with
+128-token MFMA tiles, then a 252-token pass at position 2048), also compared
+end to end with the oracle (logits and every layer's KV rows).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import kernel_check as kc
+import oracle
+from emberllm_amd import configs, emberllm
+from parity import compare
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+
+def say(msg):
+    print(f"[gpu-kernels] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def layer_cache(eng, mf, layer, n_pos):
+    kv16 = eng.kv_fp16
+    return (kc.cache_rows(eng.kv_read(0, layer, n_pos), mf, kv16),
+            kc.cache_rows(eng.kv_read(1, layer, n_pos), mf, kv16))
+
+
+WORKLOADS = [("stories110m", 128), ("smollm2_135m", 1024), ("qwen25_05b", 256), ("qwen3_06b", 4096),
+             ("qwen3_06b_q4", 512)]
+
+
+def _decode_kernels(name, depth, kv16=False):
+    path = configs.model_path(name, threads=16)
+    mf = kc.ModelFile(path)
+    rng = np.random.default_rng(depth)
+    ids = rng.integers(0, mf.V, depth)
+    say(f"decode kernels {name} depth {depth} kv16={kv16}")
+    eng = emberllm.Engine(path, ctx=depth + 8, kv_fp16=kv16)
+    eng.prefill(ids)
+    lines, ok = [], True
+    for i, layer in enumerate(sorted({0, mf.L // 2, mf.L - 1})):
+        pos = depth + i
+        eng.debug_capture(layer)
+        logits = eng.forward(int(rng.integers(0, mf.V)), pos)
+        slots = [eng.debug_read(s) for s in range(6)]
+        k, v = layer_cache(eng, mf, layer, pos + 1)
+        rep = kc.Report(f"{name}@{pos} kv16={kv16}")
+        kc.check_decode_layer(rep, mf, layer, slots, pos, k, v, kv16)
+        if layer == mf.L - 1:
+            kc.check_head(rep, mf, slots[5], logits)
+        lines.append(str(rep))
+        ok &= rep.ok
+    eng.debug_capture(-1)
+    eng.close()
+    say("\n".join(lines))
+    return ok, "\n".join(lines)
+
+
+@pytest.mark.parametrize("name,depth", WORKLOADS, ids=[f"{n}@{d}" for n, d in WORKLOADS])
+def test_decode_kernels_at_workload(name, depth):
+    ok, text = _decode_kernels(name, depth)
+    assert ok, text
+
+
+def test_decode_kernels_two_kernel_merge(monkeypatch):
+    """Qwen3-0.6B at depth 4096 with the attention merge as a second kernel
+    (EHIP_XMERGE=0), the schedule used where the XCD placement cannot be
+    verified."""
+    monkeypatch.setenv("EHIP_XMERGE", "0")
+    ok, text = _decode_kernels("qwen3_06b", 4096)
+    assert ok, text
+
+
+def test_decode_kernels_fp16_cache():
+    ok, text = _decode_kernels("qwen3_06b", 1024, kv16=True)
+    assert ok, text
+
+
+def _prefill_kernels(name, n_prompt, captures):
+    """Prefill n_prompt tokens once per (layer, pass) in `captures`, checking
+    that pass's kernels of that layer."""
+    path = configs.model_path(name, threads=16)
+    mf = kc.ModelFile(path)
+    rng = np.random.default_rng(n_prompt)
+    ids = rng.integers(0, mf.V, n_prompt)
+    eng = emberllm.Engine(path, ctx=n_prompt + 8)
+    lines, ok = [], True
+    for layer, pas in captures:
+        say(f"prefill kernels {name} n={n_prompt} layer {layer} pass {pas}")
+        eng.debug_capture_prefill(layer, pas)
+        eng.prefill(ids)
+        slots, pos0 = [], 0
+        for s in range(6):
+            rows, pos0 = eng.debug_read_prefill(s)
+            slots.append(rows)
+        n = slots[0].shape[0]
+        k, v = layer_cache(eng, mf, layer, pos0 + n)
+        rep = kc.Report(f"{name} prefill {n_prompt} pass {pas} (tokens {pos0}..{pos0 + n - 1})")
+        kc.check_prefill_layer(rep, mf, layer, slots, pos0, k, v, False)
+        lines.append(str(rep))
+        ok &= rep.ok
+    eng.debug_capture_prefill(-1, 0)
+    eng.close()
+    say("\n".join(lines))
+    return ok, "\n".join(lines)
+
+
+@pytest.mark.parametrize("name", ["qwen3_06b", "qwen3_06b_q4"])
+def test_prefill_kernels_512(name):
+    """pp512 at the Qwen3-0.6B shape: q|k|v and w1|w3 on the 64-token-tile
+    MFMA GEMM, wo and w2 on the 32x32-tile GEMM, Q8_0 and Q4_0 weights."""
+    ok, text = _prefill_kernels(name, 512, [(0, 0), (27, 0)])
+    assert ok, text
+
+
+@pytest.mark.parametrize("name", ["w_qwen3", "w_qwen3_q4"])
+def test_prefill_two_passes(name, oracle_threads):
+    """2,300 tokens: pass 0 (2048 tokens, 128-token-tile MFMA GEMMs, the
+    unsplit P.V kernel) and pass 1 (252 tokens at position 2048 over a
+    2,300-row cache), each layer's kernels checked; then the logits and every
+    layer's KV rows against the oracle's own prefill."""
+    ok, text = _prefill_kernels(name, 2300, [(0, 0), (1, 0), (0, 1), (1, 1)])
+    assert ok, text
+    path = configs.model_path(name, threads=16)
+    mf = kc.ModelFile(path)
+    ids = np.random.default_rng(2300).integers(0, mf.V, 2300)
+    say(f"{name}: 2,300-token prefill against the oracle")
+    eng = emberllm.Engine(path, ctx=2308)
+    orc = oracle.Oracle(path, ctx=2308)
+    assert eng.prefill_pass_tokens() == 2048
+    c = compare(eng.prefill(ids), orc.prefill(ids))
+    say(f"{name} logits: rel-L2 {c['rel_l2']:.2e} max-abs {c['max_abs']:.2e} top-1 {c['agree']}")
+    assert c["agree"] and c["rel_l2"] <= 1e-3 and c["max_abs"] <= 1e-2, c
+    per_layer = orc.ctx * mf.kvd * 4
+    for layer in range(mf.L):
+        for which in (0, 1):
+            g = kc.cache_rows(eng.kv_read(which, layer, 2300), mf, False)
+            o = kc.cache_rows(orc.kv(which)[layer * per_layer:(layer + 1) * per_layer], mf, False)[:2300]
+            rows = np.linalg.norm(g - o, axis=1) / np.linalg.norm(o, axis=1)
+            say(f"{name} layer {layer} {'KV'[which]} rows: median rel {np.median(rows):.1e}, max {rows.max():.1e}")
+            # layer 0 depends only on the embedding, norm, q|k|v GEMM, QK-norm
+            # and RoPE: fp32 rounding, or one ambiguous code (~1e-4 of a row)
+            assert np.median(rows) <= 1e-6 and rows.max() <= (1e-3 if layer == 0 else 1e-2), (layer, which)
+    eng.close()
+    orc.close()

@@ -2,10 +2,12 @@
 against the oracle (the CPU restatement, bit-exact with the reference's
 deterministic build) on identical seeded weights and token streams.
 
-Tolerances: tests/parity.py (task bar 1e-2 max-abs / 1e-3 rel-L2 / 99% top-1,
-raised per case to 1.5x the reference's own optimized-vs-deterministic
-deviation where that exceeds it).  Every case prints its name before it
-touches the GPU.
+Tolerances: tests/parity.py (the north-star bar 1e-2 max-abs / 1e-3 rel-L2 /
+99% top-1, which the small variant models meet; on the deep benchmark shapes
+raised to 1.5x the reference's own optimized-vs-deterministic deviation,
+which is ~1e-2 relative L2 there: see parity.py, and test_gpu_kernels.py for
+the kernel-level bound at those shapes).  Every case prints its name before
+it touches the GPU.
 """
 import sys
 
@@ -15,7 +17,7 @@ import pytest
 import oracle
 from cases import CASES, GPU_CASES
 from emberllm_amd import configs, emberllm
-from parity import FLIP_MAX_ABS, FLIP_REL_L2, check_run, compare
+from parity import FLIP_MAX_ABS, FLIP_REL_L2, TIE_MARGIN, check_run, compare
 
 pytestmark = pytest.mark.gpu
 
@@ -285,10 +287,10 @@ def _greedy_case(name, n_prompt, n_gen, seed, ctx=0, kv16=False):
 def test_device_greedy_loop(oracle_threads):
     res = _greedy_case("t_qwen3", 9, 40, 5)
     for r in res:
-        assert r["agree"] or r["margin"] < 2 * r["max_abs"], r
+        assert r["agree"] or r["margin"] < min(2 * r["max_abs"], TIE_MARGIN), r
     res = _greedy_case("t_g7", 300, 12, 6, kv16=True)
     for r in res:
-        assert r["agree"] or r["margin"] < 2 * r["max_abs"], r
+        assert r["agree"] or r["margin"] < min(2 * r["max_abs"], TIE_MARGIN), r
 
 
 def test_device_argmax_first_maximum(tmp_path):
@@ -319,7 +321,7 @@ def test_device_argmax_first_maximum(tmp_path):
 @pytest.mark.slow
 def test_device_greedy_qwen3_shape(oracle_threads):
     res = _greedy_case("qwen3_06b", 16, 24, 12, ctx=48)
-    ok = [r["agree"] or r["margin"] < 2 * r["max_abs"] for r in res]
+    ok = [r["agree"] or r["margin"] < min(2 * r["max_abs"], TIE_MARGIN) for r in res]
     assert np.mean(ok) >= 0.99, res
 
 
@@ -337,29 +339,39 @@ def test_measured_read_bandwidth():
     e.close()
 
 
-def test_xcd_check_reports_misplaced_workgroups(monkeypatch):
+def test_xcd_check_falls_back_to_the_merge_kernel(monkeypatch):
     """The in-kernel merge relies on every workgroup of a kv head running on
     the XCD the state's probe recorded; each workgroup checks that and raises
-    a flag the host turns into an error.  EHIP_XMERGE_TEST_SKEW records the
-    wrong XCDs (the kernels themselves run as usual), so the device loop must
-    fail with the placement error instead of returning tokens."""
-    monkeypatch.setenv("EHIP_XMERGE_TEST_SKEW", "3")
+    a flag.  EHIP_XMERGE_TEST_SKEW records the wrong XCDs (the kernels
+    themselves run as usual), so the check fires on the first decode launch:
+    the state must then switch to the two-kernel merge for good and re-run
+    the work, returning exactly what a state created with that schedule
+    (EHIP_XMERGE=0) returns, through ember_forward and the device loop."""
     name = "qwen3_06b"
     path = configs.model_path(name, threads=16)
     V = configs.ALL[name]["vocab_size"]
-    say("XCD placement check: forced mismatch")
-    eng = emberllm.Engine(path, ctx=160)
-    if not eng.decode_fusion() & 1:
-        eng.close()
-        pytest.skip("this GPU does not place a kv head's workgroups on one XCD; the merge runs as a second kernel")
     ids = np.arange(100) * 97 % V   # several chunks per kv head, so the merge (and its check) runs
-    tok0 = int(np.argmax(eng.prefill(ids)))
-    with pytest.raises(RuntimeError, match="another XCD"):
-        eng.generate_greedy(tok0, len(ids), 4)
-    eng.close()
-    monkeypatch.delenv("EHIP_XMERGE_TEST_SKEW")
-    e2 = emberllm.Engine(path, ctx=160)   # without the skew the same loop runs
-    e2.prefill(ids)
-    toks, _ = e2.generate_greedy(tok0, len(ids), 4)
-    assert len(toks) == 4
-    e2.close()
+    say("XCD placement check: forced mismatch")
+    monkeypatch.setenv("EHIP_XMERGE", "0")
+    ref = emberllm.Engine(path, ctx=160)
+    assert ref.decode_fusion() == 0
+    tok0 = int(np.argmax(ref.prefill(ids)))
+    want_fwd = ref.forward(tok0, len(ids))
+    want_toks, _ = ref.generate_greedy(tok0, len(ids), 9)
+    ref.close()
+    monkeypatch.delenv("EHIP_XMERGE")
+    monkeypatch.setenv("EHIP_XMERGE_TEST_SKEW", "3")
+    for path_kind in ("forward", "device loop"):
+        eng = emberllm.Engine(path, ctx=160)
+        if not eng.decode_fusion() & 1:
+            eng.close()
+            pytest.skip("this GPU does not place a kv head's workgroups on one XCD; the merge runs as a second kernel")
+        eng.prefill(ids)
+        if path_kind == "forward":
+            np.testing.assert_array_equal(eng.forward(tok0, len(ids)), want_fwd)
+            got, _ = eng.generate_greedy(tok0, len(ids), 9)
+        else:
+            got, _ = eng.generate_greedy(tok0, len(ids), 9)
+        np.testing.assert_array_equal(got, want_toks)
+        assert eng.decode_fusion() == 0, "the state must keep the two-kernel schedule after the check fired"
+        eng.close()

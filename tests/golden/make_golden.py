@@ -16,7 +16,7 @@ writer, and every fixture records the sha1 of the model file it was made from.
                    deterministic build on the GPU parity cases (tolerance
                    calibration, see tests/parity.py)
 
-Usage: python tests/golden/make_golden.py [quant f16 sampler tiny real noise]
+Usage: python tests/golden/make_golden.py [quant f16 sampler tiny real noise wide]
 """
 import ctypes
 import json
@@ -187,6 +187,33 @@ def noise_fixture():
             top1=float(np.mean([r["agree"] for r in res])), steps=len(res))
         print("noise", case["id"], out[case["id"]], flush=True)
     with open(os.path.join(HERE, "noise_floor.json"), "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+
+
+def wide_fixture():
+    """Deviation of the optimized reference from the deterministic one on the
+    2,300-token prefill of the 2-layer Qwen3-width models (the end-to-end
+    part of tests/test_gpu_kernels.py::test_prefill_two_passes), added to
+    noise_floor.json under "<name>-p2300"."""
+    fast = oracle.reference_lib(debug=False)
+    fast.ember_threads_init(min(8, os.cpu_count() or 1))
+    ref().ember_threads_init(min(8, os.cpu_count() or 1))
+    path_json = os.path.join(HERE, "noise_floor.json")
+    with open(path_json) as f:
+        out = json.load(f)
+    for name in configs.WIDE:
+        path = configs.model_path(name)
+        ids = np.random.default_rng(2300).integers(0, configs.WIDE[name]["vocab_size"], 2300)
+        lg = []
+        for debug in (True, False):
+            r = oracle.Reference(path, ctx=2308, debug=debug)
+            lg.append(r.prefill(ids))
+            r.close()
+        c = compare(lg[1], lg[0])
+        out[f"{name}-p2300"] = dict(rel_l2_median=c["rel_l2"], rel_l2_max=c["rel_l2"], max_abs_median=c["max_abs"],
+                                    max_abs_max=c["max_abs"], top1=float(c["agree"]), steps=1)
+        print("noise", name, out[f"{name}-p2300"], flush=True)
+    with open(path_json, "w") as f:
         json.dump(out, f, indent=1, sort_keys=True)
 
 

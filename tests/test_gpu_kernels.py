@@ -16,7 +16,8 @@ Qwen2.5-0.5B @256, Qwen3-0.6B Q8_0 @4096 (both decode-attention schedules),
 Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings; and a
 2-layer Qwen3-width model prefilling 2,300 tokens (one 2048-token pass with
 128-token MFMA tiles, then a 252-token pass at position 2048), also compared
-end to end with the oracle (logits and every layer's KV rows).
+end to end with the oracle (logits, at the reference builds' own noise floor
+for that prefill, and every layer's KV rows).
 """
 import sys
 
@@ -26,7 +27,7 @@ import pytest
 import kernel_check as kc
 import oracle
 from emberllm_amd import configs, emberllm
-from parity import compare
+from parity import check_run, compare
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
@@ -146,8 +147,10 @@ def test_prefill_two_passes(name, oracle_threads):
     orc = oracle.Oracle(path, ctx=2308)
     assert eng.prefill_pass_tokens() == 2048
     c = compare(eng.prefill(ids), orc.prefill(ids))
-    say(f"{name} logits: rel-L2 {c['rel_l2']:.2e} max-abs {c['max_abs']:.2e} top-1 {c['agree']}")
-    assert c["agree"] and c["rel_l2"] <= 1e-3 and c["max_abs"] <= 1e-2, c
+    # end to end, activation codes an ulp decides cascade (tests/parity.py):
+    # held to the reference's own optimized-vs-deterministic deviation on this
+    # very prefill (noise_floor.json "<name>-p2300", 1.5e-2 relative L2)
+    say(f"{name} logits: " + check_run([c], f"{name}-p2300"))
     per_layer = orc.ctx * mf.kvd * 4
     for layer in range(mf.L):
         for which in (0, 1):

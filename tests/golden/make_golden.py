@@ -16,7 +16,7 @@ writer, and every fixture records the sha1 of the model file it was made from.
                    deterministic build on the GPU parity cases (tolerance
                    calibration, see tests/parity.py)
 
-Usage: python tests/golden/make_golden.py [quant f16 sampler tiny real noise wide]
+Usage: python tests/golden/make_golden.py [quant f16 sampler tiny real noise wide workload]
 """
 import ctypes
 import json
@@ -217,7 +217,65 @@ def wide_fixture():
         json.dump(out, f, indent=1, sort_keys=True)
 
 
+# the benchmark workloads of tests/test_gpu_workloads.py: (name, prompt, steps, sampled)
+WORKLOADS = [("stories110m", 128, 128, False), ("smollm2_135m", 1024, 128, False),
+             ("qwen25_05b", 256, 128, True), ("qwen3_06b", 128, 128, False), ("qwen3_06b_q4", 512, 256, False)]
+
+
+def workload_fixture():
+    """Deviation of the optimized reference from the deterministic one over
+    the benchmark workloads' full protocol (same seeds and lengths as
+    tests/test_gpu_workloads.py): the deterministic build generates its own
+    tokens (greedy, or its sampler at T 0.8 / top-k 40 / top-p 0.9, seed
+    1234) and the optimized build is teacher forced on them; added to
+    noise_floor.json under "<name>-pp<prompt>-tg<steps>"."""
+    fast = oracle.reference_lib(debug=False)
+    fast.ember_threads_init(min(8, os.cpu_count() or 1))
+    ref().ember_threads_init(min(8, os.cpu_count() or 1))
+    path_json = os.path.join(HERE, "noise_floor.json")
+    with open(path_json) as f:
+        out = json.load(f)
+    for name, prompt, steps, sampled in WORKLOADS:
+        path = configs.model_path(name)
+        V = configs.ALL[name]["vocab_size"]
+        rng = np.random.default_rng(prompt * 7 + steps)
+        ids = rng.integers(0, V, prompt)
+        ctx = prompt + steps + 2
+        a = oracle.Reference(path, ctx=ctx, debug=True)
+        b = oracle.Reference(path, ctx=ctx, debug=False)
+        smp = oracle.Sampler()
+        ref().ember_sampler_init(ctypes.byref(smp), 0.8, 0.9, 40, 1234)
+
+        def pick(lg):
+            if not sampled:
+                return int(np.argmax(lg))
+            x = np.ascontiguousarray(lg, dtype=np.float32).copy()
+            return int(ref().ember_sample(ctypes.byref(smp), oracle.f32p(x), len(x)))
+
+        la = a.prefill(ids)
+        res = [compare(b.prefill(ids), la)]
+        t = pick(la)
+        for i in range(steps):
+            la = a.forward(t, prompt + i)
+            res.append(compare(b.forward(t, prompt + i), la))
+            t = pick(la)
+        a.close()
+        b.close()
+        ref().ember_sampler_free(ctypes.byref(smp))
+        key = f"{name}-pp{prompt}-tg{steps}"
+        out[key] = dict(
+            rel_l2_median=float(np.median([r["rel_l2"] for r in res])),
+            rel_l2_max=float(max(r["rel_l2"] for r in res)),
+            max_abs_median=float(np.median([r["max_abs"] for r in res])),
+            max_abs_max=float(max(r["max_abs"] for r in res)),
+            top1=float(np.mean([r["agree"] for r in res])), steps=len(res),
+            misses=[[i, r["margin"], r["rms"]] for i, r in enumerate(res) if not r["agree"]])
+        print("noise", key, {k: v for k, v in out[key].items()}, flush=True)
+        with open(path_json, "w") as f:
+            json.dump(out, f, indent=1, sort_keys=True)
+
+
 if __name__ == "__main__":
-    what = sys.argv[1:] or ["quant", "f16", "sampler", "tiny", "real", "noise"]
+    what = sys.argv[1:] or ["quant", "f16", "sampler", "tiny", "real", "noise", "wide", "workload"]
     for w in what:
         globals()[f"{w}_fixture"]()

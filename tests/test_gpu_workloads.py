@@ -15,10 +15,12 @@ every matmul input to Q8_0, so any reordered fp32 sum can move an activation
 code and the logits of deep models then differ by ~1e-2 relative L2: the
 reference's own optimized build differs from its deterministic one by as much
 (tests/golden/noise_floor.json).  These end-to-end runs are therefore held to
-the noise floor of the reference's two builds at the same model shape
-(tests/parity.py); the kernel-level bound (1e-6) is test_gpu_kernels'.  The
-north-star figures (1e-3 relative L2, 1e-2 max-abs, 99% top-1) are printed
-beside the bars for every run.
+the noise floor of the reference's two builds measured over the very same
+workload protocol (the optimized build teacher forced on the deterministic
+build's tokens; tests/parity.py), whose top-1 agreement there is 0.992,
+1.000, 0.961, 0.946 and 0.984; the kernel-level bound (1e-6) is
+test_gpu_kernels'.  The north-star figures (1e-3 relative L2, 1e-2 max-abs,
+99% top-1) are printed beside the bars for every run.
 
 The device-held loops must also reproduce the C-API loop exactly: the greedy
 loop's tokens equal the argmax of ember_forward's logits, and the device
@@ -37,10 +39,6 @@ from parity import check_run, compare
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
-# bars: the noise floor of the same model shape (tests/golden/noise_floor.json)
-FLOOR = {"stories110m": "stories110m-p16-d32-s11", "smollm2_135m": "smollm2_135m-p16-d32-s11",
-         "qwen25_05b": "qwen25_05b-p16-d32-s11", "qwen3_06b": "qwen3_06b-p16-d32-s11",
-         "qwen3_06b_q4": "qwen3_06b_q4-p16-d32-s11"}
 
 
 def say(msg):
@@ -102,7 +100,9 @@ def _run(name, prompt, steps, sampled=False):
     say(f"{name}: device loop reproduces the API loop on {same * 100:.1f}% of {steps} tokens")
     assert same == 1.0, (list(got[:20]), toks[:20])
     say(north_star(res))
-    say(check_run(res, FLOOR[name]))
+    # bars: the reference's optimized build against its deterministic build
+    # over this same protocol (noise_floor.json, make_golden.py workload)
+    say(check_run(res, f"{name}-pp{prompt}-tg{steps}"))
 
 
 def test_stories110m_pp128_tg128(oracle_threads):

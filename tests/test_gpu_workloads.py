@@ -40,7 +40,6 @@ from parity import check_run, compare
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
 
-
 def say(msg):
     print(f"[gpu-workload] {msg}", flush=True)
     sys.stdout.flush()

@@ -138,6 +138,8 @@ PROTOTYPES = {
                                              ctypes.POINTER(EmberSampler), _IP, _FP]),
     "ehip_time_kernel": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP]),
     "ehip_measure_read_bw": (ctypes.c_int, [_P, ctypes.c_uint64, ctypes.c_int, _FP]),
+    "ehip_sample_noalloc": (ctypes.c_int, [_P, ctypes.c_int, ctypes.POINTER(EmberSampler), _P, _P, _P, _P, _P]),
+    "ehip_noalloc_setup": (ctypes.c_int, []),
     # ember_synth.h
     "ember_synth_write": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(EmberSynthConfig)]),
     "ember_synth_fill_row": (None, [ctypes.c_uint64, ctypes.c_char_p, ctypes.c_int, ctypes.c_float,

@@ -48,6 +48,8 @@ static void set_err(const char *fmt, ...) {
 
 extern "C" const char *ehip_last_error(void) { return g_err; }
 
+void ehip::set_error_text(const char *msg) { snprintf(g_err, sizeof g_err, "%s", msg); }
+
 extern "C" int ehip_device_count(void) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess) return 0;
@@ -469,6 +471,10 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     s->xm_err = reinterpret_cast<int *>(s->logits_d + c.vocab_size);
+    if (ehip_noalloc_setup()) {   // ehip_sample_noalloc's scratch address on this device
+        ehip_state_destroy(s);
+        return nullptr;
+    }
     if (xm_probe(s)) {
         ehip_state_destroy(s);
         return nullptr;

@@ -184,6 +184,8 @@ struct SampleArgs {
     int *tokpos; int *out; int cap;  // as ArgmaxArgs
 };
 int launch_sample(hipStream_t st, const SampleArgs &a);
+// ehip_last_error()'s text for this thread (ehip.hip)
+void set_error_text(const char *msg);
 // Whether launch_sample applies penalties (which change the logits after the
 // per-part maxima were taken).
 bool sample_penalized(const SampleArgs &a);

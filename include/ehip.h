@@ -104,6 +104,29 @@ int ehip_sample(EhipState *s, const float *logits, int n, EmberSampler *smp, int
  * device time.  Same parameter support as ehip_sample. */
 int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, EmberSampler *smp, int *out_tokens, float *ms);
 
+/* ehip_sample's selection on logits already in device memory, allocating
+ * nothing.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  All pointers are device memory:
+ * logits[n] (penalties update them in place, as ember_sample does), the
+ * xorshift64* state *rng_state (advanced), the history ring history[cap]
+ * and hist_meta[2] = {hist_len, hist_pos} (both NULL: no ring; else
+ * cap = params->hist_cap, updated as ember_sampler_accept would), and
+ * *token (written).  params (host) supplies temperature, top_k, top_p,
+ * min_p, the penalties and hist_cap; its history pointer and RNG fields are
+ * not read.  The launches are enqueued on `stream` (a hipStream_t; NULL for
+ * the default stream) and the call returns without waiting.  Every
+ * intermediate lives in one fixed device array per GPU (about 36 KB, held
+ * until the process ends); n is limited to 262,144 logits and top_k to
+ * [1, 64] when temperature > 0.  Calls that overlap on one GPU race on that
+ * array.  Returns 0, or nonzero with ehip_last_error() set. */
+int ehip_sample_noalloc(float *logits, int n, const EmberSampler *params, uint64_t *rng_state,
+                        int *history, int *hist_meta, int *token, void *stream);
+/* Looks up that array's device address on the current device (done by
+ * ehip_state_create; needed before graph capture on a device without a
+ * state).  Returns 0 or nonzero. */
+int ehip_noalloc_setup(void);
+
 /* ---- inspection and measurement (tests and bench) ----------------------- */
 /* Copy the KV cache of the given layers to/from host memory in the cache's
  * own element type; which = 0 keys, 1 values; rows [0, n_pos). */

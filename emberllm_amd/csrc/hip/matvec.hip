@@ -231,9 +231,12 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
         RowGroup<DT, EPI, NCH, UPW> nxt;
         const bool more = u0 + nw * UPW < a.units;
         if (more) nxt.load(a, u0 + nw * UPW, lane, nch, nb);
+        // every row's lane partials first, then all the cross-lane sums
+        // together (independent chains the scheduler interleaves), then one
+        // epilogue in which lane j finishes row j
+        float v[UPW][NR];
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
-            float v[NR];
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 float s = 0.0f;
@@ -246,7 +249,8 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
                         d = sdot4(w.y, xr[i].y, d);
                         d = sdot4(w.z, xr[i].z, d);
                         d = sdot4(w.w, xr[i].w, d);
-                        d += __shfl_xor(d, 1);   // lanes 2j, 2j+1: both halves of block j
+                        // lanes 2j, 2j+1 hold the two halves of block j
+                        d += __builtin_amdgcn_mov_dpp(d, 0xb1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
                         if (lane & 1) d = 0;
                     } else {
                         const int m = 0x0f0f0f0f;
@@ -264,18 +268,36 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
                     const float dw = lane + 64 * i < nch ? h2f(cur.d[j][r][i]) : 0.0f;
                     s += ((float)d * dw) * dxr[i];
                 }
-                v[r] = wave_sum(s);
+                v[j][r] = s;
             }
-            const int u = u0 + j;
-            if (u < a.units) {
-                if (EPI == EPI_STORE) {
-                    const float o = a.bias ? v[0] + cur.pre[j] : v[0];
-                    if (lane == 0) a.out[u] = o;
-                    am_take(best_v, best_i, o, u);
-                } else if (lane == 0) {
-                    if (EPI == EPI_RESID) a.out[u] = cur.pre[j] + v[0];
-                    else { const float g = v[0]; a.out[u] = g / (1.0f + expf(-g)) * v[NR - 1]; }
-                }
+        }
+#pragma unroll
+        for (int j = 0; j < UPW; j++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) v[j][r] = wave_sum(v[j][r]);
+        // lane j < UPW: row u0 + j
+        float mine[NR], pre = 0.0f;
+#pragma unroll
+        for (int r = 0; r < NR; r++) mine[r] = v[0][r];
+        pre = cur.pre[0];
+#pragma unroll
+        for (int j = 1; j < UPW; j++)
+            if (lane == j) {
+#pragma unroll
+                for (int r = 0; r < NR; r++) mine[r] = v[j][r];
+                pre = cur.pre[j];
+            }
+        const int u = u0 + lane;
+        if (lane < UPW && u < a.units) {
+            if (EPI == EPI_STORE) {
+                const float o = a.bias ? mine[0] + pre : mine[0];
+                a.out[u] = o;
+                am_take(best_v, best_i, o, u);
+            } else if (EPI == EPI_RESID) {
+                a.out[u] = pre + mine[0];
+            } else {
+                const float g = mine[0];
+                a.out[u] = g / (1.0f + expf(-g)) * mine[NR - 1];
             }
         }
         if (more) cur = nxt;

@@ -468,6 +468,187 @@ __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
 }
 
 // --------------------------------------------------------------------------
+// k_pf_flash: the prefill attention on fp32 matrix cores, one pass over the
+// keys with a running softmax (the default; the three kernels above keep the
+// reference's summation order and are selected with EHIP_PF_ATTN=exact).
+//
+// Rows are (token, head) pairs of one kv group, row R = b * G + h, so every
+// K/V tile staged in LDS serves the group's G heads.  A workgroup takes 64
+// rows (16 per wave) and walks the key tiles [0, its last visible key] in
+// tiles of 64 keys.  Per tile and wave, with v_mfma_f32_16x16x4f32 (lane l
+// supplies A[l % 16][l / 16] and B[l / 16][l % 16] and receives
+// D[4 (l / 16) + r][l % 16], r = 0..3):
+//   S^T = K . Q^T  (16 keys x 16 rows per product, 4 products per tile):
+//       A = K[key 16kk + l%16][dim], B = Q[row l%16][dim] with lane quarter
+//       q = l/16 covering dims q*HD/4 .. +HD/4-1 over the HD/4 steps, so a
+//       lane's K and Q fragments are contiguous (16-byte loads); the lane
+//       receives S[row l%16][key 16kk + 4q + r];
+//   O^T += V^T . P^T (16 dims x 16 rows per product, HD/16 products): the
+//       contraction runs over the keys in the order the scores came out,
+//       key 16kk + 4q + r at step (kk, r), so the lane's own probabilities
+//       are the B operand and never leave registers; A = V^T[dim][key] is
+//       one 16-byte LDS read from the transposed V tile.
+// Each lane holds one row's running maximum (log2 units) and partial sum;
+// the four lanes of a row see the same maximum, and their partial sums and
+// output quarters are combined at the end.  Scores are q.k * (1/sqrt(hd)) *
+// log2(e), probabilities 2^(s - m): one v_exp_f32 each (model.c:57-64 and
+// 207-278 in another summation order: the products are fp32, the sums fp32
+// in the matrix cores' order).
+// Roofline: matrix-core bound, 4 * hd flops per visible (row, key) pair
+// (q.k and p.v); 157.3 TFLOP/s dense fp32 on the MI355X.
+// Grid (kv heads, row tiles), kv heads varying fastest, so a kv head's
+// workgroups share an XCD and its L2 holds the head's K/V; row tiles in
+// reverse order, so the longest (latest tokens) start first.
+constexpr int FL_BR = 64, FL_BK = 64;
+
+__device__ __forceinline__ float fl_quarter_max(float v) {   // max over lanes i, i^16, i^32, i^48
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float fl_quarter_sum(float v) { return xor32_add(xor16_add(v)); }
+
+template <int HD, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
+    constexpr int NS = HD / 4;       // score product steps; lane quarter q holds dims NS*q .. NS*q + NS - 1
+    constexpr int ND = HD / 16;      // 16-dim output products
+    constexpr int KP = HD + 4;       // K tile pitch (floats): a 16-lane quarter's 16-byte reads hit 64 banks
+    constexpr int VP = FL_BK + 4;    // transposed V tile pitch
+    static_assert(NS % 4 == 0, "head_dim must be a multiple of 16");
+    __shared__ __align__(16) float ks[FL_BK * KP];
+    __shared__ __align__(16) float vt[HD * VP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 15, q = lane >> 4;
+    const int g = blockIdx.x;
+    const int G = a.n_heads / a.n_kv, nrows = a.n_tok * G;
+    const int r0 = (gridDim.y - 1 - blockIdx.y) * FL_BR;
+    const int R = min(r0 + wave * 16 + i, nrows - 1);   // this lane's row (padding rows repeat the last)
+    const int b = R / G, h = R % G;
+    const int pos = a.pos_base + b;                       // keys [0, pos] are visible to the row
+    const int kend = a.pos_base + (min(r0 + FL_BR, nrows) - 1) / G;   // the workgroup's last visible key
+    const size_t hoff = (size_t)g * HD;
+
+    float qf[NS];
+    {
+        const float *qr = a.q + (size_t)b * a.q_stride + (size_t)(g * G + h) * HD + NS * q;
+#pragma unroll
+        for (int s = 0; s < NS; s += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(qr + s);
+            qf[s] = v.x; qf[s + 1] = v.y; qf[s + 2] = v.z; qf[s + 3] = v.w;
+        }
+    }
+    const float sscale = a.inv_sqrt * 1.4426950408889634f;
+    float m = -INFINITY, lsum = 0.0f;
+    f32x4 o[ND];
+#pragma unroll
+    for (int d = 0; d < ND; d++) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nkt = kend / FL_BK + 1;
+    for (int kt = 0; kt < nkt; kt++) {
+        const int k0 = kt * FL_BK;
+        __syncthreads();   // the previous tile has been read
+        // stage K rows [k0, k0 + 64) as ks[key][dim] and V rows as vt[dim][key]
+        // (keys past kend repeat row kend; no row sees them)
+        for (int f = tid; f < FL_BK * (HD / 4); f += WG) {
+            const int key = f / (HD / 4), c = (f % (HD / 4)) * 4;
+            const size_t off = (size_t)min(k0 + key, kend) * a.kv_dim + hoff + c;
+            float4 kv, vv;
+            if (F16) {
+                const uint2 ku = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
+                const uint2 vu = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
+                kv = make_float4(h2f(ku.x & 0xffff), h2f(ku.x >> 16), h2f(ku.y & 0xffff), h2f(ku.y >> 16));
+                vv = make_float4(h2f(vu.x & 0xffff), h2f(vu.x >> 16), h2f(vu.y & 0xffff), h2f(vu.y >> 16));
+            } else {
+                kv = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.kc) + off);
+                vv = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.vc) + off);
+            }
+            *reinterpret_cast<float4 *>(&ks[key * KP + c]) = kv;
+            vt[(c + 0) * VP + key] = vv.x;
+            vt[(c + 1) * VP + key] = vv.y;
+            vt[(c + 2) * VP + key] = vv.z;
+            vt[(c + 3) * VP + key] = vv.w;
+        }
+        __syncthreads();
+        // S^T: this lane gets S[row i][key 16kk + 4q + r]
+        f32x4 sc[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            sc[kk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const float *kr = &ks[(16 * kk + i) * KP + NS * q];
+#pragma unroll
+            for (int s = 0; s < NS; s += 4) {
+                const float4 kv = *reinterpret_cast<const float4 *>(kr + s);
+                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qf[s], sc[kk], 0, 0, 0);
+                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qf[s + 1], sc[kk], 0, 0, 0);
+                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qf[s + 2], sc[kk], 0, 0, 0);
+                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[s + 3], sc[kk], 0, 0, 0);
+            }
+        }
+        // running softmax of the row (log2 units); keys past the row's position are masked
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = k0 + 16 * kk + 4 * q + r;
+                const float v = t <= pos ? sc[kk][r] * sscale : -INFINITY;
+                sc[kk][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        const float mn = fmaxf(m, fl_quarter_max(mx));   // finite: key 0 is in the first tile
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first tile (m = -inf)
+        m = mn;
+        lsum *= alpha;
+#pragma unroll
+        for (int d = 0; d < ND; d++) o[d] *= alpha;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = __builtin_amdgcn_exp2f(sc[kk][r] - mn);   // masked: 2^-inf = 0
+                sc[kk][r] = p;
+                lsum += p;
+            }
+        // O^T += V^T . P^T over the tile's keys in the scores' order
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                const float4 vv = *reinterpret_cast<const float4 *>(&vt[(16 * d + i) * VP + 16 * kk + 4 * q]);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sc[kk][0], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sc[kk][1], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sc[kk][2], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sc[kk][3], o[d], 0, 0, 0);
+            }
+    }
+    // o[d][r] = O^T[dim 16d + 4q + r][row i]: four consecutive dims of the row
+    const float inv = 1.0f / fl_quarter_sum(lsum);
+    if (r0 + wave * 16 + i < nrows) {
+        float *out = a.out + (size_t)b * a.n_heads * HD + (size_t)(g * G + h) * HD + 4 * q;
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+            *reinterpret_cast<float4 *>(out + 16 * d) = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
+    }
+}
+
+int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a) {
+    if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || a.q_stride % 4) return -1;
+    const int G = a.n_heads / a.n_kv;
+    const dim3 grid(a.n_kv, (a.n_tok * G + FL_BR - 1) / FL_BR);
+    switch (a.hd) {
+#define FLL(H)                                                                                  \
+    case H:                                                                                     \
+        if (f16kv) hipLaunchKernelGGL((k_pf_flash<H, true>), grid, dim3(WG), 0, st, a);         \
+        else hipLaunchKernelGGL((k_pf_flash<H, false>), grid, dim3(WG), 0, st, a);              \
+        return 0;
+        FLL(48) FLL(64) FLL(128)
+#undef FLL
+    }
+    return -1;
+}
+
+// --------------------------------------------------------------------------
 template <int HD, int GM, bool F16>
 static void pf_go(hipStream_t st, const AttnArgs &a) {
     constexpr int QT = 4 * PfRows<GM>::QW;

@@ -229,6 +229,12 @@ fail:
 // ---------------------------------------------------------------- state ----
 constexpr int PF_CHUNK = 2048;  // prefill tokens per pass through the layers (at most)
 constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores per pass (at most)
+// Prefill passes whose keys (start + tokens) fit in this many positions keep
+// the reference's summation order in the attention: there it costs little,
+// and the small models then match the reference's deterministic build to
+// rounding.  Longer passes run the attention on matrix cores.
+constexpr int PF_EXACT_KEYS = 512;
+enum { PF_AUTO = 0, PF_EXACT = 1, PF_MFMA = 2 };
 
 // A captured run of device-loop steps.  One graph launch per token leaves
 // the GPU idle for ~7 us between graphs (against ~1.5 us between the kernels
@@ -271,6 +277,11 @@ struct EhipState {
     // [n_heads][pf_chunk][attn_prefill_tiles(ldk)], row max and 1/sum [n_heads][pf_chunk]
     float *pf_scores, *pf_tmax, *pf_rowmax, *pf_rowinv;
     int pf_chunk;       // tokens per prefill pass
+    // prefill attention: the reference's summation order (three kernels and
+    // the score scratch above) for passes whose keys fit in PF_EXACT_KEYS,
+    // the matrix-core kernel with a running softmax beyond (PF_AUTO);
+    // EHIP_PF_ATTN=exact or =mfma forces one of them for every pass
+    int pf_mode;
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
@@ -416,9 +427,18 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     const size_t ldk_max = (size_t)attn_prefill_ldk(0, ctx);
-    s->pf_chunk = (int)std::max<size_t>(1, std::min<size_t>(std::min(PF_CHUNK, ctx),
-                                                            PF_SCORES_MAX / (4 * ldk_max * c.n_heads)));
+    {
+        const char *pa = getenv("EHIP_PF_ATTN");
+        s->pf_mode = pa && !strcmp(pa, "exact") ? PF_EXACT : (pa && !strcmp(pa, "mfma") ? PF_MFMA : PF_AUTO);
+    }
+    s->pf_chunk = std::min(PF_CHUNK, ctx);
+    if (s->pf_mode == PF_EXACT)
+        s->pf_chunk = (int)std::max<size_t>(1, std::min<size_t>(s->pf_chunk, PF_SCORES_MAX / (4 * ldk_max * c.n_heads)));
     const size_t pfc = (size_t)s->pf_chunk;
+    // exact-order score scratch: every pass (PF_EXACT), or passes of up to
+    // PF_EXACT_KEYS keys (PF_AUTO)
+    const size_t ex_rows = s->pf_mode == PF_EXACT ? pfc : std::min<size_t>(pfc, PF_EXACT_KEYS);
+    const size_t ex_ldk = s->pf_mode == PF_EXACT ? ldk_max : (size_t)attn_prefill_ldk(0, std::min(PF_EXACT_KEYS, ctx));
     const int wide = std::max(std::max(c.dim, c.hidden_dim), qd);
     bool ok = (s->kc = salloc(s, kvb, true)) && (s->vc = salloc(s, kvb, true)) &&
               (s->tokpos_d = (int *)salloc(s, 16, true)) &&
@@ -438,10 +458,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->dxp = (float *)salloc(s, 4 * pfc * (wide / QB + 1))) &&
               (s->xsum = (int *)salloc(s, 4 * pfc * (wide / QB + 1))) &&
               (s->ids_d = (int *)salloc(s, 4 * pfc)) &&
-              (s->pf_scores = (float *)salloc(s, 4 * pfc * ldk_max * c.n_heads)) &&
-              (s->pf_rowinv = (float *)salloc(s, 4 * pfc * c.n_heads)) &&
-              (s->pf_rowmax = (float *)salloc(s, 4 * pfc * c.n_heads)) &&
-              (s->pf_tmax = (float *)salloc(s, 4 * pfc * c.n_heads * (size_t)attn_prefill_tiles((int)ldk_max))) &&
+
               (s->am_val = (float *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->am_idx = (int *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
               (s->gen_tok = (int *)salloc(s, 4 * (size_t)ctx, true)) &&
@@ -452,6 +469,11 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->smp_cval = (float *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX)) &&
               (s->smp_cidx = (int *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
+    if (ok && s->pf_mode != PF_MFMA)
+        ok = (s->pf_scores = (float *)salloc(s, 4 * ex_rows * ex_ldk * c.n_heads)) &&
+             (s->pf_rowinv = (float *)salloc(s, 4 * ex_rows * c.n_heads)) &&
+             (s->pf_rowmax = (float *)salloc(s, 4 * ex_rows * c.n_heads)) &&
+             (s->pf_tmax = (float *)salloc(s, 4 * ex_rows * c.n_heads * (size_t)attn_prefill_tiles((int)ex_ldk)));
     if (ok) {
         // RoPE table with the reference's arithmetic (model.c:69-71): the
         // angle pos * freq in fp32, then the host libm cosf / sinf
@@ -907,7 +929,8 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             at.out = s->O;
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
             at.ldk = attn_prefill_ldk(start + c0, mt);
-            rc |= launch_attention(s->st, s->f16kv, at);
+            const bool exact = s->pf_mode == PF_EXACT || (s->pf_mode == PF_AUTO && start + c0 + mt <= PF_EXACT_KEYS);
+            rc |= exact ? launch_attention(s->st, s->f16kv, at) : launch_attention_mfma(s->st, s->f16kv, at);
             if (psnap(DBG_O, s->O, qd, qd)) return nullptr;
             QuantRowsArgs q2{};
             q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;

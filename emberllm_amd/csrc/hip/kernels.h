@@ -78,6 +78,8 @@ struct AttnArgs {
 };
 // prefill: q rows already normed and rotated, k/v already in the cache
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
+// prefill on fp32 matrix cores with a running softmax (no score scratch)
+int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a);
 inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }
 // tile-maximum slots per prefill score row (64-key tiles, padded to 4)
 __host__ __device__ inline int attn_prefill_tiles(int ldk) { return ((ldk + 63) / 64 + 3) & ~3; }

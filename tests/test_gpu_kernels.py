@@ -4,7 +4,9 @@ Every decode kernel (q|k|v matvec with its RMSNorm prologue, QK-norm / RoPE
 / KV store, split-K attention and its merge, wo + residual, w1|w3 + SwiGLU,
 w2 + residual, final norm + lm_head) and every prefill kernel (row
 quantization, the int8 MFMA GEMMs in both tile sizes and the short-prompt
-GEMM, QK post-processing, the prefill attention) is captured on the GPU and
+GEMM, QK post-processing, the prefill attention in both forms: the
+exact-order kernels up to 512 keys and the fp32 matrix-core kernel beyond,
+or forced at pp512) is captured on the GPU and
 recomputed in float64 from the model file on the GPU's own inputs
 (tests/kernel_check.py, itself pinned against the oracle on the CPU by
 tests/test_kernel_check.py).  Bound: 1e-6 of the sum of |terms| for
@@ -128,6 +130,15 @@ def test_prefill_kernels_512(name):
     """pp512 at the Qwen3-0.6B shape: q|k|v and w1|w3 on the 64-token-tile
     MFMA GEMM, wo and w2 on the 32x32-tile GEMM, Q8_0 and Q4_0 weights."""
     ok, text = _prefill_kernels(name, 512, [(0, 0), (27, 0)])
+    assert ok, text
+
+
+def test_prefill_kernels_512_matrix_cores(monkeypatch):
+    """pp512 at the Qwen3-0.6B shape with the attention forced onto the fp32
+    matrix-core kernel (EHIP_PF_ATTN=mfma; by default passes of up to 512
+    keys keep the reference's summation order)."""
+    monkeypatch.setenv("EHIP_PF_ATTN", "mfma")
+    ok, text = _prefill_kernels("qwen3_06b", 512, [(0, 0), (27, 0)])
     assert ok, text
 
 

@@ -366,26 +366,30 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 // Short prompts: the 128-unit tiles above leave most CUs idle (a 128-token
 // wo or w2 product is 16 workgroups), and the reference's block order keeps
 // K in one workgroup.  This variant takes 32 units x 32 tokens per workgroup,
-// one 16 x 16 v_mfma_i32_16x16x32_i8 tile per wave and quant block, and
-// GS_KB = 16 blocks per double-buffered stage so a short K needs few global
-// round trips.  Fragments of the 16 x 16 x 32 product: lane l holds
-// A[l % 16][8 (l / 16) .. +7] (eight int8 of a weight row),
-// B[8 (l / 16) .. +7][l % 16] (of a token row), and outputs
+// one 16 x 16 v_mfma_i32_16x16x32_i8 tile per wave and quant block.  K is
+// consumed in stages of GS_KB = 4 blocks, and the loads of the next
+// GS_P - 1 stages are in flight in a ring of registers while a stage is
+// stored to LDS and computed: with a short K the kernel's time is the
+// global round trip, which one stage of prefetch exposed once per stage.
+// Loads land in registers, so the compiler's in-order wait for the oldest
+// stage lets the younger ones stay in flight.  Fragments of the 16 x 16 x 32
+// product: lane l holds A[l % 16][8 (l / 16) .. +7] (eight int8 of a weight
+// row), B[8 (l / 16) .. +7][l % 16] (of a token row), and outputs
 // D[4 (l / 16) + r][l % 16], r = 0..3.  The epilogue is the same
 // sum += ((float)isum * dw) * dx in block order.
-constexpr int GS_U = 32, GS_T = 32, GS_KB = 16;
+constexpr int GS_U = 32, GS_T = 32, GS_KB = 4, GS_P = 8;
 
 template <int DT, int EPI>
 __global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
     constexpr int WB = DT == DT_Q8 ? 32 : 16;                 // weight bytes per row and block
     constexpr int WROW = GS_KB * WB, XROW = GS_KB * 32;        // stage bytes per row
     constexpr int WP = WROW + 16, XP = XROW + 16;              // LDS row pitches
-    constexpr int WLD = GS_U * WROW / 16 / WG, XLD = GS_T * XROW / 16 / WG;
-    constexpr int NSC = GS_KB * GS_U / WG;                     // scales of each kind per thread
-    static_assert(GS_U == GS_T && GS_KB * GS_U % WG == 0 && WLD >= 1 && XLD >= 1, "layout");
+    constexpr int WCH = GS_U * WROW / 16, XCH = GS_T * XROW / 16;   // 16-byte chunks per stage
+    constexpr int NSC = GS_KB * GS_U;                          // scales of each kind per stage
+    static_assert(GS_U == GS_T && WCH <= WG && XCH == WG && NSC <= WG, "one chunk per thread and stage");
     __shared__ __align__(16) uint8_t ws[2][GS_U * WP];
     __shared__ __align__(16) int8_t xsm[2][GS_T * XP];
-    __shared__ float dws[2][GS_KB][GS_U], dxs[2][GS_KB][GS_T];
+    __shared__ __align__(16) float dws[2][GS_KB][GS_U], dxs[2][GS_KB][GS_T];
     __shared__ int sxs[2][GS_KB][GS_T];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;
@@ -393,84 +397,90 @@ __global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
     const int K = a.W.cols, nb = K / QB, nst = (nb + GS_KB - 1) / GS_KB;
     const int wu = (wave & 1) * 16, wt = (wave >> 1) * 16;
 
-    i32x4 wr[WLD], xr[XLD];
-    float dwr[NSC], dxr[NSC];
-    int xsr[NSC];
-    auto load = [&](int st) {
+    // register ring: slot j holds a stage s with s % GS_P == j
+    i32x4 wr[GS_P], xr[GS_P];
+    uint16_t dwr[GS_P];
+    float dxr[GS_P];
+    int xsr[GS_P];
+    auto load = [&](int j, int st) {
         const int b0 = st * GS_KB;
-#pragma unroll
-        for (int i = 0; i < WLD; i++) {
-            const int f = tid + i * WG, row = f / (WROW / 16), c = (f % (WROW / 16)) * 16;
+        if (tid < WCH) {
+            const int row = tid / (WROW / 16), c = (tid % (WROW / 16)) * 16;
             const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
-            wr[i] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
+            wr[j] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
         }
-#pragma unroll
-        for (int i = 0; i < XLD; i++) {
-            const int f = tid + i * WG, row = f / (XROW / 16), c = (f % (XROW / 16)) * 16;
+        {
+            const int row = tid / (XROW / 16), c = (tid % (XROW / 16)) * 16;
             const int t = min(t0 + row, a.n - 1), blk = min(b0 + c / 32, nb - 1);
-            xr[i] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
+            xr[j] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
         }
-#pragma unroll
-        for (int i = 0; i < NSC; i++) {
-            const int f = tid + i * WG, kb = f / GS_U, r = f % GS_U, blk = min(b0 + kb, nb - 1);
+        if (tid < NSC) {
+            const int kb = tid / GS_U, r = tid % GS_U, blk = min(b0 + kb, nb - 1);
             const int t = min(t0 + r, a.n - 1);
-            dwr[i] = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk]);
-            dxr[i] = a.dx[(size_t)t * nb + blk];
-            xsr[i] = DT == DT_Q4 ? a.xs[(size_t)t * nb + blk] : 0;
+            dwr[j] = a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk];
+            dxr[j] = a.dx[(size_t)t * nb + blk];
+            if (DT == DT_Q4) xsr[j] = a.xs[(size_t)t * nb + blk];
         }
     };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < WLD; i++) {
-            const int f = tid + i * WG;
-            *reinterpret_cast<i32x4 *>(ws[buf] + (f / (WROW / 16)) * WP + (f % (WROW / 16)) * 16) = wr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < XLD; i++) {
-            const int f = tid + i * WG;
-            *reinterpret_cast<i32x4 *>(xsm[buf] + (f / (XROW / 16)) * XP + (f % (XROW / 16)) * 16) = xr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < NSC; i++) {
-            const int f = tid + i * WG;
-            dws[buf][f / GS_U][f % GS_U] = dwr[i];
-            dxs[buf][f / GS_T][f % GS_T] = dxr[i];
-            sxs[buf][f / GS_T][f % GS_T] = xsr[i];
+    auto store = [&](int j, int buf) {
+        if (tid < WCH)
+            *reinterpret_cast<i32x4 *>(ws[buf] + (tid / (WROW / 16)) * WP + (tid % (WROW / 16)) * 16) = wr[j];
+        *reinterpret_cast<i32x4 *>(xsm[buf] + (tid / (XROW / 16)) * XP + (tid % (XROW / 16)) * 16) = xr[j];
+        if (tid < NSC) {
+            dws[buf][tid / GS_U][tid % GS_U] = h2f(dwr[j]);
+            dxs[buf][tid / GS_T][tid % GS_T] = dxr[j];
+            if (DT == DT_Q4) sxs[buf][tid / GS_T][tid % GS_T] = xsr[j];
         }
     };
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int st = 0; st < nst; st++) {
-        const int buf = st & 1;
-        if (st + 1 < nst) load(st + 1);
-#pragma unroll 4
-        for (int kb = 0; kb < GS_KB; kb++) {
-            if (st * GS_KB + kb >= nb) break;
-            const uint8_t *wp = ws[buf] + (wu + fr) * WP + kb * WB;
-            long af;
-            if (DT == DT_Q8) {
-                af = *reinterpret_cast<const long *>(wp + 8 * fg);
-            } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
-                const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
-                af = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
-            }
-            const long bf = *reinterpret_cast<const long *>(xsm[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
-            const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, i32x4{0, 0, 0, 0}, 0, 0, 0);
-            const float dx = dxs[buf][kb][wt + fr];
-            const int xsum = DT == DT_Q4 ? sxs[buf][kb][wt + fr] : 0;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
-                acc[r] += ((float)isum * dws[buf][kb][wu + 4 * fg + r]) * dx;
-            }
-        }
-        __syncthreads();
-        if (st + 1 < nst) {
-            store(buf ^ 1);
+    for (int j = 0; j < GS_P - 1; j++)
+        if (j < nst) load(j, j);
+    for (int s0 = 0; s0 < nst; s0 += GS_P) {
+#pragma unroll
+        for (int j = 0; j < GS_P; j++) {
+            const int st = s0 + j;
+            if (st >= nst) break;
+            const int buf = st & 1;
+            // every wave has finished the stage that last used this buffer
+            store(j, buf);
             __syncthreads();
+            if (st + GS_P - 1 < nst) load((j + GS_P - 1) % GS_P, st + GS_P - 1);
+            // the stage's fragments and scales first, then its products, then
+            // the epilogues in block order (blocks past nb contribute nothing)
+            const int nkb = min(GS_KB, nb - st * GS_KB);
+            long af[GS_KB], bf[GS_KB];
+            float dx[GS_KB];
+            f32x4 dw[GS_KB];
+            int xsum[GS_KB];
+#pragma unroll
+            for (int kb = 0; kb < GS_KB; kb++) {
+                const uint8_t *wp = ws[buf] + (wu + fr) * WP + kb * WB;
+                if (DT == DT_Q8) {
+                    af[kb] = *reinterpret_cast<const long *>(wp + 8 * fg);
+                } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
+                    const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
+                    af[kb] = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
+                }
+                bf[kb] = *reinterpret_cast<const long *>(xsm[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
+                dx[kb] = dxs[buf][kb][wt + fr];
+                dw[kb] = *reinterpret_cast<const f32x4 *>(&dws[buf][kb][wu + 4 * fg]);
+                xsum[kb] = DT == DT_Q4 ? sxs[buf][kb][wt + fr] : 0;
+            }
+            i32x4 d[GS_KB];
+#pragma unroll
+            for (int kb = 0; kb < GS_KB; kb++)
+                d[kb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[kb], bf[kb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int kb = 0; kb < GS_KB; kb++) {
+                if (kb >= nkb) break;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
+                    acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+                }
+            }
         }
     }
     const int t = t0 + wt + fr;

@@ -234,6 +234,7 @@ constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores
 // and the small models then match the reference's deterministic build to
 // rounding.  Longer passes run the attention on matrix cores.
 constexpr int PF_EXACT_KEYS = 512;
+constexpr int PF_GRAPHS = 8;   // prefill pass graphs kept per state
 enum { PF_AUTO = 0, PF_EXACT = 1, PF_MFMA = 2 };
 
 // A captured run of device-loop steps.  One graph launch per token leaves
@@ -285,11 +286,18 @@ struct EhipState {
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
+    // one hipGraph per prefill pass shape (first position, tokens, whether it
+    // ends the prompt and so runs the head), least recently used evicted
+    struct PfGraph { StepGraph sg; int pos0 = -1, n = 0, last = 0; unsigned long long used = 0; };
+    PfGraph pfg[PF_GRAPHS];
+    unsigned long long pf_clock = 0;
     StepGraph gen[2];   // device greedy loop: 1 step, GEN_UNROLL steps
     // device sampler: xorshift64* state, history ring, candidates; the
     // sampling decode graph is captured for one parameter set
     unsigned long long *smp_rng; int *smp_meta, *smp_hist; int smp_hist_cap;
     float *smp_psum, *smp_cval; int *smp_cidx, *smp_cnt;
+    // sampling with any top_k: every token's e, sort keys, running sums
+    float *smp_we, *smp_wcum; unsigned long long *smp_wk;
     StepGraph smp[2];   // device sampling loop: 1 step, GEN_UNROLL steps
     SampleParams smp_graph_p; int smp_graph_cap;
     hipEvent_t ev0, ev1;
@@ -335,6 +343,7 @@ extern "C" void ehip_state_destroy(EhipState *s) {
     if (s->graph) (void)hipGraphDestroy(s->graph);
     for (StepGraph &g : s->gen) graph_free(g);
     for (StepGraph &g : s->smp) graph_free(g);
+    for (auto &pg : s->pfg) graph_free(pg.sg);
     if (s->smp_hist) (void)hipFree(s->smp_hist);
     for (void *p : s->allocs) (void)hipFree(p);
     if (s->tokpos_h) (void)hipHostFree(s->tokpos_h);
@@ -467,7 +476,10 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->smp_cnt = (int *)salloc(s, 4 * 2 * SAMPLE_GRID, true)) &&
               (s->smp_psum = (float *)salloc(s, 4 * SAMPLE_GRID)) &&
               (s->smp_cval = (float *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX)) &&
-              (s->smp_cidx = (int *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX));
+              (s->smp_cidx = (int *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX)) &&
+              (s->smp_we = (float *)salloc(s, 4 * (size_t)c.vocab_size)) &&
+              (s->smp_wcum = (float *)salloc(s, 4 * (size_t)c.vocab_size)) &&
+              (s->smp_wk = (unsigned long long *)salloc(s, 8 * 2 * (size_t)sample_wide_pad(c.vocab_size)));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
     if (ok && s->pf_mode != PF_MFMA)
         ok = (s->pf_scores = (float *)salloc(s, 4 * ex_rows * ex_ldk * c.n_heads)) &&
@@ -796,15 +808,11 @@ static SampleArgs sample_args(EhipState *s, const SampleParams &p, int cap, int 
     a.psum = s->smp_psum; a.scnt = s->smp_cnt; a.cval = s->smp_cval; a.cidx = s->smp_cidx;
     a.am_val = s->am_val; a.am_idx = s->am_idx;
     a.tokpos = s->tokpos_d; a.out = s->gen_tok; a.cap = s->ctx;
+    a.we = s->smp_we; a.wkeys = s->smp_wk; a.wcum = s->smp_wcum;
     return a;
 }
 
-static bool sampler_supported(const EmberSampler *smp) {
-    return smp->temperature <= 0.0f || (smp->top_k >= 1 && smp->top_k <= SAMPLE_TOPK_MAX);
-}
-
 extern "C" int ehip_sample(EhipState *s, const float *logits, int n, EmberSampler *smp, int *token) {
-    if (!sampler_supported(smp)) { set_err("device sampler: top_k %d outside [1,%d]", smp->top_k, SAMPLE_TOPK_MAX); return -1; }
     if (n <= 0 || n > s->m->cfg.vocab_size) { set_err("device sampler: %d logits for a vocabulary of %d", n, s->m->cfg.vocab_size); return -1; }
     if (logits) HCHK(hipMemcpyAsync(s->logits_d, logits, 4 * (size_t)n, hipMemcpyHostToDevice, s->st), -1);
     if (sampler_upload(s, smp)) return -1;
@@ -825,7 +833,6 @@ extern "C" int ehip_generate_sampled(EhipState *s, int tok, int pos, int n, Embe
     const int V = s->m->cfg.vocab_size;
     if (n <= 0 || pos < 0 || (long)pos + n > s->ctx) { set_err("generate: positions %d..%d exceed the context of %d", pos, pos + n - 1, s->ctx); return -1; }
     if (tok < 0 || tok >= V) { set_err("generate: token id %d out of range [0,%d)", tok, V); return -1; }
-    if (!sampler_supported(smp)) { set_err("device sampler: top_k %d outside [1,%d]", smp->top_k, SAMPLE_TOPK_MAX); return -1; }
     // the host sampler is updated only after a run whose merge check passed,
     // so a re-run after the schedule fallback starts from the same state
     int rc = generate_sampled_once(s, tok, pos, n, smp, out_tokens, ms);
@@ -886,14 +893,14 @@ static int generate_sampled_once(EhipState *s, int tok, int pos, int n, EmberSam
     return 0;
 }
 
-extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
+// The launches of one prefill pass: tokens pos0 .. pos0 + mt - 1, whose ids
+// are in ids_d; `last` adds the head over the final token and the logits copy.
+static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass) {
     const EhipModel *m = s->m;
     const EhipConfig &c = m->cfg;
     const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd, hid = c.hidden_dim;
     const int stride = qd + 2 * kvd;
-    for (int c0 = 0; c0 < n; c0 += s->pf_chunk) {
-        const int mt = std::min(s->pf_chunk, n - c0);
-        HCHK(hipMemcpyAsync(s->ids_d, ids + c0, 4 * (size_t)mt, hipMemcpyHostToDevice, s->st), nullptr);
+    {
         for (int l = 0; l < c.n_layers; l++) {
             const DevLayer &y = m->layers[l];
             QuantRowsArgs q{};
@@ -902,36 +909,36 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             if (l == 0) { q.ids = s->ids_d; q.emb = m->emb; q.x_out = s->X; }
             q.xf = m->any_f32 ? s->xf : nullptr; q.qx = s->qx; q.dx = s->dxp; q.xs = s->xsum;
             // copies of the captured layer's tensors of this pass
-            const bool snap = l == s->pdbg_layer && c0 / s->pf_chunk == s->pdbg_pass;
+            const bool snap = l == s->pdbg_layer && pass == s->pdbg_pass;
             auto psnap = [&](int slot, const float *src, int stride, int width) -> int {
                 if (!snap) return 0;
                 HCHK(hipMemcpy2DAsync(s->pdbg[slot], 4 * (size_t)width, src, 4 * (size_t)stride, 4 * (size_t)width,
                                       mt, hipMemcpyDeviceToDevice, s->st), -1);
                 return 0;
             };
-            if (snap) { s->pdbg_n = mt; s->pdbg_pos = start + c0; }
-            if (l > 0 && psnap(DBG_XIN, s->X, c.dim, c.dim)) return nullptr;
+            if (snap) { s->pdbg_n = mt; s->pdbg_pos = pos0; }
+            if (l > 0 && psnap(DBG_XIN, s->X, c.dim, c.dim)) return -1;
             int rc = launch_quant_rows(s->st, q);
-            if (l == 0 && psnap(DBG_XIN, s->X, c.dim, c.dim)) return nullptr;   // the embedded rows
+            if (l == 0 && psnap(DBG_XIN, s->X, c.dim, c.dim)) return -1;   // the embedded rows
             GemmArgs g{};
             g.W = y.qkv; g.units = stride; g.n = mt; g.qx = s->qx; g.dx = s->dxp; g.xs = s->xsum; g.xf = q.xf;
             g.out = s->QKV; g.out_stride = stride; g.bias = y.bias_qkv;
             rc |= launch_gemm(s->st, EPI_STORE, g);
-            if (psnap(DBG_QKV, s->QKV, stride, stride)) return nullptr;
+            if (psnap(DBG_QKV, s->QKV, stride, stride)) return -1;
             QkPostArgs p{};
             p.qkv = s->QKV; p.stride = stride; p.q_norm = y.q_norm; p.k_norm = y.k_norm;
             p.rope = s->rope; p.eps = c.norm_eps; p.rope_style = c.rope_style;
             AttnArgs at = attn_args(s, l);
             p.kc = at.kc; p.vc = at.vc; p.kv_dim = kvd; p.hd = hd; p.n_heads = c.n_heads;
-            p.n_kv = c.n_kv_heads; p.pos_base = start + c0; p.n_tok = mt;
+            p.n_kv = c.n_kv_heads; p.pos_base = pos0; p.n_tok = mt;
             rc |= launch_qkpost(s->st, s->f16kv, p);
-            at.q = s->QKV; at.q_stride = stride; at.pos_base = start + c0; at.n_tok = mt;
+            at.q = s->QKV; at.q_stride = stride; at.pos_base = pos0; at.n_tok = mt;
             at.out = s->O;
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
-            at.ldk = attn_prefill_ldk(start + c0, mt);
-            const bool exact = s->pf_mode == PF_EXACT || (s->pf_mode == PF_AUTO && start + c0 + mt <= PF_EXACT_KEYS);
+            at.ldk = attn_prefill_ldk(pos0, mt);
+            const bool exact = s->pf_mode == PF_EXACT || (s->pf_mode == PF_AUTO && pos0 + mt <= PF_EXACT_KEYS);
             rc |= exact ? launch_attention(s->st, s->f16kv, at) : launch_attention_mfma(s->st, s->f16kv, at);
-            if (psnap(DBG_O, s->O, qd, qd)) return nullptr;
+            if (psnap(DBG_O, s->O, qd, qd)) return -1;
             QuantRowsArgs q2{};
             q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;
             q2.xf = q.xf; q2.qx = s->qx; q2.dx = s->dxp; q2.xs = s->xsum;
@@ -940,7 +947,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             g2.W = y.wo; g2.units = c.dim; g2.n = mt; g2.qx = s->qx; g2.dx = s->dxp; g2.xs = s->xsum;
             g2.xf = q.xf; g2.out = s->X; g2.out_stride = c.dim;
             rc |= launch_gemm(s->st, EPI_RESID, g2);
-            if (psnap(DBG_XMID, s->X, c.dim, c.dim)) return nullptr;
+            if (psnap(DBG_XMID, s->X, c.dim, c.dim)) return -1;
             QuantRowsArgs q3 = q;
             q3.ids = nullptr; q3.norm_w = y.ffn_norm;
             rc |= launch_quant_rows(s->st, q3);
@@ -948,7 +955,7 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             g3.W = y.w13; g3.units = 2 * hid; g3.n = mt; g3.qx = s->qx; g3.dx = s->dxp; g3.xs = s->xsum;
             g3.xf = q.xf; g3.out = s->H; g3.out_stride = 2 * hid;
             rc |= launch_gemm(s->st, EPI_STORE, g3);
-            if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return nullptr;
+            if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return -1;
             QuantRowsArgs q4{};
             q4.x = s->H; q4.x_stride = 2 * hid; q4.cols = hid; q4.n = mt; q4.swiglu = 1;
             q4.xf = q.xf; q4.qx = s->qx; q4.dx = s->dxp; q4.xs = s->xsum;
@@ -957,17 +964,64 @@ extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
             g4.W = y.w2; g4.units = c.dim; g4.n = mt; g4.qx = s->qx; g4.dx = s->dxp; g4.xs = s->xsum;
             g4.xf = q.xf; g4.out = s->X; g4.out_stride = c.dim;
             rc |= launch_gemm(s->st, EPI_RESID, g4);
-            if (psnap(DBG_XOUT, s->X, c.dim, c.dim)) return nullptr;
-            if (rc) { set_err("a prefill kernel could not be launched for this shape"); return nullptr; }
+            if (psnap(DBG_XOUT, s->X, c.dim, c.dim)) return -1;
+            if (rc) { set_err("a prefill kernel could not be launched for this shape"); return -1; }
         }
-        if (c0 + mt == n) {
-            if (enq_head(s, s->X + (size_t)(mt - 1) * c.dim)) { set_err("head launch failed"); return nullptr; }
-            HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * (size_t)c.vocab_size, hipMemcpyDeviceToHost, s->st), nullptr);
+        if (last) {
+            if (enq_head(s, s->X + (size_t)(mt - 1) * c.dim)) { set_err("head launch failed"); return -1; }
+            HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * (size_t)c.vocab_size, hipMemcpyDeviceToHost, s->st), -1);
+        }
+    }
+    return 0;
+}
+
+// The graph of a prefill pass shape, captured on first use.
+static hipGraphExec_t prefill_graph(EhipState *s, int pos0, int mt, bool last, int pass) {
+    EhipState::PfGraph *hit = nullptr, *lru = &s->pfg[0];
+    for (auto &pg : s->pfg) {
+        if (pg.sg.x && pg.pos0 == pos0 && pg.n == mt && pg.last == (int)last) hit = &pg;
+        if (pg.used < lru->used) lru = &pg;
+    }
+    if (!hit) {
+        hit = lru;
+        graph_free(hit->sg);
+        HCHK(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), nullptr);
+        const int rc = enq_prefill_pass(s, pos0, mt, last, pass);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(s->st, &g);
+        if (rc) { if (g) (void)hipGraphDestroy(g); return nullptr; }
+        if (e != hipSuccess) { set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return nullptr; }
+        hit->sg.g = g;
+        if (hipGraphInstantiate(&hit->sg.x, g, nullptr, nullptr, 0) != hipSuccess) {
+            graph_free(hit->sg);
+            set_err("prefill graph instantiation failed");
+            return nullptr;
+        }
+        hit->pos0 = pos0; hit->n = mt; hit->last = last;
+    }
+    hit->used = ++s->pf_clock;
+    return hit->sg.x;
+}
+
+extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
+    for (int c0 = 0; c0 < n; c0 += s->pf_chunk) {
+        const int mt = std::min(s->pf_chunk, n - c0), pass = c0 / s->pf_chunk;
+        const bool last = c0 + mt == n;
+        HCHK(hipMemcpyAsync(s->ids_d, ids + c0, 4 * (size_t)mt, hipMemcpyHostToDevice, s->st), nullptr);
+        // one graph per pass shape; eager launches while a layer's tensors
+        // are being captured for inspection, or with graphs switched off
+        if (s->graph_mode && s->pdbg_layer < 0) {
+            const hipGraphExec_t x = prefill_graph(s, start + c0, mt, last, pass);
+            if (!x) return nullptr;
+            HCHK(hipGraphLaunch(x, s->st), nullptr);
+        } else if (enq_prefill_pass(s, start + c0, mt, last, pass)) {
+            return nullptr;
         }
     }
     HCHK(hipStreamSynchronize(s->st), nullptr);
     return s->logits_h;
 }
+
 
 // ------------------------------------------------------- inspection ----
 extern "C" int ehip_kv_read(EhipState *s, int which, int layer, int n_pos, void *host) {

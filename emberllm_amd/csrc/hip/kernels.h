@@ -165,8 +165,8 @@ int launch_argmax_merge(hipStream_t st, const float *pval, const int *pidx, int 
 // ember_sample (src/sample.c:76-175) on the device: penalties over a device
 // history ring, then either the first maximum (temperature <= 0) or
 // temperature -> softmax -> top-k -> min-p -> top-p -> one xorshift64* draw,
-// for top_k in [1, SAMPLE_TOPK_MAX].  The chosen token is accepted into the
-// ring and fed to the decode loop as the argmax path does (tokpos/out).
+// for any top_k (0 = no cap).  The chosen token is accepted into the ring and
+// fed to the decode loop as the argmax path does (tokpos/out).
 struct SampleParams {
     float temperature, top_p, min_p, repeat_penalty, presence_penalty, frequency_penalty;
     int top_k;
@@ -184,8 +184,19 @@ struct SampleArgs {
     float *am_val; int *am_idx;      // per-part maxima (the greedy winners)
     int nparts;                      // > 0: am_val already holds that many for these logits
     int *tokpos; int *out; int cap;  // as ArgmaxArgs
+    // top_k = 0 or > SAMPLE_TOPK_MAX: every token's e [n], the sort keys
+    // [2][sample_wide_pad(n)] and the running sums of the walk [n]
+    float *we; unsigned long long *wkeys; float *wcum;
 };
 int launch_sample(hipStream_t st, const SampleArgs &a);
+// keys sorted per sampler call with any top_k: n rounded up to a power of two
+// of at least one sort tile
+constexpr int SAMPLE_WIDE_TILE = 4096;
+inline int sample_wide_pad(int n) {
+    int p = SAMPLE_WIDE_TILE;
+    while (p < n) p <<= 1;
+    return p;
+}
 // ehip_last_error()'s text for this thread (ehip.hip)
 void set_error_text(const char *msg);
 // Whether launch_sample applies penalties (which change the logits after the

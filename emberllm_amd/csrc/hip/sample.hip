@@ -16,6 +16,7 @@
 // matvec can write the per-workgroup winners itself (matvec.hip), leaving
 // only the merge.
 #include <climits>
+#include <utility>
 
 #include "kernels.h"
 
@@ -560,6 +561,204 @@ __global__ __launch_bounds__(WG) void k_samp_fused(SampleArgs a) {
     }
 }
 
+// --------------------------------------------------------------------------
+// Any top_k (0 = no cap, or more than SAMPLE_TOPK_MAX): every token can be a
+// candidate, so the whole (p desc, index asc) order is formed, and with it
+// every token's probability exactly as the reference forms it: with a
+// hundred thousand candidates the running sums are ~1e-5 apart, so a
+// last-bit difference in the softmax sum would move a draw now and then.
+// Five steps:
+//   k_sw_e      e = exp(l/T - M) for every token, correctly rounded (the
+//               exponential in double precision, rounded once to float: what
+//               the host's expf returns);
+//   k_sw_sum    one wave: S = the sum of e in index order, one addition at a
+//               time (sample.c:131-133);
+//   k_sw_tile   p = e / S and a 64-bit key per token, ~bits(p) above the
+//               index, whose ascending order is the reference's stable
+//               descending sort; 4096 keys per workgroup sorted in LDS
+//               (bitonic network);
+//   k_sw_merge  runs of L sorted keys merged pairwise by rank: each key's
+//               place is its index in its run plus the number of keys of the
+//               other run before it (a binary search), log2(n / 4096) passes;
+//   k_sw_draw   one wave: top-k cap, min-p (a search of the sorted p), then
+//               the running sum in sorted order, one addition at a time as
+//               the reference does (sample.c:149-175), stopping where it
+//               reaches top_p and keeping every partial sum; the draw is the
+//               first partial sum above r, found by binary search (the sums
+//               never decrease).
+// The two sequential sums are the part that cannot be parallelized exactly;
+// each costs about one dependent addition per token.
+
+// e of a logit, correctly rounded
+__device__ __forceinline__ float sw_e(float l, float T, float M) { return (float)exp((double)(l / T - M)); }
+
+// The sum of the 64 lanes' v in lane order, added to acc one value at a time;
+// lane q receives the running sum through its own value.
+__device__ __forceinline__ float sw_chain(float &acc, float v) {
+    float mine = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 64; q++) {
+        acc += lane_f(v, q);
+        mine = (int)threadIdx.x == q ? acc : mine;
+    }
+    return mine;
+}
+
+__global__ __launch_bounds__(WG) void k_sw_e(SampleArgs a) {
+    __shared__ float red[NWAVE];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const float T = a.p.temperature;
+    int lo, hi;
+    samp_slice(a.n, lo, hi);
+    float g = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SAMP_PARTS; k++)
+        if (tid + k * WG < a.nparts) g = fmaxf(g, a.am_val[tid + k * WG]);
+    g = wave_max(g);
+    if (lane == 0) red[w] = g;
+    __syncthreads();
+    // max(l) / T == max(l / T): correctly rounded division is monotone
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) / T;
+    float l[SAMP_E];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) l[k] = a.logits[min(lo + tid + k * WG, a.n - 1)];
+#pragma unroll
+    for (int k = 0; k < SAMP_E; k++) {
+        const int i = lo + tid + k * WG;
+        if (k * WG < hi - lo && i < hi) a.we[i] = sw_e(l[k], T, M);
+    }
+}
+
+// one wave: S = e_0 + e_1 + ... in index order, into psum[0]
+__global__ __launch_bounds__(64) void k_sw_sum(SampleArgs a) {
+    const int lane = threadIdx.x;
+    float acc = 0.0f;
+    float nxt = a.we[min(lane, a.n - 1)];
+    for (int c0 = 0; c0 < a.n; c0 += 64) {
+        const float v = c0 + lane < a.n ? nxt : 0.0f;   // + 0 past the end changes nothing
+        nxt = a.we[min(c0 + 64 + lane, a.n - 1)];      // the next chunk's load in flight
+        (void)sw_chain(acc, v);
+    }
+    if (lane == 0) a.psum[0] = acc;
+}
+
+constexpr int SW_PER = SAMPLE_WIDE_TILE / WG;   // keys per thread in the tile sort
+
+__global__ __launch_bounds__(WG) void k_sw_tile(SampleArgs a) {
+    __shared__ unsigned long long ks[SAMPLE_WIDE_TILE];
+    const int tid = threadIdx.x;
+    const float S = a.psum[0];
+    const int base = blockIdx.x * SAMPLE_WIDE_TILE;
+#pragma unroll
+    for (int k = 0; k < SW_PER; k++) {
+        const int e = tid + k * WG, i = base + e;
+        unsigned long long key = ~0ull;   // padding sorts last
+        if (i < a.n) {
+            const float p = a.we[i] / S;
+            key = ((unsigned long long)~__float_as_uint(p) << 32) | (unsigned)i;
+        }
+        ks[e] = key;
+    }
+    for (int k = 2; k <= SAMPLE_WIDE_TILE; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            __syncthreads();
+            for (int e = tid; e < SAMPLE_WIDE_TILE / 2; e += WG) {
+                // pair (x, x + j), x with bit j clear; ascending where bit k of x is clear
+                const int x = 2 * e - (e & (j - 1));
+                const unsigned long long u = ks[x], v = ks[x + j];
+                const bool up = (x & k) == 0;
+                if ((u > v) == up) { ks[x] = v; ks[x + j] = u; }
+            }
+        }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SW_PER; k++) a.wkeys[base + tid + k * WG] = ks[tid + k * WG];
+}
+
+// src runs of L keys, pairs (2r, 2r + 1) merged into dst runs of 2L.  A key of
+// the first run goes after the other run's smaller keys, one of the second
+// run after its smaller or equal ones (equal keys are padding), so every
+// destination is distinct.
+__global__ __launch_bounds__(WG) void k_sw_merge(const unsigned long long *src, unsigned long long *dst, int L) {
+    const int i = blockIdx.x * WG + threadIdx.x;
+    const unsigned long long key = src[i];
+    const int r = i / L, j = i % L, b = (r & ~1) * L;
+    const bool first = (r & 1) == 0;
+    const unsigned long long *o = src + (first ? b + L : b);
+    int lo = 0, hi = L;   // count of o[] before key
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const unsigned long long v = o[mid];
+        if (first ? v < key : v <= key) lo = mid + 1;
+        else hi = mid;
+    }
+    dst[b + j + lo] = key;
+}
+
+__global__ __launch_bounds__(64) void k_sw_draw(SampleArgs a, const unsigned long long *keys) {
+    const int lane = threadIdx.x;
+    const SampState st = samp_state_load(a);
+    auto pof = [](unsigned long long k) { return __uint_as_float(~(unsigned)(k >> 32)); };
+    int m = a.p.top_k > 0 && a.p.top_k < a.n ? a.p.top_k : a.n;
+    // min-p (sample.c:145-150): keep the first token, then while p >= min_p * p_0
+    if (a.p.min_p > 0.0f && a.p.min_p < 1.0f) {
+        const float thresh = a.p.min_p * pof(keys[0]);
+        for (int c0 = 1; c0 < m; c0 += 64) {
+            const int i = c0 + lane;
+            const unsigned long long drop = __ballot(i < m && !(pof(keys[min(i, m - 1)]) >= thresh));
+            if (drop) { m = c0 + __builtin_ctzll(drop); break; }
+        }
+    }
+    // the running sum in sorted order; lane q keeps the sum through candidate c0 + q
+    const bool tp = a.p.top_p > 0.0f && a.p.top_p < 1.0f;
+    float cum = 0.0f, cutoff = 0.0f;
+    bool done = false;
+    for (int c0 = 0; c0 < m && !done; c0 += 64) {
+        const int i = c0 + lane;
+        const float pv = i < m ? pof(keys[i]) : 0.0f;   // + 0 past the end changes nothing
+        const float mine = sw_chain(cum, pv);
+        int last = m - 1;
+        if (tp) {
+            const unsigned long long hit = __ballot(i < m && mine >= a.p.top_p);
+            if (hit) { last = c0 + __builtin_ctzll(hit); done = true; }
+        }
+        if (i < m && i <= last) a.wcum[i] = mine;
+        if (done) { m = last + 1; cutoff = lane_f(mine, last - c0); }
+    }
+    if (!done) cutoff = cum;
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's partial sums are stored
+    unsigned long long x = st.rng;
+    x ^= x >> 12; x ^= x << 25; x ^= x >> 27;
+    const unsigned int u = (unsigned int)((x * 0x2545F4914F6CDD1DULL) >> 32);
+    const float r = (float)(u >> 8) / 16777216.0f * cutoff;
+    int lo = 0, hi = m;   // first i < m with r < wcum[i]; none: the last candidate
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (r < a.wcum[mid]) hi = mid;
+        else lo = mid + 1;
+    }
+    const int chosen = (int)(unsigned)keys[min(lo, m - 1)];
+    if (lane == 0) {
+        a.rng[0] = x;
+        samp_emit(a, st, chosen);
+    }
+}
+
+static int launch_sample_wide(hipStream_t st, const SampleArgs &b) {
+    if (!b.we || !b.wkeys || !b.wcum) return -1;
+    const int pad = sample_wide_pad(b.n);
+    hipLaunchKernelGGL(k_sw_e, dim3(SAMPLE_GRID), dim3(WG), 0, st, b);
+    hipLaunchKernelGGL(k_sw_sum, dim3(1), dim3(64), 0, st, b);
+    hipLaunchKernelGGL(k_sw_tile, dim3(pad / SAMPLE_WIDE_TILE), dim3(WG), 0, st, b);
+    unsigned long long *src = b.wkeys, *dst = b.wkeys + pad;
+    for (int L = SAMPLE_WIDE_TILE; L < pad; L <<= 1) {
+        hipLaunchKernelGGL(k_sw_merge, dim3(pad / WG), dim3(WG), 0, st, src, dst, L);
+        std::swap(src, dst);
+    }
+    hipLaunchKernelGGL(k_sw_draw, dim3(1), dim3(64), 0, st, b, (const unsigned long long *)src);
+    return 0;
+}
+
 // greedy with penalties: first maximum over the penalized logits
 __global__ void k_samp_greedy_emit(SampleArgs a) {
     if (threadIdx.x == 0) {
@@ -591,7 +790,7 @@ int launch_sample(hipStream_t st, const SampleArgs &a) {
         hipLaunchKernelGGL(k_samp_greedy_emit, dim3(1), dim3(64), 0, st, a);
         return 0;
     }
-    if (a.p.top_k < 1 || a.p.top_k > SAMPLE_TOPK_MAX) return -1;
+    const bool wide = a.p.top_k < 1 || a.p.top_k > SAMPLE_TOPK_MAX;
     SampleArgs b = a;
     if (pen || b.nparts <= 0) {   // per-part maxima of the logits as they now are
         ArgmaxArgs g{};
@@ -602,6 +801,7 @@ int launch_sample(hipStream_t st, const SampleArgs &a) {
         b.nparts = nb;
     }
     if (b.nparts > SAMP_PARTS * WG) return -1;
+    if (wide) return launch_sample_wide(st, b);
     hipLaunchKernelGGL(k_samp_fused, dim3(SAMPLE_GRID), dim3(WG), 0, st, b);
     return 0;
 }

@@ -90,9 +90,11 @@ int ehip_generate_greedy(EhipState *s, int tok, int pos, int n, int *out_tokens,
  * into the ring.  `logits` (host, n <= vocab floats) is copied to the device
  * and left unmodified; NULL samples (and overwrites) the logits the last
  * decode step left on the device.  The sampler's rng_state, history,
- * hist_len and hist_pos are updated as ember_sample would.  Supports
- * temperature <= 0 or top_k in [1, 64]; otherwise returns nonzero (use
- * ember_sample on the host).  Returns 0 and *token, or nonzero. */
+ * hist_len and hist_pos are updated as ember_sample would.  Any top_k:
+ * 1..64 keeps the first 64 candidates by bounds; 0 (no cap) or more than 64
+ * sorts every token's probability and walks the running sum in that order,
+ * one addition per candidate as the reference does.  Returns 0 and *token,
+ * or nonzero. */
 int ehip_sample(EhipState *s, const float *logits, int n, EmberSampler *smp, int *token);
 
 /* The generate loop of src/main.c:197-206 held on the device with the full

@@ -1,8 +1,11 @@
 """GPU parity of the device sampler (ehip_sample, ehip_generate_sampled)
 against ember_sample: the reference's own chosen tokens and RNG states
-(tests/golden/sampler.npz, from the compiled reference), and the host
-sampler (itself pinned to the reference) on vocabulary-sized logits with
-ties.  Chosen tokens and RNG states are integers and must match exactly.
+(tests/golden/sampler.npz, from the compiled reference: seven settings,
+top_k 0, 5, 40 and 100 among them), and the host sampler (itself pinned to
+the reference) on vocabulary-sized logits with ties.  top_k 1..64 takes the
+bounded candidate path, top_k 0 or above 64 the whole-vocabulary sort and
+sequential walk.  Chosen tokens and RNG states are integers and must match
+exactly.
 """
 import ctypes
 import os
@@ -42,10 +45,6 @@ def sampler(temp, top_p, top_k, seed, rp=1.0, last_n=0, pres=0.0, freq=0.0, min_
     return s
 
 
-def supported(temp, top_k):
-    return temp <= 0.0 or 1 <= top_k <= 64
-
-
 def test_device_sampler_reference_golden():
     g = np.load(os.path.join(GOLD, "sampler.npz"))
     V = g["logits"].shape[1]
@@ -53,15 +52,13 @@ def test_device_sampler_reference_golden():
     eng = emberllm.Engine(small_model(V))
     ran = 0
     for k, (t, p, topk, seed, rp, ln, pr, fr, mp) in enumerate(g["settings"]):
-        if not supported(t, int(topk)):
-            continue
         s = sampler(t, p, topk, seed, rp, ln, pr, fr, mp)
         for i in range(g["logits"].shape[0]):
             c = eng.sample(g["logits"][i], s)
             assert c == g["chosen"][k, i] and s.rng_state == g["states"][k, i], (k, i, c, g["chosen"][k, i])
         lib().ember_sampler_free(ctypes.byref(s))
         ran += 1
-    assert ran >= 3
+    assert ran == len(g["settings"])
     eng.close()
 
 
@@ -71,7 +68,12 @@ def test_device_sampler_reference_golden():
     dict(temp=0.7, top_p=0.95, top_k=64, min_p=0.05),
     dict(temp=1.3, top_p=0.8, top_k=20, rp=1.2, last_n=32, pres=0.3, freq=0.2),
     dict(temp=0.0, top_p=0.9, top_k=0, rp=1.5, last_n=8),
-], ids=["t08p09k40", "k1", "minp", "penalties", "greedy-penalties"])
+    dict(temp=0.8, top_p=0.9, top_k=0),
+    dict(temp=1.0, top_p=1.0, top_k=0),
+    dict(temp=0.6, top_p=0.8, top_k=100, min_p=0.02),
+    dict(temp=1.1, top_p=0.97, top_k=1000, rp=1.2, last_n=32, pres=0.3, freq=0.2),
+], ids=["t08p09k40", "k1", "minp", "penalties", "greedy-penalties", "k0", "k0-p1-whole-vocab",
+        "k100-minp", "k1000-penalties"])
 def test_device_sampler_matches_host_on_vocab_logits(params):
     V = 151936
     say(f"vocab {V}: {params}")
@@ -93,17 +95,20 @@ def test_device_sampler_matches_host_on_vocab_logits(params):
     eng.close()
 
 
+@pytest.mark.parametrize("top_k", [50, 0], ids=["k50", "k0"])
 @pytest.mark.parametrize("kind", ["flat", "two-level", "quantized", "one-hot", "spread-ties"])
-def test_device_sampler_degenerate_logits(kind):
-    """Flat and heavily tied logits: many tokens share the bound, which sends
-    the sampler down its whole-vocabulary path; "spread-ties" (514 tokens tied
-    at the top, about 8 per slice) takes its bitonic sort of up to 1024."""
+def test_device_sampler_degenerate_logits(kind, top_k):
+    """Flat and heavily tied logits.  With top_k 50 many tokens share the
+    bound, which sends the bounded path through its whole-vocabulary stream;
+    "spread-ties" (514 tokens tied at the top, about 8 per slice) takes its
+    bitonic sort of up to 1024.  With top_k 0 the ties are ordered by index
+    in the full sort."""
     V = 151936
-    say(f"vocab {V}: {kind} logits")
+    say(f"vocab {V}: {kind} logits, top_k {top_k}")
     eng = emberllm.Engine(small_model(V))
     rng = np.random.default_rng(5)
-    a = sampler(0.9, 0.95, 50, 31)
-    b = sampler(0.9, 0.95, 50, 31)
+    a = sampler(0.9, 0.95, top_k, 31)
+    b = sampler(0.9, 0.95, top_k, 31)
     for step in range(4):
         if kind == "flat":
             lg = np.full(V, 0.25, np.float32)
@@ -124,8 +129,9 @@ def test_device_sampler_degenerate_logits(kind):
     eng.close()
 
 
+@pytest.mark.parametrize("top_k", [40, 0], ids=["k40", "k0"])
 @pytest.mark.parametrize("penalties", [True, False], ids=["penalties", "plain"])
-def test_generate_sampled_equals_host_loop(penalties):
+def test_generate_sampled_equals_host_loop(penalties, top_k):
     """ehip_generate_sampled = the generate loop of forward + ember_sample.
     Without penalties the lm_head's per-workgroup winners feed the sampler."""
     path = configs.model_path("t_qwen3")
@@ -135,8 +141,8 @@ def test_generate_sampled_equals_host_loop(penalties):
     a.prefill(ids)
     lg = b.prefill(ids)
     pen = dict(rp=1.1, last_n=16) if penalties else {}
-    sa = sampler(0.8, 0.9, 40, 4242, **pen)
-    sb = sampler(0.8, 0.9, 40, 4242, **pen)
+    sa = sampler(0.8, 0.9, top_k, 4242, **pen)
+    sb = sampler(0.8, 0.9, top_k, 4242, **pen)
     for t in ids:
         lib().ember_sampler_accept(ctypes.byref(sa), int(t))
         lib().ember_sampler_accept(ctypes.byref(sb), int(t))

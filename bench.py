@@ -177,6 +177,10 @@ def main():
     ap.add_argument("--sampled-only", action="store_true",
                     help="profiling aid: fill the cache to --depth, run only the device sampling loop "
                          "(T 0.8, top-k 40, top-p 0.9) and print its rate; no JSON line")
+    ap.add_argument("--read-sweep", action="store_true",
+                    help="only measure the streaming read bandwidth over buffers of 16 MiB to 4 GiB "
+                         "(repeated passes over one buffer: what fits in the 256 MB Infinity Cache is "
+                         "re-read from it) and print one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 64 MiB device-to-device 8 times (a kernel of known traffic, for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -201,6 +205,17 @@ def main():
     if lib.ehip_device_count() <= 0:
         print("bench.py: no GPU visible to the HIP runtime", file=sys.stderr)
         sys.exit(1)
+    if args.read_sweep:
+        # a 2-layer model is enough to own a state; the kernel reads its own buffers
+        eng = emberllm.Engine(configs.model_path("t_llama"), ctx=64)
+        sweep = {}
+        for mib in (16, 32, 64, 128, 192, 256, 384, 512, 1024, 4096):
+            reps = max(4, min(200, (8 << 30) // (mib << 20)))   # about 8 GiB read per size
+            sweep[mib] = round(eng.measure_read_bw(mib << 20, reps), 1)
+            log(f"read {mib} MiB x {reps}: {sweep[mib]:.0f} GB/s")
+        eng.close()
+        print(json.dumps({"read_sweep_GB_s_by_MiB": sweep, "passes": "about 8 GiB per size after one untimed pass"}))
+        return
     c = configs.ALL[args.model]
     K, W, depth = args.steps, args.warmup, args.depth
     e_kv = 2 if args.kv == "f16" else 4

@@ -13,6 +13,11 @@
 // into equal chunks, one per workgroup of that head; with max_chunks =
 // ATT_DEC_WPC * #CUs / n_kv every CU streams the same share whatever the position (a CU
 // holding one more chunk than the others would set the kernel's length).
+// With the in-kernel merge the grid is 1-D instead: 8 * xm_slots workgroups,
+// workgroup L on XCD L % 8 (round-robin dispatch) taking slot L / 8 there;
+// the kv heads g = x, x + 8, ... of XCD x share its slots as chunks, so every
+// chunk of a kv head runs on one XCD whatever the number of kv heads (with 8
+// kv heads this is the 2-D grid above, slot for chunk).
 // Chunks hold at least ATT_DEC_RMIN rows: at short contexts a few chunks
 // (and a short merge) beat many chunks of two or three rows.  A
 // workgroup serves all kv_mul query heads of its kv head from the same K/V
@@ -121,8 +126,13 @@ template <int HD, bool F16> struct DecLay {
     static_assert(HD % PE == 0 && P % 2 == 0, "head_dim must split into an even number of pieces");
 };
 
-template <int HD, int GM, bool F16, int NL, int NW, bool XM>
+// XMODE: 0 = chunk partials for k_attn_merge; 1 = in-kernel merge on the
+// 2-D grid (n_kv a multiple of 8: chunk c of kv head g is workgroup
+// g + n_kv c, max_chunks = 8 xm_slots / n_kv); 2 = in-kernel merge on the
+// 1-D grid of 8 * xm_slots.
+template <int HD, int GM, bool F16, int NL, int NW, int XMODE>
 __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
+    constexpr bool XM = XMODE != 0;
     using L = DecLay<HD, F16>;
     constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL;
     constexpr int NT = NW * 64, RPB = NW * RPL;   // threads, rows per workgroup load
@@ -136,7 +146,22 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     __shared__ int sm_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = blockIdx.x, c = blockIdx.y;   // kv heads vary fastest: neighbours read whole cache rows
+    int g, c, nchunk;   // kv head, chunk, chunks of the kv head
+    if constexpr (XMODE == 2) {
+        // the mapping's arguments are read before anything depends on them,
+        // so their scalar loads are in flight together
+        asm volatile("" ::"s"(a.n_kv), "s"(a.xm_slots), "s"(a.q), "s"(a.tokpos), "s"(a.xm_xcc));
+        const int L = blockIdx.x, x = L & 7, s = L >> 3;
+        const int H = x < a.n_kv ? (a.n_kv - 1 - x) / 8 + 1 : 0;   // kv heads on this XCD
+        if (H == 0) return;
+        nchunk = a.xm_slots / H;
+        g = x + 8 * (s % H);
+        c = s / H;
+        if (c >= nchunk) return;
+    } else {
+        g = blockIdx.x; c = blockIdx.y;   // kv heads vary fastest: neighbours read whole cache rows
+        nchunk = a.max_chunks;
+    }
     const int G = a.n_heads / a.n_kv;
     const int xcc_want = XM ? a.xm_xcc[g] : 0;
     const int j = lane % LPR, rw = lane / LPR;
@@ -160,10 +185,9 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
         load_floats<PE>(kw, a.k_norm + jc * PE);
     }
     const int pos = a.tokpos[1];
-    // rows [0, pos] split into equal chunks over the grid's max_chunks
-    // workgroups of this kv head (two per CU over all kv heads), at least
-    // ATT_DEC_RMIN rows each
-    const int R = dec_chunk_rows(pos, a.max_chunks);
+    // rows [0, pos] split into equal chunks over the kv head's workgroups
+    // (two per CU over all kv heads), at least ATT_DEC_RMIN rows each
+    const int R = dec_chunk_rows(pos, nchunk);
     const int nc = (pos + 1 + R - 1) / R;
     if (c >= nc) return;
     const int t0 = c * R, t1 = min(pos + 1, t0 + R);
@@ -541,17 +565,26 @@ int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu) {
     return std::max(1, std::max(by_rows, by_cus));
 }
 
+int attn_decode_slots(int ctx, int n_kv, int n_cu) {
+    const int hmax = (n_kv + 7) / 8;   // kv heads on the busiest XCD
+    const int by_rows = hmax * ((ctx + ATT_DEC_CR - 1) / ATT_DEC_CR);
+    return std::max(hmax, std::max(by_rows, ATT_DEC_WPC * n_cu / 8));
+}
+
 template <int HD, bool F16, int GM>
 static void dec_launch(hipStream_t st, const AttnArgs &a, dim3 grid) {
     constexpr int NL = ATT_DEC_NL, NW = ATT_DEC_NW;
-    if (a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, true>), grid, dim3(NW * 64), 0, st, a);
-    else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, false>), grid, dim3(NW * 64), 0, st, a);
+    if (!a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 0>), grid, dim3(NW * 64), 0, st, a);
+    else if (grid.y > 1) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 1>), grid, dim3(NW * 64), 0, st, a);
+    else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 2>), grid, dim3(NW * 64), 0, st, a);
 }
 
 template <int HD, bool F16>
 static int dec_pick_g(hipStream_t st, const AttnArgs &a, bool with_merge) {
     const int G = a.n_heads / a.n_kv;
-    dim3 grid(a.n_kv, a.max_chunks);
+    // the in-kernel merge's 1-D grid is the 2-D one, chunk for slot, when n_kv
+    // is a multiple of 8 (whose prologue needs no mapping)
+    const dim3 grid = !a.xm_cnt || a.n_kv % 8 == 0 ? dim3(a.n_kv, a.max_chunks) : dim3(8 * a.xm_slots);
     if (G <= 1) dec_launch<HD, F16, 1>(st, a, grid);
     else if (G <= 2) dec_launch<HD, F16, 2>(st, a, grid);
     else if (G <= 4) dec_launch<HD, F16, 4>(st, a, grid);
@@ -565,8 +598,17 @@ static int dec_pick_g(hipStream_t st, const AttnArgs &a, bool with_merge) {
 
 int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_merge) {
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || !a.part) return -1;
-    if (a.xm_cnt && (!a.xm_err || !a.xm_xcc)) return -1;
-    if ((long)a.max_chunks * ATT_DEC_CR < a.ctx) return -1;
+    if (a.xm_cnt) {
+        // every kv head gets xm_slots / (its XCD's kv heads) chunks of at most
+        // ATT_DEC_CR rows; with n_kv a multiple of 8 that is the 2-D grid's
+        // max_chunks = 8 xm_slots / n_kv
+        const int per_head = a.xm_slots / ((a.n_kv + 7) / 8);
+        if (!a.xm_err || !a.xm_xcc || a.xm_slots <= 0) return -1;
+        if (a.n_kv % 8 == 0 ? a.max_chunks != 8 * a.xm_slots / a.n_kv : a.max_chunks < a.xm_slots) return -1;
+        if ((long)per_head * ATT_DEC_CR < a.ctx) return -1;
+    } else if ((long)a.max_chunks * ATT_DEC_CR < a.ctx) {
+        return -1;
+    }
     switch (a.hd) {
         case 48: return f16kv ? dec_pick_g<48, true>(st, a, with_merge) : dec_pick_g<48, false>(st, a, with_merge);
         case 64: return f16kv ? dec_pick_g<64, true>(st, a, with_merge) : dec_pick_g<64, false>(st, a, with_merge);

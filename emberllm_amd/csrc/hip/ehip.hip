@@ -264,7 +264,8 @@ struct EhipState {
     float *x, *qkv, *o, *h, *logits_d, *logits_h;
     float *part;
     float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
-    int mc_dec;
+    int mc_dec;     // chunks per kv head, two-kernel merge
+    int xm_slots;   // slots per XCD, in-kernel merge (attn_decode.hip)
     // in-kernel merge of the decode attention chunks (see attn_decode.hip):
     // arrival counters [n_layers][n_kv][XM_CNT_STRIDE], the XCD of each kv
     // head's workgroups, and the error flag, which sits at logits_d[vocab] so
@@ -360,33 +361,35 @@ static int env_int(const char *name, int dflt) {
 }
 
 // Decide whether the decode attention merges its chunks in-kernel: run the
-// probe kernel on the attention's grid and require every workgroup of each kv
-// head to report the same XCD (the dispatcher deals a grid's workgroups to
-// the XCDs round-robin, so with n_kv a multiple of the XCD count each head
-// stays on one).  EHIP_XMERGE=0 forces the merge kernel.
+// probe kernel on the attention's 1-D grid of 8 * xm_slots workgroups and
+// require the workgroups L, L + 8, L + 16, ... (the chunks of the kv heads
+// g = L % 8, L % 8 + 8, ...) to report one XCD (the dispatcher deals a
+// grid's workgroups to the XCDs round-robin).  EHIP_XMERGE=0 forces the
+// merge kernel.
 static int xm_probe(EhipState *s) {
-    const int nkv = s->m->cfg.n_kv_heads, gy = s->mc_dec;
+    const int nkv = s->m->cfg.n_kv_heads, gx = 8 * s->xm_slots;
     s->xm_on = false;
     if (!env_int("EHIP_XMERGE", 1)) return 0;
-    std::vector<int> h((size_t)nkv * gy, -1);
+    std::vector<int> h((size_t)gx, -1);
     int *d = nullptr;
     HCHK(hipMalloc(&d, 4 * h.size()), -1);
-    const int rc = launch_xcc_probe(s->st, nkv, gy, d);
+    const int rc = launch_xcc_probe(s->st, gx, 1, d);
     const hipError_t e1 = hipStreamSynchronize(s->st);
     const hipError_t e2 = hipMemcpy(h.data(), d, 4 * h.size(), hipMemcpyDeviceToHost);
     (void)hipFree(d);
     if (rc || e1 != hipSuccess || e2 != hipSuccess) { set_err("XCD probe kernel failed"); return -1; }
     bool ok = true;
-    for (int g = 0; g < nkv && ok; g++)
-        for (int y = 1; y < gy && ok; y++) ok = h[(size_t)y * nkv + g] == h[g];
+    for (int L = 8; L < gx && ok; L++) ok = h[L] == h[L % 8];
     if (!ok) return 0;
+    std::vector<int> xcc((size_t)nkv);
+    for (int g = 0; g < nkv; g++) xcc[g] = h[g % 8];
     // EHIP_XMERGE_TEST_SKEW=k records every kv head's XCD as k further on
     // (test hook): each workgroup's own check then fails, so the error path
     // can be exercised while the kernels run exactly as usual
     const int skew = env_int("EHIP_XMERGE_TEST_SKEW", 0);
     if (skew)
-        for (int g = 0; g < nkv; g++) h[g] = (h[g] + skew) & 7;
-    HCHK(hipMemcpy(s->xm_xcc, h.data(), 4 * (size_t)nkv, hipMemcpyHostToDevice), -1);
+        for (int g = 0; g < nkv; g++) xcc[g] = (xcc[g] + skew) & 7;
+    HCHK(hipMemcpy(s->xm_xcc, xcc.data(), 4 * (size_t)nkv, hipMemcpyHostToDevice), -1);
     s->xm_on = true;
     return 0;
 }
@@ -430,6 +433,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || n_cu <= 0) n_cu = 1;
     s->mc_dec = attn_decode_chunks(ctx, c.n_kv_heads, hd, n_cu);
+    s->xm_slots = attn_decode_slots(ctx, c.n_kv_heads, n_cu);
     if (s->mc_dec <= 0) {
         set_err("head_dim %d not supported by the attention kernel", hd);
         ehip_state_destroy(s);
@@ -458,7 +462,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->logits_d = (float *)salloc(s, 4 * ((size_t)c.vocab_size + 4), true)) &&
               (s->xm_cnt = (int *)salloc(s, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, true)) &&
               (s->xm_xcc = (int *)salloc(s, 4 * (size_t)c.n_kv_heads)) &&
-              (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * s->mc_dec * (hd + 2))) &&
+              (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * std::max(s->mc_dec, s->xm_slots) * (hd + 2))) &&
               (s->X = (float *)salloc(s, 4 * pfc * c.dim)) &&
               (s->QKV = (float *)salloc(s, 4 * pfc * (qd + 2 * kvd))) &&
               (s->O = (float *)salloc(s, 4 * pfc * qd)) &&
@@ -545,6 +549,9 @@ static int enq_attn_decode(EhipState *s, int l, bool with_merge = true) {
     a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
     a.part = s->part; a.max_chunks = s->mc_dec;
     if (s->xm_on) {
+        const int nkv = s->m->cfg.n_kv_heads;
+        a.xm_slots = s->xm_slots;
+        a.max_chunks = nkv % 8 == 0 ? 8 * s->xm_slots / nkv : s->xm_slots;
         a.xm_cnt = s->xm_cnt + (size_t)l * s->m->cfg.n_kv_heads * XM_CNT_STRIDE;
         a.xm_xcc = s->xm_xcc;
         a.xm_err = s->xm_err;

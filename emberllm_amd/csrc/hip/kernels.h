@@ -68,6 +68,12 @@ struct AttnArgs {
     // zero between launches; xm_xcc: the XCD of each kv head's workgroups;
     // xm_err: set nonzero by a workgroup that finds itself on another XCD.
     int *xm_cnt; const int *xm_xcc; int *xm_err;
+    // with xm_cnt: the grid is 1-D, 8 * xm_slots workgroups (max_chunks =
+    // xm_slots); workgroup L takes slot L / 8 of XCD L % 8 (where round-robin
+    // dispatch places it), whose slots the kv heads g = L % 8, L % 8 + 8, ...
+    // share as their chunks.  With n_kv a multiple of 8 that is the 2-D grid
+    // (n_kv, max_chunks = 8 xm_slots / n_kv), which is what runs.
+    int xm_slots;
     float *out;            // [n_tok][n_heads*hd]
     // prefill scratch: scores [n_heads][n_tok][ldk] (ldk >= pos_base + n_tok,
     // a multiple of 4); the maximum of each 64-key tile of a row,
@@ -91,6 +97,9 @@ int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_
 // workgroups per kv head: two per CU over all kv heads, or more when a chunk
 // would exceed ATT_DEC_CR rows (0: head_dim not supported)
 int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu);
+// slots per XCD of the in-kernel-merge grid: two workgroups per CU, or more
+// when a chunk of the XCD with the most kv heads would exceed ATT_DEC_CR rows
+int attn_decode_slots(int ctx, int n_kv, int n_cu);
 constexpr int ATT_DEC_NL = 5;       // K and V pieces per thread per batch in the decode attention
 constexpr int ATT_DEC_NW = 4;       // waves per decode attention workgroup
 constexpr int ATT_DEC_WPC = 2;      // decode attention workgroups per CU

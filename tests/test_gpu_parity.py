@@ -339,15 +339,17 @@ def test_measured_read_bandwidth():
     e.close()
 
 
-def test_xcd_check_falls_back_to_the_merge_kernel(monkeypatch):
+@pytest.mark.parametrize("name", ["qwen3_06b", "stories110m"])
+def test_xcd_check_falls_back_to_the_merge_kernel(name, monkeypatch):
     """The in-kernel merge relies on every workgroup of a kv head running on
     the XCD the state's probe recorded; each workgroup checks that and raises
     a flag.  EHIP_XMERGE_TEST_SKEW records the wrong XCDs (the kernels
     themselves run as usual), so the check fires on the first decode launch:
     the state must then switch to the two-kernel merge for good and re-run
     the work, returning exactly what a state created with that schedule
-    (EHIP_XMERGE=0) returns, through ember_forward and the device loop."""
-    name = "qwen3_06b"
+    (EHIP_XMERGE=0) returns, through ember_forward and the device loop.
+    Qwen3-0.6B has 8 kv heads (one per XCD), stories110M 12 (two on four of
+    the XCDs)."""
     path = configs.model_path(name, threads=16)
     V = configs.ALL[name]["vocab_size"]
     ids = np.arange(100) * 97 % V   # several chunks per kv head, so the merge (and its check) runs

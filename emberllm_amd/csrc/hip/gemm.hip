@@ -377,33 +377,48 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 // row), B[8 (l / 16) .. +7][l % 16] (of a token row), and outputs
 // D[4 (l / 16) + r][l % 16], r = 0..3.  The epilogue is the same
 // sum += ((float)isum * dw) * dx in block order.
-constexpr int GS_U = 32, GS_T = 32, GS_KB = 4, GS_P = 8;
+constexpr int GS_U = 32, GS_T = 32, GS_KB = 4;
 
-template <int DT, int EPI>
-__global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
+// SPLIT > 1 (K of at least 1024): the workgroup runs SPLIT of the 4-wave
+// pipelines above side by side, pipeline q over the q-th contiguous part of
+// the blocks, and adds their sums in pipeline order at the end.  The waves'
+// serial walk over K (each block's product feeds the next block's sum) is
+// then a SPLIT-th as long, and SPLIT times as many waves share each SIMD.
+template <int DT, int EPI, int SPLIT>
+__global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
+    constexpr int P = SPLIT > 1 ? 4 : 8;                       // register ring depth (stages)
     constexpr int WB = DT == DT_Q8 ? 32 : 16;                 // weight bytes per row and block
     constexpr int WROW = GS_KB * WB, XROW = GS_KB * 32;        // stage bytes per row
     constexpr int WP = WROW + 16, XP = XROW + 16;              // LDS row pitches
     constexpr int WCH = GS_U * WROW / 16, XCH = GS_T * XROW / 16;   // 16-byte chunks per stage
     constexpr int NSC = GS_KB * GS_U;                          // scales of each kind per stage
     static_assert(GS_U == GS_T && WCH <= WG && XCH == WG && NSC <= WG, "one chunk per thread and stage");
-    __shared__ __align__(16) uint8_t ws[2][GS_U * WP];
-    __shared__ __align__(16) int8_t xsm[2][GS_T * XP];
-    __shared__ __align__(16) float dws[2][GS_KB][GS_U], dxs[2][GS_KB][GS_T];
-    __shared__ int sxs[2][GS_KB][GS_T];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint8_t ws[SPLIT][2][GS_U * WP];
+    __shared__ __align__(16) int8_t xsm[SPLIT][2][GS_T * XP];
+    __shared__ __align__(16) float dws[SPLIT][2][GS_KB][GS_U], dxs[SPLIT][2][GS_KB][GS_T];
+    __shared__ int sxs[SPLIT][2][GS_KB][GS_T];
+    __shared__ __align__(16) float red[SPLIT > 1 ? SPLIT - 1 : 1][NWAVE][64][4];
+    const int tid = threadIdx.x % WG, q = threadIdx.x / WG;    // thread of pipeline q
+    const int lane = tid & 63, wave = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;
     const int u0 = blockIdx.x * GS_U, t0 = blockIdx.y * GS_T;
-    const int K = a.W.cols, nb = K / QB, nst = (nb + GS_KB - 1) / GS_KB;
+    const int K = a.W.cols, nb = K / QB;
+    const int nbq = (nb + SPLIT - 1) / SPLIT, kb0 = q * nbq, kb1 = min(nb, kb0 + nbq);   // this pipeline's blocks
+    const int nst = (nbq + GS_KB - 1) / GS_KB;                // stages, the same in every pipeline
     const int wu = (wave & 1) * 16, wt = (wave >> 1) * 16;
+    uint8_t (&wsq)[2][GS_U * WP] = ws[q];
+    int8_t (&xsq)[2][GS_T * XP] = xsm[q];
+    float (&dwq)[2][GS_KB][GS_U] = dws[q];
+    float (&dxq)[2][GS_KB][GS_T] = dxs[q];
+    int (&sxq)[2][GS_KB][GS_T] = sxs[q];
 
-    // register ring: slot j holds a stage s with s % GS_P == j
-    i32x4 wr[GS_P], xr[GS_P];
-    uint16_t dwr[GS_P];
-    float dxr[GS_P];
-    int xsr[GS_P];
+    // register ring: slot j holds a stage s with s % P == j
+    i32x4 wr[P], xr[P];
+    uint16_t dwr[P];
+    float dxr[P];
+    int xsr[P];
     auto load = [&](int j, int st) {
-        const int b0 = st * GS_KB;
+        const int b0 = kb0 + st * GS_KB;
         if (tid < WCH) {
             const int row = tid / (WROW / 16), c = (tid % (WROW / 16)) * 16;
             const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
@@ -424,49 +439,50 @@ __global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
     };
     auto store = [&](int j, int buf) {
         if (tid < WCH)
-            *reinterpret_cast<i32x4 *>(ws[buf] + (tid / (WROW / 16)) * WP + (tid % (WROW / 16)) * 16) = wr[j];
-        *reinterpret_cast<i32x4 *>(xsm[buf] + (tid / (XROW / 16)) * XP + (tid % (XROW / 16)) * 16) = xr[j];
+            *reinterpret_cast<i32x4 *>(wsq[buf] + (tid / (WROW / 16)) * WP + (tid % (WROW / 16)) * 16) = wr[j];
+        *reinterpret_cast<i32x4 *>(xsq[buf] + (tid / (XROW / 16)) * XP + (tid % (XROW / 16)) * 16) = xr[j];
         if (tid < NSC) {
-            dws[buf][tid / GS_U][tid % GS_U] = h2f(dwr[j]);
-            dxs[buf][tid / GS_T][tid % GS_T] = dxr[j];
-            if (DT == DT_Q4) sxs[buf][tid / GS_T][tid % GS_T] = xsr[j];
+            dwq[buf][tid / GS_U][tid % GS_U] = h2f(dwr[j]);
+            dxq[buf][tid / GS_T][tid % GS_T] = dxr[j];
+            if (DT == DT_Q4) sxq[buf][tid / GS_T][tid % GS_T] = xsr[j];
         }
     };
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < GS_P - 1; j++)
+    for (int j = 0; j < P - 1; j++)
         if (j < nst) load(j, j);
-    for (int s0 = 0; s0 < nst; s0 += GS_P) {
+    for (int s0 = 0; s0 < nst; s0 += P) {
 #pragma unroll
-        for (int j = 0; j < GS_P; j++) {
+        for (int j = 0; j < P; j++) {
             const int st = s0 + j;
             if (st >= nst) break;
             const int buf = st & 1;
             // every wave has finished the stage that last used this buffer
             store(j, buf);
             __syncthreads();
-            if (st + GS_P - 1 < nst) load((j + GS_P - 1) % GS_P, st + GS_P - 1);
+            if (st + P - 1 < nst) load((j + P - 1) % P, st + P - 1);
             // the stage's fragments and scales first, then its products, then
-            // the epilogues in block order (blocks past nb contribute nothing)
-            const int nkb = min(GS_KB, nb - st * GS_KB);
+            // the epilogues in block order (blocks past the pipeline's end
+            // contribute nothing)
+            const int nkb = min(GS_KB, kb1 - (kb0 + st * GS_KB));
             long af[GS_KB], bf[GS_KB];
             float dx[GS_KB];
             f32x4 dw[GS_KB];
             int xsum[GS_KB];
 #pragma unroll
             for (int kb = 0; kb < GS_KB; kb++) {
-                const uint8_t *wp = ws[buf] + (wu + fr) * WP + kb * WB;
+                const uint8_t *wp = wsq[buf] + (wu + fr) * WP + kb * WB;
                 if (DT == DT_Q8) {
                     af[kb] = *reinterpret_cast<const long *>(wp + 8 * fg);
                 } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
                     const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
                     af[kb] = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
                 }
-                bf[kb] = *reinterpret_cast<const long *>(xsm[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
-                dx[kb] = dxs[buf][kb][wt + fr];
-                dw[kb] = *reinterpret_cast<const f32x4 *>(&dws[buf][kb][wu + 4 * fg]);
-                xsum[kb] = DT == DT_Q4 ? sxs[buf][kb][wt + fr] : 0;
+                bf[kb] = *reinterpret_cast<const long *>(xsq[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
+                dx[kb] = dxq[buf][kb][wt + fr];
+                dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wu + 4 * fg]);
+                xsum[kb] = DT == DT_Q4 ? sxq[buf][kb][wt + fr] : 0;
             }
             i32x4 d[GS_KB];
 #pragma unroll
@@ -483,6 +499,17 @@ __global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
             }
         }
     }
+    if constexpr (SPLIT > 1) {   // the pipelines' sums, added in pipeline order
+        if (q > 0)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[q - 1][wave][lane][r] = acc[r];
+        __syncthreads();
+        if (q > 0) return;
+#pragma unroll
+        for (int p = 0; p < SPLIT - 1; p++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] += red[p][wave][lane][r];
+    }
     const int t = t0 + wt + fr;
     if (t >= a.n) return;
 #pragma unroll
@@ -495,6 +522,13 @@ __global__ __launch_bounds__(WG) void k_gemm_small(GemmArgs a) {
     }
 }
 
+// K of at least 1024 (32 blocks) splits into 4 pipelines when the grid fits
+// the GPU at one 1024-thread workgroup per CU (the split's LDS); shorter K
+// keeps the blocks of every output in one sequential sum, and a larger grid
+// keeps 256-thread workgroups (two rounds of split workgroups measured
+// slower: q|k|v 12.7 against 11.1 us, w1|w3 17.8 against 13.2 at 128 tokens)
+constexpr int GS_SPLIT = 4, GS_SPLIT_MIN_BLOCKS = 32, GS_SPLIT_MAX_GRID = 256;
+
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
     if (a.W.dtype == DT_Q8 || a.W.dtype == DT_Q4) {
@@ -506,9 +540,16 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         const long g64 = (long)gu * ((a.n + 63) / 64);
         if (g64 < 256 || (a.units <= 1024 && g64 < 1024)) {
             const dim3 gs((a.units + GS_U - 1) / GS_U, (a.n + GS_T - 1) / GS_T);
+            const bool split = a.W.cols / QB >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT_MAX_GRID;
 #define GSF(DT)                                                                                          \
-            if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE>), gs, dim3(WG), 0, st, a); \
-            else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID>), gs, dim3(WG), 0, st, a); \
+            if (split) {                                                                                 \
+                if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, GS_SPLIT>), gs, dim3(WG * GS_SPLIT), 0, st, a); \
+                else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, GS_SPLIT>), gs, dim3(WG * GS_SPLIT), 0, st, a); \
+                else return -1;                                                                          \
+                return 0;                                                                                \
+            }                                                                                            \
+            if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, 1>), gs, dim3(WG), 0, st, a); \
+            else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, 1>), gs, dim3(WG), 0, st, a); \
             else return -1;                                                                              \
             return 0;
             if (a.W.dtype == DT_Q8) { GSF(DT_Q8) }

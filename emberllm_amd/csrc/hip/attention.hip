@@ -544,12 +544,14 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
 #pragma unroll
     for (int d = 0; d < ND; d++) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // K rows [k0, k0 + 64) staged as ks[key][dim] and V rows as vt[dim][key]
+    // (keys past kend repeat row kend; no row sees them).  (Loading the next
+    // tile into registers during the current one's products measured no
+    // faster and cost the second wave per SIMD.)
     const int nkt = kend / FL_BK + 1;
     for (int kt = 0; kt < nkt; kt++) {
         const int k0 = kt * FL_BK;
         __syncthreads();   // the previous tile has been read
-        // stage K rows [k0, k0 + 64) as ks[key][dim] and V rows as vt[dim][key]
-        // (keys past kend repeat row kend; no row sees them)
         for (int f = tid; f < FL_BK * (HD / 4); f += WG) {
             const int key = f / (HD / 4), c = (f % (HD / 4)) * 4;
             const size_t off = (size_t)min(k0 + key, kend) * a.kv_dim + hoff + c;
@@ -571,19 +573,23 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
         }
         __syncthreads();
         // S^T: this lane gets S[row i][key 16kk + 4q + r]
+        // (the four products interleaved: consecutive MFMAs never wait on each other)
         f32x4 sc[4];
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            sc[kk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            const float *kr = &ks[(16 * kk + i) * KP + NS * q];
+        for (int kk = 0; kk < 4; kk++) sc[kk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < NS; s += 4) {
-                const float4 kv = *reinterpret_cast<const float4 *>(kr + s);
-                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qf[s], sc[kk], 0, 0, 0);
-                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qf[s + 1], sc[kk], 0, 0, 0);
-                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qf[s + 2], sc[kk], 0, 0, 0);
-                sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[s + 3], sc[kk], 0, 0, 0);
-            }
+        for (int s = 0; s < NS; s += 4) {
+            float4 kv[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) kv[kk] = *reinterpret_cast<const float4 *>(&ks[(16 * kk + i) * KP + NS * q + s]);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kk].x, qf[s], sc[kk], 0, 0, 0);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kk].y, qf[s + 1], sc[kk], 0, 0, 0);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kk].z, qf[s + 2], sc[kk], 0, 0, 0);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kk].w, qf[s + 3], sc[kk], 0, 0, 0);
         }
         // running softmax of the row (log2 units); keys past the row's position are masked
         float mx = -INFINITY;
@@ -610,17 +616,22 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
                 sc[kk][r] = p;
                 lsum += p;
             }
-        // O^T += V^T . P^T over the tile's keys in the scores' order
+        // O^T += V^T . P^T over the tile's keys in the scores' order (the
+        // output products interleaved)
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++)
+        for (int kk = 0; kk < 4; kk++) {
+            float4 vv[ND];
 #pragma unroll
-            for (int d = 0; d < ND; d++) {
-                const float4 vv = *reinterpret_cast<const float4 *>(&vt[(16 * d + i) * VP + 16 * kk + 4 * q]);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sc[kk][0], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sc[kk][1], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sc[kk][2], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sc[kk][3], o[d], 0, 0, 0);
-            }
+            for (int d = 0; d < ND; d++) vv[d] = *reinterpret_cast<const float4 *>(&vt[(16 * d + i) * VP + 16 * kk + 4 * q]);
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[d].x, sc[kk][0], o[d], 0, 0, 0);
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[d].y, sc[kk][1], o[d], 0, 0, 0);
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[d].z, sc[kk][2], o[d], 0, 0, 0);
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[d].w, sc[kk][3], o[d], 0, 0, 0);
+        }
     }
     // o[d][r] = O^T[dim 16d + 4q + r][row i]: four consecutive dims of the row
     const float inv = 1.0f / fl_quarter_sum(lsum);

@@ -6,6 +6,13 @@
 #   _ref/libember_ref_debug.so  flags of `make debug` (Makefile:57-59)
 #   _ref/libember_ref.so        flags of the optimized build (Makefile:23),
 #                               -march=x86-64-v3 in place of -march=native
+#   _ref/ember_cli              the reference's command-line program, every
+#                               source file, `make debug` flags (the CPU side
+#                               the product library's build of the same
+#                               program is compared with)
+#   _ref/ember_cli_o3           the same program with the optimized flags (its
+#                               own build-to-build deviation, the bar for
+#                               sampled completions)
 # -Wl,-Bsymbolic keeps the library's internal calls inside itself, since its
 # exported ember_* names equal the product library's.
 REF ?= /root/reference
@@ -14,7 +21,7 @@ SRC := $(filter-out $(REF)/src/main.c,$(wildcard $(REF)/src/*.c))
 COMMON = -std=c11 -D_DEFAULT_SOURCE -fPIC -shared -pthread -Wl,-Bsymbolic -w
 
 .PHONY: all
-all: _ref/libember_ref_debug.so _ref/libember_ref.so
+all: _ref/libember_ref_debug.so _ref/libember_ref.so _ref/ember_cli _ref/ember_cli_o3
 
 _ref:
 	mkdir -p _ref
@@ -24,3 +31,9 @@ _ref/libember_ref_debug.so: $(SRC) | _ref
 
 _ref/libember_ref.so: $(SRC) | _ref
 	$(CC) $(COMMON) -O3 -ffast-math -march=x86-64-v3 -funroll-loops -o $@ $(SRC) -lm
+
+_ref/ember_cli: $(wildcard $(REF)/src/*.c) | _ref
+	$(CC) -std=c11 -D_DEFAULT_SOURCE -pthread -w -O2 -fno-fast-math -ffp-contract=off -o $@ $(wildcard $(REF)/src/*.c) -lm
+
+_ref/ember_cli_o3: $(wildcard $(REF)/src/*.c) | _ref
+	$(CC) -std=c11 -D_DEFAULT_SOURCE -pthread -w -O3 -ffast-math -march=x86-64-v3 -funroll-loops -o $@ $(wildcard $(REF)/src/*.c) -lm

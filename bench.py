@@ -22,6 +22,11 @@ reported, never as `value`:
   prefill_tok_s_pp128 / _pp4096   ember_prefill at position 0 (mean of 5
                         after 1 warmup, src/main.c:251-266); the last
                         pp4096 run leaves the cache filled for the decode
+  ttft_ms_pp128 / _pp4096         the same prefills plus the first token's
+                        selection on the host (time to first token)
+  load_s                ember_model_load + ember_state_new_ex: the file
+                        mapped, weights repacked and uploaded, KV cache and
+                        scratch allocated
   roofline              the dominant kernel (split-K attention of one layer
                         at depth 4096): algorithmic bytes per launch over
                         its average duration (HIP events, isolated launches
@@ -223,10 +228,15 @@ def main():
     path = configs.model_path(args.model, threads=16)
     log(f"model {path} ready in {time.time() - t0:.1f} s")
     ctx = depth + max(K, W) + 2
+    t = time.perf_counter()
+    # ember_model_load + ember_state_new_ex: the file mapped, every weight
+    # repacked and uploaded, the KV cache and scratch allocated
     eng = emberllm.Engine(path, ctx=ctx, kv_fp16=args.kv == "f16")
+    load_s = time.perf_counter() - t
+    log(f"load (model file to a ready state, ctx {ctx}): {load_s:.2f} s")
     rng = np.random.default_rng(4096)
     V = c["vocab_size"]
-    out = {}
+    out = {"load_s": load_s}
 
     # ---- prefill --------------------------------------------------------
     def prefill_rate(n, reps=5, warm=1):
@@ -234,23 +244,27 @@ def main():
         untimed run, then the mean of `reps` timed ones; returns (mean, sd,
         last logits)."""
         ids = rng.integers(0, V, n).astype(np.int32)
-        rates = []
+        rates, firsts = [], []
         for r in range(warm + reps):
             t = time.perf_counter()
             lg = eng.prefill(ids)
             dt = time.perf_counter() - t
+            int(np.argmax(lg))   # the first generated token: time to first token
             if r >= warm:
                 rates.append(n / dt)
+                firsts.append(time.perf_counter() - t)
+        out[f"ttft_ms_pp{n}"] = float(np.mean(firsts)) * 1e3
         return float(np.mean(rates)), float(np.std(rates, ddof=1) if len(rates) > 1 else 0.0), lg
 
     if not args.decode_only:
         out["prefill_tok_s_pp128"], out["prefill_tok_s_pp128_sd"], _ = prefill_rate(128)
-        log(f"prefill pp128 {out['prefill_tok_s_pp128']:.1f} tok/s")
+        log(f"prefill pp128 {out['prefill_tok_s_pp128']:.1f} tok/s, "
+            f"time to first token {out['ttft_ms_pp128']:.2f} ms")
     # fill the cache to `depth` (also timed: pp<depth>, mean of 5 after 1 warmup)
     key = f"prefill_tok_s_pp{depth}"
     out[key], out[key + "_sd"], lg = prefill_rate(depth, reps=1 if args.decode_only else 5,
                                                   warm=0 if args.decode_only else 1)
-    log(f"prefill pp{depth} {out[key]:.1f} tok/s")
+    log(f"prefill pp{depth} {out[key]:.1f} tok/s, time to first token {out[f'ttft_ms_pp{depth}']:.2f} ms")
     tok0 = int(np.argmax(lg))
 
     def sampled_rate():

@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "../../../include/ember.h"
@@ -85,10 +86,152 @@ static size_t file_row_bytes(int dt, int cols) {
     return dt == DT_F32 ? (size_t)cols * 4 : (size_t)(cols / QB) * (dt == DT_Q8 ? 34 : 18);
 }
 
-// Repack row-concatenated matrices (all of one dtype and width) from the
-// file encoding into the device layout described in dev_common.h.
-static bool upload_mat(EhipModel *m, DMat *out, const EhipWeight *parts, const int *rows, int nparts,
-                       int cols, const char *what) {
+// Weight upload.  Every matrix is first allocated in its device layout and
+// described by one job per file tensor; the jobs' row bytes then stream
+// through a ring of pinned host slots, several tensors to a slot: host
+// threads copy the slot's rows out of the mapped file, the slot's DMA to a
+// device staging buffer and one repack launch per tensor in it are queued on
+// the upload stream, and the slot is reused once its event has passed, so the
+// host copy of one slot overlaps the transfer and repack of the previous ones.
+// The repack only moves bytes (each block's fp16 scale to the scale array,
+// its 32 or 16 quant bytes to the row's payload), so the device matrix holds
+// the file's values exactly.
+__global__ void k_repack_blocks(const uint16_t *__restrict__ src, int nrows, int nb, int bs_half,
+                                uint8_t *__restrict__ q, size_t qrow, uint16_t *__restrict__ d, size_t row0) {
+    const size_t nblk = (size_t)nrows * nb;
+    const int pay_half = bs_half - 1;
+    for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nblk; b += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = b / nb, j = b % nb;
+        const uint16_t *blk = src + b * bs_half;
+        d[(row0 + r) * nb + j] = blk[0];
+        uint16_t *dst = reinterpret_cast<uint16_t *>(q + (row0 + r) * qrow + j * (size_t)(2 * pay_half));
+        for (int i = 0; i < pay_half; i++) dst[i] = blk[1 + i];
+    }
+}
+
+namespace {
+
+// Rows [0, nrows) of one file tensor (row bytes frb) into rows row0.. of a
+// device matrix (payload q with row pitch qrow, scales d; F32: q only).
+struct UploadJob {
+    const uint8_t *src;
+    int nrows, dt, nb;
+    size_t frb, qrow, row0;
+    uint8_t *q;
+    uint16_t *d;
+};
+
+struct WeightStager {
+    static constexpr int SLOTS = 3;
+    static constexpr size_t SLOT_MAX = (size_t)32 << 20;
+    struct Seg { size_t job, r, n, off; };   // rows [r, r+n) of a job at slot offset off
+    size_t slot_bytes;
+    hipStream_t st = nullptr;
+    uint8_t *pin[SLOTS] = {}, *dev[SLOTS] = {};
+    hipEvent_t ev[SLOTS] = {};
+    int next = 0, threads = 1;
+    bool ok = false;
+
+    // `total`: the file bytes of all weight tensors; slots need not exceed it.
+    explicit WeightStager(size_t total) : slot_bytes(std::min(SLOT_MAX, std::max<size_t>(total, 4096))) {
+        if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) { st = nullptr; return; }
+        for (int i = 0; i < SLOTS; i++) {
+            if (hipHostMalloc(reinterpret_cast<void **>(&pin[i]), slot_bytes, hipHostMallocDefault) != hipSuccess) {
+                pin[i] = nullptr;
+                return;
+            }
+            if (hipMalloc(reinterpret_cast<void **>(&dev[i]), slot_bytes) != hipSuccess) { dev[i] = nullptr; return; }
+            if (hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess) { ev[i] = nullptr; return; }
+        }
+        threads = (int)std::min(8u, std::max(1u, std::thread::hardware_concurrency()));
+        ok = true;
+    }
+    ~WeightStager() {
+        if (st) (void)hipStreamSynchronize(st);
+        for (int i = 0; i < SLOTS; i++) {
+            if (ev[i]) (void)hipEventDestroy(ev[i]);
+            if (dev[i]) (void)hipFree(dev[i]);
+            if (pin[i]) (void)hipHostFree(pin[i]);
+        }
+        if (st) (void)hipStreamDestroy(st);
+    }
+
+    // Copy the slot's segments into pin[k], the bytes split evenly over the
+    // host threads (pieces of at least 1 MiB).
+    void fill(int k, const std::vector<UploadJob> &jobs, const std::vector<Seg> &segs, size_t used) {
+        auto copy_range = [&](size_t lo, size_t hi) {
+            for (const Seg &g : segs) {
+                const size_t len = g.n * jobs[g.job].frb;
+                const size_t a = std::max(lo, g.off), b = std::min(hi, g.off + len);
+                if (a < b) memcpy(pin[k] + a, jobs[g.job].src + g.r * jobs[g.job].frb + (a - g.off), b - a);
+            }
+        };
+        const int nt = (int)std::max<size_t>(1, std::min<size_t>(threads, used >> 20));
+        const size_t piece = (used + nt - 1) / nt;
+        std::vector<std::thread> ts;
+        for (int t = 1; t < nt; t++) ts.emplace_back(copy_range, t * piece, std::min(used, (t + 1) * piece));
+        copy_range(0, std::min(used, piece));
+        for (auto &t : ts) t.join();
+    }
+
+    bool flush(const std::vector<UploadJob> &jobs, std::vector<Seg> &segs, size_t used) {
+        if (segs.empty()) return true;
+        const int k = next;
+        next = (next + 1) % SLOTS;
+        HCHK(hipEventSynchronize(ev[k]), false);   // the DMA and repacks that last used the slot are done
+        fill(k, jobs, segs, used);
+        HCHK(hipMemcpyAsync(dev[k], pin[k], used, hipMemcpyHostToDevice, st), false);
+        for (const Seg &g : segs) {
+            const UploadJob &j = jobs[g.job];
+            if (j.dt == DT_F32) {
+                HCHK(hipMemcpyAsync(j.q + (j.row0 + g.r) * j.qrow, dev[k] + g.off, g.n * j.frb,
+                                    hipMemcpyDeviceToDevice, st), false);
+                continue;
+            }
+            const size_t nblk = g.n * (size_t)j.nb;
+            const int grid = (int)std::min<size_t>(4096, (nblk + 255) / 256);
+            k_repack_blocks<<<grid, 256, 0, st>>>(reinterpret_cast<const uint16_t *>(dev[k] + g.off), (int)g.n,
+                                                  j.nb, j.dt == DT_Q8 ? 17 : 9, j.q, j.qrow, j.d, j.row0 + g.r);
+            HCHK(hipGetLastError(), false);
+        }
+        HCHK(hipEventRecord(ev[k], st), false);
+        segs.clear();
+        return true;
+    }
+
+    // Stream every job through the slots, then wait for the last repack.
+    bool run(const std::vector<UploadJob> &jobs) {
+        std::vector<Seg> segs;
+        size_t used = 0;
+        for (size_t i = 0; i < jobs.size(); i++) {
+            const UploadJob &j = jobs[i];
+            if (j.frb > slot_bytes) { set_err("a weight row of %zu bytes exceeds the upload slot", j.frb); return false; }
+            for (size_t r = 0; r < (size_t)j.nrows;) {
+                const size_t fit = (slot_bytes - used) / j.frb;
+                if (fit == 0) {
+                    if (!flush(jobs, segs, used)) return false;
+                    used = 0;
+                    continue;
+                }
+                const size_t n = std::min(fit, (size_t)j.nrows - r);
+                segs.push_back({ i, r, n, used });
+                used = std::min(slot_bytes, (used + n * j.frb + 15) & ~(size_t)15);
+                r += n;
+            }
+        }
+        if (!flush(jobs, segs, used)) return false;
+        HCHK(hipStreamSynchronize(st), false);
+        return true;
+    }
+};
+
+}  // namespace
+
+// Allocate row-concatenated matrices (all of one dtype and width) in the
+// device layout described in dev_common.h and queue one upload job per file
+// tensor.
+static bool upload_mat(EhipModel *m, std::vector<UploadJob> &jobs, DMat *out, const EhipWeight *parts,
+                       const int *rows, int nparts, int cols, const char *what) {
     const int dt = parts[0].dtype;
     int R = 0;
     for (int i = 0; i < nparts; i++) {
@@ -102,35 +245,18 @@ static bool upload_mat(EhipModel *m, DMat *out, const EhipWeight *parts, const i
     const size_t qrow = dt == DT_F32 ? (size_t)cols * 4 : (dt == DT_Q8 ? (size_t)cols : (size_t)cols / 2);
     const size_t qbytes = qrow * R, dbytes = dt == DT_F32 ? 0 : (size_t)R * nb * 2;
     const size_t qpad = (qbytes + 255) & ~(size_t)255;
-    std::vector<uint8_t> host(qpad + dbytes);
-    uint8_t *hq = host.data();
-    uint16_t *hd = reinterpret_cast<uint16_t *>(host.data() + qpad);
+    uint8_t *dev = static_cast<uint8_t *>(dev_alloc(m, qpad + dbytes));
+    if (!dev) { set_err("hipMalloc of %zu bytes for %s failed", qpad + dbytes, what); return false; }
+    uint16_t *dsc = dt == DT_F32 ? nullptr : reinterpret_cast<uint16_t *>(dev + qpad);
+    const size_t frb = file_row_bytes(dt, cols);
     size_t r0 = 0;
     for (int p = 0; p < nparts; p++) {
-        const uint8_t *src = static_cast<const uint8_t *>(parts[p].data);
-        const size_t frb = file_row_bytes(dt, cols);
-        for (int r = 0; r < rows[p]; r++, r0++) {
-            const uint8_t *row = src + (size_t)r * frb;
-            if (dt == DT_F32) {
-                memcpy(hq + r0 * qrow, row, qrow);
-                continue;
-            }
-            const size_t bs = dt == DT_Q8 ? 34 : 18, pay = bs - 2;
-            for (int b = 0; b < nb; b++) {
-                const uint8_t *blk = row + (size_t)b * bs;
-                uint16_t d;
-                memcpy(&d, blk, 2);
-                hd[r0 * nb + b] = d;
-                memcpy(hq + r0 * qrow + (size_t)b * pay, blk + 2, pay);
-            }
-        }
+        jobs.push_back({ static_cast<const uint8_t *>(parts[p].data), rows[p], dt, nb, frb, qrow, r0, dev, dsc });
+        r0 += rows[p];
     }
-    uint8_t *dev = static_cast<uint8_t *>(dev_alloc(m, host.size()));
-    if (!dev) { set_err("hipMalloc of %zu bytes for %s failed", host.size(), what); return false; }
-    HCHK(hipMemcpy(dev, host.data(), host.size(), hipMemcpyHostToDevice), false);
     out->dtype = dt; out->rows = R; out->cols = cols;
     out->q = dev;
-    out->d = dt == DT_F32 ? nullptr : reinterpret_cast<const uint16_t *>(dev + qpad);
+    out->d = dsc;
     if (dt == DT_F32) m->any_f32 = true;
     return true;
 }
@@ -161,21 +287,10 @@ extern "C" void ehip_model_free(EhipModel *m) {
 
 extern "C" uint64_t ehip_model_bytes(const EhipModel *m) { return m ? m->bytes : 0; }
 
-extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *layers, EhipWeight tok_emb,
-                                        EhipWeight lm_head, const float *final_norm,
-                                        const float *rope_inv_freq) {
-    const EhipConfig &c = *cfg;
+static bool upload_weights(EhipModel *m, std::vector<UploadJob> &jobs, const EhipLayer *layers, EhipWeight tok_emb,
+                           EhipWeight lm_head, const float *final_norm) {
+    const EhipConfig &c = m->cfg;
     const int hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
-    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) { set_err("n_heads must be a multiple of n_kv_heads"); return nullptr; }
-    if (hd != 48 && hd != 64 && hd != 128) { set_err("head_dim %d not supported by the attention kernel", hd); return nullptr; }
-    if (c.n_heads / c.n_kv_heads > 8) { set_err("more than 8 query heads per kv head"); return nullptr; }
-    if (tok_emb.dtype != DT_F32 && tok_emb.dtype != DT_Q8) { set_err("embedding must be F32 or Q8_0"); return nullptr; }
-    EhipModel *m = new EhipModel();
-    m->cfg = c;
-    m->bytes = 0;
-    m->any_f32 = false;
-    int hiprc = hipSetDevice(0);
-    if (hiprc != hipSuccess) { set_err("hipSetDevice(0) failed: no usable GPU"); delete m; return nullptr; }
     m->layers.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; l++) {
         const EhipLayer &y = layers[l];
@@ -184,46 +299,67 @@ extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *
         snprintf(what, sizeof what, "layer %d qkv", l);
         EhipWeight qkv[3] = { y.wq, y.wk, y.wv };
         int qkv_rows[3] = { qd, kvd, kvd };
-        if (!upload_mat(m, &d.qkv, qkv, qkv_rows, 3, c.dim, what)) goto fail;
+        if (!upload_mat(m, jobs, &d.qkv, qkv, qkv_rows, 3, c.dim, what)) return false;
         snprintf(what, sizeof what, "layer %d wo", l);
-        if (!upload_mat(m, &d.wo, &y.wo, &c.dim, 1, qd, what)) goto fail;
-        {
-            EhipWeight w13[2] = { y.w1, y.w3 };
-            int rows13[2] = { c.hidden_dim, c.hidden_dim };
-            snprintf(what, sizeof what, "layer %d w1|w3", l);
-            if (!upload_mat(m, &d.w13, w13, rows13, 2, c.dim, what)) goto fail;
-        }
+        if (!upload_mat(m, jobs, &d.wo, &y.wo, &c.dim, 1, qd, what)) return false;
+        EhipWeight w13[2] = { y.w1, y.w3 };
+        int rows13[2] = { c.hidden_dim, c.hidden_dim };
+        snprintf(what, sizeof what, "layer %d w1|w3", l);
+        if (!upload_mat(m, jobs, &d.w13, w13, rows13, 2, c.dim, what)) return false;
         snprintf(what, sizeof what, "layer %d w2", l);
-        if (!upload_mat(m, &d.w2, &y.w2, &c.dim, 1, c.hidden_dim, what)) goto fail;
-        {
-            const float *an = y.attn_norm, *fn = y.ffn_norm;
-            if (!(d.attn_norm = upload_f32(m, &an, &c.dim, 1))) goto fail;
-            if (!(d.ffn_norm = upload_f32(m, &fn, &c.dim, 1))) goto fail;
-            d.q_norm = d.k_norm = nullptr;
-            if (c.qk_norm && y.q_norm) {
-                if (!y.k_norm) { set_err("layer %d has q_norm but no k_norm", l); goto fail; }
-                if (!(d.q_norm = upload_f32(m, &y.q_norm, &hd, 1))) goto fail;
-                if (!(d.k_norm = upload_f32(m, &y.k_norm, &hd, 1))) goto fail;
-            }
-            d.bias_qkv = nullptr;
-            if (y.bq || y.bk || y.bv) {
-                const float *bp[3] = { y.bq, y.bk, y.bv };
-                int bl[3] = { qd, kvd, kvd };
-                if (!(d.bias_qkv = upload_f32(m, bp, bl, 3))) goto fail;
-            }
+        if (!upload_mat(m, jobs, &d.w2, &y.w2, &c.dim, 1, c.hidden_dim, what)) return false;
+        const float *an = y.attn_norm, *fn = y.ffn_norm;
+        if (!(d.attn_norm = upload_f32(m, &an, &c.dim, 1))) return false;
+        if (!(d.ffn_norm = upload_f32(m, &fn, &c.dim, 1))) return false;
+        d.q_norm = d.k_norm = nullptr;
+        if (c.qk_norm && y.q_norm) {
+            if (!y.k_norm) { set_err("layer %d has q_norm but no k_norm", l); return false; }
+            if (!(d.q_norm = upload_f32(m, &y.q_norm, &hd, 1))) return false;
+            if (!(d.k_norm = upload_f32(m, &y.k_norm, &hd, 1))) return false;
+        }
+        d.bias_qkv = nullptr;
+        if (y.bq || y.bk || y.bv) {
+            const float *bp[3] = { y.bq, y.bk, y.bv };
+            int bl[3] = { qd, kvd, kvd };
+            if (!(d.bias_qkv = upload_f32(m, bp, bl, 3))) return false;
         }
     }
-    {
-        if (!upload_mat(m, &m->emb, &tok_emb, &c.vocab_size, 1, c.dim, "tok_embeddings")) goto fail;
-        if (lm_head.data == tok_emb.data) m->head = m->emb;
-        else if (!upload_mat(m, &m->head, &lm_head, &c.vocab_size, 1, c.dim, "lm_head")) goto fail;
-        if (!(m->final_norm = upload_f32(m, &final_norm, &c.dim, 1))) goto fail;
-        m->inv_freq.assign(rope_inv_freq, rope_inv_freq + hd / 2);
+    if (!upload_mat(m, jobs, &m->emb, &tok_emb, &c.vocab_size, 1, c.dim, "tok_embeddings")) return false;
+    if (lm_head.data == tok_emb.data) m->head = m->emb;
+    else if (!upload_mat(m, jobs, &m->head, &lm_head, &c.vocab_size, 1, c.dim, "lm_head")) return false;
+    if (!(m->final_norm = upload_f32(m, &final_norm, &c.dim, 1))) return false;
+    return true;
+}
+
+extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *layers, EhipWeight tok_emb,
+                                        EhipWeight lm_head, const float *final_norm,
+                                        const float *rope_inv_freq) {
+    const EhipConfig &c = *cfg;
+    const int hd = c.head_dim;
+    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) { set_err("n_heads must be a multiple of n_kv_heads"); return nullptr; }
+    if (hd != 48 && hd != 64 && hd != 128) { set_err("head_dim %d not supported by the attention kernel", hd); return nullptr; }
+    if (c.n_heads / c.n_kv_heads > 8) { set_err("more than 8 query heads per kv head"); return nullptr; }
+    if (tok_emb.dtype != DT_F32 && tok_emb.dtype != DT_Q8) { set_err("embedding must be F32 or Q8_0"); return nullptr; }
+    if (hipSetDevice(0) != hipSuccess) { set_err("hipSetDevice(0) failed: no usable GPU"); return nullptr; }
+    EhipModel *m = new EhipModel();
+    m->cfg = c;
+    m->bytes = 0;
+    m->any_f32 = false;
+    m->inv_freq.assign(rope_inv_freq, rope_inv_freq + hd / 2);
+    std::vector<UploadJob> jobs;
+    bool ok = upload_weights(m, jobs, layers, tok_emb, lm_head, final_norm);
+    if (ok) {
+        size_t total = 0;
+        for (const UploadJob &j : jobs) total += j.nrows * j.frb;
+        WeightStager up(total);   // its destructor waits for the upload stream
+        if (!up.ok) set_err("allocating the weight upload buffers failed");
+        ok = up.ok && up.run(jobs);
+    }
+    if (!ok) {
+        ehip_model_free(m);
+        return nullptr;
     }
     return m;
-fail:
-    ehip_model_free(m);
-    return nullptr;
 }
 
 // ---------------------------------------------------------------- state ----

@@ -168,6 +168,55 @@ def cpu_baseline(path, c, depth, budget_s):
                        f"({time.time() - t_start:.0f} s total) on '{cpu}', {ncpu} cores available")}
 
 
+def quantize_bench(model):
+    """ember_quantize_file (src/quant.c:59-125) on an fp32 file of `model`'s
+    shape: this library (blocks encoded on the GPU) against the reference's
+    requantizer compiled from its sources with its default flags
+    (oracle/_ref/libember_ref.so: -O3 -ffast-math, one CPU thread as in the
+    reference), each after one untimed run that warms the page cache; both
+    write their file to the same directory.  The output must equal, byte for
+    byte, the file written by the reference's deterministic build
+    (libember_ref_debug.so); its fast-math build rounds some blocks
+    differently."""
+    import filecmp
+    import tempfile
+    from emberllm_amd import _native, configs
+    if os.path.join(ROOT, "oracle") not in sys.path:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    lib, ref, ref_det = _native.lib(), oracle.reference_lib(debug=False), oracle.reference_lib(debug=True)
+    t0 = time.time()
+    f32 = configs.model_path(f"{model}_f32", dict(configs.ALL[model], dtype=_native.DT_F32), threads=16)
+    mb = os.path.getsize(f32) / 1e6
+    log(f"fp32 model {f32} ({mb:.0f} MB) ready in {time.time() - t0:.1f} s")
+    res = {}
+    with tempfile.TemporaryDirectory(dir=os.path.dirname(f32)) as tmp:
+        for name, target in (("q8_0", _native.DT_Q8_0), ("q4_0", _native.DT_Q4_0)):
+            out, ref_out = os.path.join(tmp, f"gpu_{name}.ember"), os.path.join(tmp, f"ref_{name}.ember")
+            times = {}
+            for who, fn, dst, reps in (("gpu", lib.ember_quantize_file, out, 3),
+                                       ("ref_cpu", ref.ember_quantize_file, ref_out, 1)):
+                assert fn(f32.encode(), dst.encode(), target) == 0, who
+                ts = []
+                for _ in range(reps):
+                    t = time.perf_counter()
+                    assert fn(f32.encode(), dst.encode(), target) == 0, who
+                    ts.append(time.perf_counter() - t)
+                times[who] = float(np.mean(ts))
+            det_out = os.path.join(tmp, f"det_{name}.ember")
+            assert ref_det.ember_quantize_file(f32.encode(), det_out.encode(), target) == 0
+            same = filecmp.cmp(out, det_out, shallow=False)
+            res[name] = {"gpu_s": round(times["gpu"], 4), "ref_cpu_s": round(times["ref_cpu"], 3),
+                         "speedup": round(times["ref_cpu"] / times["gpu"], 1),
+                         "identical_to_reference_deterministic_build": same,
+                         "out_MB": round(os.path.getsize(out) / 1e6, 1)}
+            for p in (out, ref_out, det_out):
+                os.remove(p)
+            log(f"quantize {name}: GPU {times['gpu']:.3f} s, reference CPU {times['ref_cpu']:.2f} s, "
+                f"file identical to the reference's deterministic build: {same}")
+    print(json.dumps({"quantize": res, "model": f"{model}-shape fp32 file", "input_MB": round(mb, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,6 +235,10 @@ def main():
                     help="only measure the streaming read bandwidth over buffers of 16 MiB to 4 GiB "
                          "(repeated passes over one buffer: what fits in the 256 MB Infinity Cache is "
                          "re-read from it) and print one JSON line")
+    ap.add_argument("--quantize", action="store_true",
+                    help="only time ember_quantize_file (blocks encoded on the GPU) on an fp32 file of "
+                         "--model's shape, to Q8_0 and Q4_0, beside the reference's CPU requantizer on the "
+                         "same file; check the outputs are identical and print one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 64 MiB device-to-device 8 times (a kernel of known traffic, for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -220,6 +273,9 @@ def main():
             log(f"read {mib} MiB x {reps}: {sweep[mib]:.0f} GB/s")
         eng.close()
         print(json.dumps({"read_sweep_GB_s_by_MiB": sweep, "passes": "about 8 GiB per size after one untimed pass"}))
+        return
+    if args.quantize:
+        quantize_bench(args.model)
         return
     c = configs.ALL[args.model]
     K, W, depth = args.steps, args.warmup, args.depth

@@ -78,6 +78,15 @@ class EmberSynthConfig(ctypes.Structure):
 assert ctypes.sizeof(EmberHeader) == 256 and ctypes.sizeof(EmberTensor) == 88
 
 _P = ctypes.c_void_p
+
+
+class EhipQuantJob(ctypes.Structure):
+    """ehip.h EhipQuantJob: rows x cols fp32 (host) -> Q8_0 / Q4_0 blocks (host)."""
+    _fields_ = [("src", ctypes.c_void_p), ("rows", ctypes.c_int64), ("cols", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("dst", ctypes.c_void_p)]
+
+
+assert ctypes.sizeof(EhipQuantJob) == 32
 _FP = ctypes.POINTER(ctypes.c_float)
 _IP = ctypes.POINTER(ctypes.c_int)
 
@@ -140,6 +149,7 @@ PROTOTYPES = {
     "ehip_measure_read_bw": (ctypes.c_int, [_P, ctypes.c_uint64, ctypes.c_int, _FP]),
     "ehip_sample_noalloc": (ctypes.c_int, [_P, ctypes.c_int, ctypes.POINTER(EmberSampler), _P, _P, _P, _P, _P]),
     "ehip_noalloc_setup": (ctypes.c_int, []),
+    "ehip_quantize_rows": (ctypes.c_int, [ctypes.POINTER(EhipQuantJob), ctypes.c_int]),
     # ember_synth.h
     "ember_synth_write": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(EmberSynthConfig)]),
     "ember_synth_fill_row": (None, [ctypes.c_uint64, ctypes.c_char_p, ctypes.c_int, ctypes.c_float,

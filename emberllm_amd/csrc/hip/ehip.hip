@@ -20,12 +20,12 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <thread>
 #include <vector>
 
 #include "../../../include/ember.h"
 #include "../../../include/ehip.h"
 #include "kernels.h"
+#include "staging.h"
 
 using namespace ehip;
 
@@ -143,7 +143,7 @@ struct WeightStager {
             if (hipMalloc(reinterpret_cast<void **>(&dev[i]), slot_bytes) != hipSuccess) { dev[i] = nullptr; return; }
             if (hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess) { ev[i] = nullptr; return; }
         }
-        threads = (int)std::min(8u, std::max(1u, std::thread::hardware_concurrency()));
+        threads = staging_threads();
         ok = true;
     }
     ~WeightStager() {
@@ -156,22 +156,12 @@ struct WeightStager {
         if (st) (void)hipStreamDestroy(st);
     }
 
-    // Copy the slot's segments into pin[k], the bytes split evenly over the
-    // host threads (pieces of at least 1 MiB).
-    void fill(int k, const std::vector<UploadJob> &jobs, const std::vector<Seg> &segs, size_t used) {
-        auto copy_range = [&](size_t lo, size_t hi) {
-            for (const Seg &g : segs) {
-                const size_t len = g.n * jobs[g.job].frb;
-                const size_t a = std::max(lo, g.off), b = std::min(hi, g.off + len);
-                if (a < b) memcpy(pin[k] + a, jobs[g.job].src + g.r * jobs[g.job].frb + (a - g.off), b - a);
-            }
-        };
-        const int nt = (int)std::max<size_t>(1, std::min<size_t>(threads, used >> 20));
-        const size_t piece = (used + nt - 1) / nt;
-        std::vector<std::thread> ts;
-        for (int t = 1; t < nt; t++) ts.emplace_back(copy_range, t * piece, std::min(used, (t + 1) * piece));
-        copy_range(0, std::min(used, piece));
-        for (auto &t : ts) t.join();
+    // Copy the slot's segments out of the mapped file into pin[k].
+    void fill(int k, const std::vector<UploadJob> &jobs, const std::vector<Seg> &segs) {
+        std::vector<CopySpan> spans;
+        for (const Seg &g : segs)
+            spans.push_back({ pin[k] + g.off, jobs[g.job].src + g.r * jobs[g.job].frb, g.n * jobs[g.job].frb });
+        parallel_copy(spans, threads);
     }
 
     bool flush(const std::vector<UploadJob> &jobs, std::vector<Seg> &segs, size_t used) {
@@ -179,7 +169,7 @@ struct WeightStager {
         const int k = next;
         next = (next + 1) % SLOTS;
         HCHK(hipEventSynchronize(ev[k]), false);   // the DMA and repacks that last used the slot are done
-        fill(k, jobs, segs, used);
+        fill(k, jobs, segs);
         HCHK(hipMemcpyAsync(dev[k], pin[k], used, hipMemcpyHostToDevice, st), false);
         for (const Seg &g : segs) {
             const UploadJob &j = jobs[g.job];

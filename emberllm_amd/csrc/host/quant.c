@@ -12,10 +12,14 @@
  * tensors stay F32, rows not divisible by 32 stay F32, already-quantized
  * tensors pass through, and in Q4_0 mode tok_embeddings / lm_head become
  * Q8_0.  Layout: tokenizer blob right after the header, table 8-aligned,
- * data region and every tensor 64-aligned (tools/convert.py:57-112).
+ * data region and every tensor 64-aligned (tools/convert.py:57-112).  The
+ * blocks of every tensor to be quantized are encoded on the GPU in one
+ * ehip_quantize_rows call (the same arithmetic as the row quantizers here);
+ * without a GPU the call fails with a message, as state creation does.
  */
 #define _DEFAULT_SOURCE
 #include "ember.h"
+#include "ehip.h"
 #include "util.h"
 
 #include <math.h>
@@ -102,10 +106,17 @@ int ember_quantize_file(const char *in_path, const char *out_path, int target) {
     const int n = h->n_tensors;
     EmberTensor *meta = ember_xcalloc((size_t)n, sizeof(EmberTensor), "quantize table");
     uint8_t **data = ember_xcalloc((size_t)n, sizeof(uint8_t *), "quantize data");
+    EhipQuantJob *jobs = ember_xcalloc((size_t)n, sizeof(EhipQuantJob), "quantize jobs");
+    int n_jobs = 0;
     for (int i = 0; i < n; i++) {
         const EmberTensor *t = &tab[i];
         const void *src = ember_model_data(m, t);
-        if (!src) { ember_model_free(m); return 1; }
+        if (!src) {
+            for (int k = 0; k < i; k++) free(data[k]);
+            free(data); free(meta); free(jobs);
+            ember_model_free(m);
+            return 1;
+        }
         meta[i] = *t;
         int want = target;
         if (target == EMBER_DT_Q4_0 &&
@@ -123,11 +134,24 @@ int ember_quantize_file(const char *in_path, const char *out_path, int target) {
         meta[i].dtype = want;
         meta[i].nbytes = rb * (size_t)rows;
         data[i] = ember_xmalloc(meta[i].nbytes, "quantized tensor");
-        for (int r = 0; r < rows; r++) {
-            const float *row = (const float *)src + (size_t)r * cols;
-            if (want == EMBER_DT_Q8_0) ember_quant_q8_row(row, data[i] + r * rb, cols);
-            else ember_quant_q4_row(row, data[i] + r * rb, cols);
+        jobs[n_jobs++] = (EhipQuantJob){ (const float *)src, rows, cols, want, data[i] };
+    }
+    int rc = 0;
+    if (n_jobs > 0) {
+        if (ehip_device_count() <= 0) {
+            fprintf(stderr, "ember: no GPU is visible to the HIP runtime\n");
+            rc = 1;
+        } else if (ehip_quantize_rows(jobs, n_jobs) != 0) {
+            fprintf(stderr, "ember: quantization failed: %s\n", ehip_last_error());
+            rc = 1;
         }
+    }
+    free(jobs);
+    if (rc) {
+        for (int i = 0; i < n; i++) free(data[i]);
+        free(data); free(meta);
+        ember_model_free(m);
+        return rc;
     }
     EmberHeader nh = *h;
     nh.tokenizer_offset = sizeof(EmberHeader);
@@ -141,7 +165,6 @@ int ember_quantize_file(const char *in_path, const char *out_path, int target) {
         cur += meta[i].nbytes;
     }
     FILE *f = fopen(out_path, "wb");
-    int rc = 0;
     if (!f) {
         fprintf(stderr, "ember: cannot write %s\n", out_path);
         rc = 1;

@@ -129,6 +129,26 @@ int ehip_sample_noalloc(float *logits, int n, const EmberSampler *params, uint64
  * state).  Returns 0 or nonzero. */
 int ehip_noalloc_setup(void);
 
+/* One tensor for the requantizer: `rows` x `cols` fp32 values (row-major,
+ * host memory, cols a multiple of 32) to be encoded as `dtype`
+ * (EMBER_DT_Q8_0: 34-byte blocks, EMBER_DT_Q4_0: 18-byte blocks) into
+ * rows*(cols/32) blocks at `dst` (host memory). */
+typedef struct {
+    const float *src;
+    int64_t rows;
+    int32_t cols, dtype;
+    void *dst;
+} EhipQuantJob;
+
+/* Block quantization of every job on the device, replacing the per-row
+ * quantizer loops of quantize_tensor (src/quant.c:26-57, with
+ * ember_quantize_q8_0 / ember_quantize_q4_0 of src/kernels.c:73-115) that
+ * ember_quantize_file runs.  The blocks equal the host quantizers'
+ * (ember_quant_q8_row / ember_quant_q4_row) byte for byte.  Synchronous:
+ * returns once every block is in its destination; 0, or nonzero with
+ * ehip_last_error() set (bad job, no GPU, failed copy). */
+int ehip_quantize_rows(const EhipQuantJob *jobs, int n_jobs);
+
 /* ---- inspection and measurement (tests and bench) ----------------------- */
 /* Copy the KV cache of the given layers to/from host memory in the cache's
  * own element type; which = 0 keys, 1 values; rows [0, n_pos). */

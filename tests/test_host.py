@@ -1,7 +1,7 @@
 """CPU tests of the product's host library (libember.so without a GPU):
 the exported ABI, the bit-exact quantizers and fp16 conversions, the
-sampler, the tokenizers, the loader's error handling, the requantizer and
-the synthetic model generator.
+sampler, the tokenizers, the loader's error handling, the requantizer's
+failure without a GPU and the synthetic model generator.
 """
 import ctypes
 import os
@@ -91,20 +91,20 @@ def test_quantizers_match_reference_golden():
         assert np.array_equal(q8, g["q8"][i]) and np.array_equal(q4, g["q4"][i]), i
 
 
-@pytest.mark.parametrize("target", [_native.DT_Q8_0, _native.DT_Q4_0])
-def test_quantize_file_equals_direct_quantized_synthesis(tmp_path, target):
-    """ember_quantize_file on the fp32 model reproduces, byte for byte, the
-    model the generator encodes directly (same file rules, quant.c:26-125)."""
-    base = dict(configs.TINY["t_qwen3"], dtype=_native.DT_F32)
-    f32 = configs.model_path("hq_f32", base)
-    direct = configs.model_path(f"hq_{target}", dict(base, dtype=target))
-    out = str(tmp_path / "q.ember")
-    assert L.ember_quantize_file(f32.encode(), out.encode(), target) == 0
-    assert open(out, "rb").read() == open(direct, "rb").read()
-    if HAVE_REF:
-        ref_out = str(tmp_path / "r.ember")
-        assert oracle.reference_lib().ember_quantize_file(f32.encode(), ref_out.encode(), target) == 0
-        assert open(out, "rb").read() == open(ref_out, "rb").read()
+def test_quantize_file_without_gpu_fails_loudly(tmp_path):
+    """ember_quantize_file encodes its blocks on the GPU (its parity with the
+    reference's requantizer is a GPU test); without one it reports an error
+    and writes nothing.  Nothing falls back to the CPU."""
+    if L.ehip_device_count() > 0:
+        pytest.skip("a GPU is visible")
+    f32 = configs.model_path("hq_f32", dict(configs.TINY["t_qwen3"], dtype=_native.DT_F32))
+    out = tmp_path / "q.ember"
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from emberllm_amd import _native\n"
+            "sys.exit(_native.lib().ember_quantize_file(%r, %r, 1))\n") % (ROOT, f32.encode(), str(out).encode())
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1 and "ember: no GPU" in r.stderr, (r.returncode, r.stderr)
+    assert not out.exists()
 
 
 # ---------------------------------------------------------------- sampler ---

@@ -5,7 +5,8 @@
 // (src/model.c:305-351).
 //
 // k_quant_rows: one workgroup per token row builds the Q8_0 activation codes
-// (optionally after the embedding lookup, an RMSNorm or the SwiGLU gate).
+// (optionally after the embedding lookup, an RMSNorm or the SwiGLU gate), one
+// lane per 32-element block.
 // k_gemm_mfma (Q8_0 / Q4_0 weights): int8 matrix cores, one
 // v_mfma_i32_32x32x32_i8 per 32-weight quant block, so each block's integer
 // dot product is exact and separately available; the fp32 epilogue of every
@@ -18,13 +19,21 @@
 
 namespace ehip {
 
+// The row is staged in LDS with each 32-element block padded to QP floats,
+// so that the quantizing lanes (one whole block each, in registers) read
+// their blocks with fewer bank conflicts.  Element i lives at xs[lds_at(i)].
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr int QP = 36;
+__device__ __forceinline__ int lds_at(int i) { return i + (i / QB) * (QP - QB); }
+
 __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     float *xs = reinterpret_cast<float *>(smem);
     __shared__ float red[NWAVE];
     const int K = a.cols, nb = K / QB, b = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // the row loops are unrolled so a thread's global loads are issued together
+    const int tid = threadIdx.x;
+    // the row loops are unrolled so a thread's global loads are issued together;
+    // thread tid sums the squares of elements tid, tid + WG, ... in that order
     float ss = 0.0f;
     if (a.ids) {
         const int tok = a.ids[b];
@@ -34,7 +43,7 @@ __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
             if (a.emb.dtype == DT_F32) v = reinterpret_cast<const float *>(a.emb.q)[(size_t)tok * K + i];
             else v = (float)reinterpret_cast<const int8_t *>(a.emb.q)[(size_t)tok * K + i] *
                      h2f(a.emb.d[(size_t)tok * nb + i / QB]);
-            xs[i] = v; ss += v * v;
+            xs[lds_at(i)] = v; ss += v * v;
             a.x_out[(size_t)b * K + i] = v;
         }
     } else if (a.swiglu) {
@@ -43,41 +52,65 @@ __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
         for (int i = tid; i < K; i += WG) {
             const float g = row[i];
             const float v = g / (1.0f + expf(-g)) * row[K + i];
-            xs[i] = v; ss += v * v;
+            xs[lds_at(i)] = v; ss += v * v;
         }
     } else {
         const float *row = a.x + (size_t)b * a.x_stride;
 #pragma unroll 4
-        for (int i = tid; i < K; i += WG) { const float v = row[i]; xs[i] = v; ss += v * v; }
+        for (int i = tid; i < K; i += WG) { const float v = row[i]; xs[lds_at(i)] = v; ss += v * v; }
     }
     if (a.norm_w) {
         const float tot = block_sum(ss, red);
         const float scale = 1.0f / sqrtf(tot / (float)K + a.eps);
 #pragma unroll 4
-        for (int i = tid; i < K; i += WG) xs[i] = xs[i] * scale * a.norm_w[i];
+        for (int i = tid; i < K; i += WG) xs[lds_at(i)] = xs[lds_at(i)] * scale * a.norm_w[i];
     }
     __syncthreads();
     if (a.xf)
-        for (int i = tid; i < K; i += WG) a.xf[(size_t)b * K + i] = xs[i];
+        for (int i = tid; i < K; i += WG) a.xf[(size_t)b * K + i] = xs[lds_at(i)];
     if (a.qx) {
-        for (int blk = wave * 2 + (lane >> 5); blk < nb; blk += NWAVE * 2) {
-            float dq;
-            const int q = quant_q8_lane(xs[blk * QB + (lane & 31)], &dq);
-            a.qx[(size_t)b * K + blk * QB + (lane & 31)] = (int8_t)q;
-            int s = q;
+        // one lane per block: the quant_q8_lane arithmetic (d = amax/127, the
+        // inverse of the unrounded d, round half away from zero, clamp) with
+        // the block in registers, so no lane exchanges are needed
+        for (int blk = tid; blk < nb; blk += WG) {
+            float v[QB];
+            const float4 *src = reinterpret_cast<const float4 *>(xs + blk * QP);
 #pragma unroll
-            for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off);
-            if ((lane & 31) == 0) {
-                a.dx[(size_t)b * nb + blk] = dq;
-                a.xs[(size_t)b * nb + blk] = s;
+            for (int i = 0; i < QB / 4; i++) {
+                const float4 t = src[i];
+                v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
             }
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < QB; i++) amax = fmaxf(amax, fabsf(v[i]));
+            const float d = amax / 127.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            int sum = 0;
+            uint32_t packed[QB / 4];
+#pragma unroll
+            for (int i = 0; i < QB / 4; i++) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int q = (int)fminf(fmaxf(roundf(v[4 * i + j] * id), -127.0f), 127.0f);
+                    sum += q;
+                    w |= ((uint32_t)q & 0xffu) << (8 * j);
+                }
+                packed[i] = w;
+            }
+            i32x4 *dst = reinterpret_cast<i32x4 *>(a.qx + (size_t)b * K + (size_t)blk * QB);
+            dst[0] = i32x4{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+            dst[1] = i32x4{(int)packed[4], (int)packed[5], (int)packed[6], (int)packed[7]};
+            a.dx[(size_t)b * nb + blk] = h2f(f2h(d));
+            a.xs[(size_t)b * nb + blk] = sum;
         }
     }
 }
 
 int launch_quant_rows(hipStream_t st, const QuantRowsArgs &a) {
-    if (a.cols % QB != 0 || (size_t)a.cols * 4 > 64 * 1024 || a.n <= 0) return -1;
-    hipLaunchKernelGGL(k_quant_rows, dim3(a.n), dim3(WG), (size_t)a.cols * 4, st, a);
+    const size_t lds = (size_t)(a.cols / QB) * QP * 4;
+    if (a.cols % QB != 0 || lds > 64 * 1024 || a.n <= 0) return -1;
+    hipLaunchKernelGGL(k_quant_rows, dim3(a.n), dim3(WG), lds, st, a);
     return 0;
 }
 
@@ -215,7 +248,6 @@ __global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
 // (i%4) + 4*(i/8); A fragments hold W[u][16h .. 16h+15] of one block, B
 // fragments X[t][16h .. 16h+15], h = lane / 32.
 constexpr int GM_U = 128;
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }

@@ -16,7 +16,8 @@ last bits of a running-sum boundary, as the reference's own optimized build
 of t_qwen3 at T 0.9, top-k 40, top-p 0.95; over 8 seeds the GPU build must
 reproduce the deterministic build's completions at least as often as the
 optimized build does, less one.  `ember bench` (src/main.c:230-294) must run
-on the GPU build.
+on the GPU build, and `ember quantize` (src/main.c:527-531) must write the
+same file as the reference program.
 """
 import json
 import os
@@ -94,6 +95,21 @@ def test_bench_runs_on_the_gpu_build():
     text = out.decode(errors="replace")
     say(text.strip().replace("\n", " | "))
     assert "prefill (pp32)" in text and "decode  (tg16)" in text, text
+
+
+@needs_clis
+@pytest.mark.parametrize("target", ["q8_0", "q4_0"])
+def test_quantize_command_writes_the_reference_programs_file(tmp_path, target):
+    """`ember quantize` (src/main.c:527-531): the GPU build's file equals the
+    one the reference program writes, byte for byte."""
+    f32 = configs.model_path("hq_f32_t_qwen3", dict(configs.TINY["t_qwen3"], dtype=0))
+    outs = []
+    for tag, cli in (("gpu", GPU_CLI), ("ref", REF_CLI)):
+        out = str(tmp_path / f"{tag}.ember")
+        run(cli, ["quantize", f32, out, target])
+        outs.append(open(out, "rb").read())
+    say(f"quantize {target}: {len(outs[0])} bytes")
+    assert outs[0] == outs[1]
 
 
 def _free_port():

@@ -39,19 +39,26 @@ template <int GM> struct PfRows { static constexpr int QW = GM >= 8 ? 1 : 8 / GM
 template <int HD, bool F16>
 __device__ __forceinline__ void stage_rows(float *dst, int pitch, const void *cache, int kv_dim, size_t hoff,
                                            int t0, int tmax, int tid) {
-    // PF_KT rows of hd elements of one kv head, widened to fp32, row t at dst + t * pitch
-    constexpr int F4 = HD / 4;
-    for (int f = tid; f < PF_KT * F4; f += WG) {
-        const int t = f / F4, c = (f % F4) * 4;
+    // PF_KT rows of hd elements of one kv head, widened to fp32, row t at dst + t * pitch;
+    // every load of the thread is issued before the first store
+    constexpr int F4 = HD / 4, N = PF_KT * F4 / WG;
+    static_assert(PF_KT * F4 % WG == 0, "whole float4 chunks per thread");
+    float4 v[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int f = tid + i * WG, t = f / F4, c = (f % F4) * 4;
         const size_t off = (size_t)min(t0 + t, tmax) * kv_dim + hoff + c;
-        float4 v;
         if (F16) {
             const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(cache) + off);
-            v = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
+            v[i] = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
         } else {
-            v = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(cache) + off);
+            v[i] = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(cache) + off);
         }
-        *reinterpret_cast<float4 *>(dst + t * pitch + c) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int f = tid + i * WG;
+        *reinterpret_cast<float4 *>(dst + (f / F4) * pitch + (f % F4) * 4) = v[i];
     }
 }
 
@@ -67,14 +74,26 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
     const int kt0 = blockIdx.x * PF_KT, b0 = blockIdx.y * QT;
     const int blast = min(a.n_tok, b0 + QT) - 1;
     if (b0 >= a.n_tok || kt0 > a.pos_base + blast) return;   // causal: no key of this tile is visible
+    // the Q rows' loads go out with the K tile's, then both are stored
+    constexpr int NQ = (QT * GM * (HD / 4) + WG - 1) / WG;
+    float4 qv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int f = tid + i * WG;
+        if (f < QT * GM * (HD / 4)) {
+            const int r = f / (HD / 4), c = (f % (HD / 4)) * 4;
+            const int qb = r / GM, h = r % GM;
+            const int b = min(b0 + qb, a.n_tok - 1);
+            qv[i] = *reinterpret_cast<const float4 *>(
+                a.q + (size_t)b * a.q_stride + (size_t)(g * G + min(h, G - 1)) * HD + c);
+        }
+    }
     stage_rows<HD, F16>(ks, KP, a.kc, a.kv_dim, (size_t)g * HD, kt0, a.pos_base + blast, tid);
-    for (int f = tid; f < QT * GM * (HD / 4); f += WG) {
-        const int r = f / (HD / 4), c = (f % (HD / 4)) * 4;
-        const int qb = r / GM, h = r % GM;
-        const int b = min(b0 + qb, a.n_tok - 1);
-        const float4 v = *reinterpret_cast<const float4 *>(
-            a.q + (size_t)b * a.q_stride + (size_t)(g * G + min(h, G - 1)) * HD + c);
-        *reinterpret_cast<float4 *>(&qs[r * HD + c]) = v;
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int f = tid + i * WG;
+        if (f < QT * GM * (HD / 4))
+            *reinterpret_cast<float4 *>(&qs[(f / (HD / 4)) * HD + (f % (HD / 4)) * 4]) = qv[i];
     }
     __syncthreads();
     float acc[QW][GM];
@@ -415,16 +434,6 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     }
 }
 
-// RMSNorm of one head vector held in LDS by one wave (model.c:50-55)
-template <int HD>
-__device__ __forceinline__ void head_norm(float *v, const float *w, float eps, int lane) {
-    float ss = 0.0f;
-    for (int d = lane; d < HD; d += 64) ss += v[d] * v[d];
-    ss = wave_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
-    for (int d = lane; d < HD; d += 64) v[d] = v[d] * scale * w[d];
-}
-
 // rotate pair i of one head vector (model.c:66-80) by the tabulated
 // (cos, sin) of pos * freq_i, computed on the host with the reference's
 // expression and libm
@@ -437,32 +446,69 @@ __device__ __forceinline__ void rope_pair(float *v, int i, int hd, float2 cs, in
 }
 
 // ---- prefill QK-norm + RoPE + KV store -----------------------------------
+// One wave per (token, head vector).  Every global load (the vector, its
+// norm weights, the RoPE table row, and for a key the value row) is issued at
+// the start, so the wave waits for memory once.
 template <int HD, bool F16>
 __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
+    constexpr int ND = (HD + 63) / 64, NP = (HD / 2 + 63) / 64;   // elements / pairs per lane
     __shared__ float v[HD];
     const int lane = threadIdx.x, b = blockIdx.x, vh = blockIdx.y;
     const int qd = a.n_heads * HD, pos = a.pos_base + b;
     const bool isq = vh < a.n_heads;
     const int g = vh - a.n_heads;
     float *row = a.qkv + (size_t)b * a.stride + (isq ? (size_t)vh * HD : (size_t)qd + (size_t)g * HD);
-    for (int d = lane; d < HD; d += 64) v[d] = row[d];
+    const float *vrow = a.qkv + (size_t)b * a.stride + qd + a.kv_dim + (size_t)max(g, 0) * HD;
+    const float *nw = isq ? a.q_norm : a.k_norm;
+    float x[ND], w[ND], vv[ND];
+    float2 cs[NP];
+#pragma unroll
+    for (int k = 0; k < ND; k++) {
+        const int d = lane + 64 * k;
+        if (d < HD) {
+            x[k] = row[d];
+            if (a.q_norm) w[k] = nw[d];
+            if (!isq) vv[k] = vrow[d];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int i = lane + 64 * k;
+        if (i < HD / 2) cs[k] = a.rope[(size_t)pos * (HD / 2) + i];
+    }
+    if (a.q_norm) {   // RMSNorm of the head vector (model.c:50-55): lane sums d = lane, lane + 64
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ND; k++)
+            if (lane + 64 * k < HD) ss += x[k] * x[k];
+        ss = wave_sum(ss);
+        const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+        for (int k = 0; k < ND; k++) x[k] = x[k] * scale * w[k];
+    }
+#pragma unroll
+    for (int k = 0; k < ND; k++)
+        if (lane + 64 * k < HD) v[lane + 64 * k] = x[k];
     __syncthreads();
-    if (a.q_norm) { head_norm<HD>(v, isq ? a.q_norm : a.k_norm, a.eps, lane); __syncthreads(); }
-    for (int i = lane; i < HD / 2; i += 64) rope_pair(v, i, HD, a.rope[(size_t)pos * (HD / 2) + i], a.rope_style);
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+        if (lane + 64 * k < HD / 2) rope_pair(v, lane + 64 * k, HD, cs[k], a.rope_style);
     __syncthreads();
     if (isq) {
         for (int d = lane; d < HD; d += 64) row[d] = v[d];
         return;
     }
-    const float *vrow = a.qkv + (size_t)b * a.stride + qd + a.kv_dim + (size_t)g * HD;
     const size_t off = (size_t)pos * a.kv_dim + (size_t)g * HD;
-    for (int d = lane; d < HD; d += 64) {
+#pragma unroll
+    for (int k = 0; k < ND; k++) {
+        const int d = lane + 64 * k;
+        if (d >= HD) continue;
         if (F16) {
             reinterpret_cast<uint16_t *>(a.kc)[off + d] = f2h(v[d]);
-            reinterpret_cast<uint16_t *>(a.vc)[off + d] = f2h(vrow[d]);
+            reinterpret_cast<uint16_t *>(a.vc)[off + d] = f2h(vv[k]);
         } else {
             reinterpret_cast<float *>(a.kc)[off + d] = v[d];
-            reinterpret_cast<float *>(a.vc)[off + d] = vrow[d];
+            reinterpret_cast<float *>(a.vc)[off + d] = vv[k];
         }
     }
 }
@@ -552,24 +598,36 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
     for (int kt = 0; kt < nkt; kt++) {
         const int k0 = kt * FL_BK;
         __syncthreads();   // the previous tile has been read
-        for (int f = tid; f < FL_BK * (HD / 4); f += WG) {
-            const int key = f / (HD / 4), c = (f % (HD / 4)) * 4;
-            const size_t off = (size_t)min(k0 + key, kend) * a.kv_dim + hoff + c;
-            float4 kv, vv;
-            if (F16) {
-                const uint2 ku = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
-                const uint2 vu = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
-                kv = make_float4(h2f(ku.x & 0xffff), h2f(ku.x >> 16), h2f(ku.y & 0xffff), h2f(ku.y >> 16));
-                vv = make_float4(h2f(vu.x & 0xffff), h2f(vu.x >> 16), h2f(vu.y & 0xffff), h2f(vu.y >> 16));
-            } else {
-                kv = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.kc) + off);
-                vv = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.vc) + off);
+        // SCH chunks of K and V per thread are loaded before any is stored,
+        // so the tile costs NST / SCH memory round trips rather than NST
+        constexpr int NST = FL_BK * (HD / 4) / WG, SCH = NST < 4 ? NST : 4;
+        static_assert(FL_BK * (HD / 4) % WG == 0 && NST % SCH == 0, "whole chunks per thread");
+#pragma unroll
+        for (int c0 = 0; c0 < NST; c0 += SCH) {
+            float4 kv[SCH], vv[SCH];
+#pragma unroll
+            for (int j = 0; j < SCH; j++) {
+                const int f = tid + (c0 + j) * WG, key = f / (HD / 4), c = (f % (HD / 4)) * 4;
+                const size_t off = (size_t)min(k0 + key, kend) * a.kv_dim + hoff + c;
+                if (F16) {
+                    const uint2 ku = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
+                    const uint2 vu = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
+                    kv[j] = make_float4(h2f(ku.x & 0xffff), h2f(ku.x >> 16), h2f(ku.y & 0xffff), h2f(ku.y >> 16));
+                    vv[j] = make_float4(h2f(vu.x & 0xffff), h2f(vu.x >> 16), h2f(vu.y & 0xffff), h2f(vu.y >> 16));
+                } else {
+                    kv[j] = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.kc) + off);
+                    vv[j] = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.vc) + off);
+                }
             }
-            *reinterpret_cast<float4 *>(&ks[key * KP + c]) = kv;
-            vt[(c + 0) * VP + key] = vv.x;
-            vt[(c + 1) * VP + key] = vv.y;
-            vt[(c + 2) * VP + key] = vv.z;
-            vt[(c + 3) * VP + key] = vv.w;
+#pragma unroll
+            for (int j = 0; j < SCH; j++) {
+                const int f = tid + (c0 + j) * WG, key = f / (HD / 4), c = (f % (HD / 4)) * 4;
+                *reinterpret_cast<float4 *>(&ks[key * KP + c]) = kv[j];
+                vt[(c + 0) * VP + key] = vv[j].x;
+                vt[(c + 1) * VP + key] = vv[j].y;
+                vt[(c + 2) * VP + key] = vv[j].z;
+                vt[(c + 3) * VP + key] = vv[j].w;
+            }
         }
         __syncthreads();
         // S^T: this lane gets S[row i][key 16kk + 4q + r]

@@ -137,6 +137,123 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
     }
 }
 
+// Passes whose keys fit in PF_SM_KEYS: the scores and the softmax of a row
+// in one kernel.  grid (token tiles of 4, kv groups); wave w carries token
+// b0 + w and the group's G heads (GM rows), lane = key of the tile.  Each
+// 64-key tile of K is staged in LDS and scored as in k_pf_scores (dims in
+// order, multiply and add rounded apart, then times 1/sqrt(hd)); a row's
+// scores stay in LDS.  Then per row: the maximum, the exponentials
+// expf(s - max) (positions past the row's length 0), their sum added in
+// position order by one lane per row (k_pf_rowsum's sequential sum: the
+// zeros leave it unchanged), and the probabilities e * (1/sum), which go to
+// the score rows for k_pf_pv2 to read instead of recomputing them.
+constexpr int PF_SM_KEYS = 512;
+template <int HD, int GM, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
+    constexpr int QT = 4, KP = HD + 4, NR = QT * GM, SP = PF_SM_KEYS + 4;
+    __shared__ __align__(16) float ks[PF_KT * KP];
+    __shared__ __align__(16) float qs[NR * HD];
+    __shared__ __align__(16) float ss[NR * SP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.n_heads / a.n_kv, g = blockIdx.y;
+    const int b0 = blockIdx.x * QT;
+    if (b0 >= a.n_tok) return;
+    const int kend = a.pos_base + min(a.n_tok, b0 + QT) - 1;   // the last key any row here sees
+    const int nkt = kend / PF_KT + 1;
+    const int b = b0 + wave;                                     // this wave's token (uniform)
+    const bool tok_ok = b < a.n_tok;
+    const int len = tok_ok ? a.pos_base + b + 1 : 0;             // keys visible to its rows
+    constexpr int NQ = (NR * (HD / 4) + WG - 1) / WG;
+    float4 qv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int f = tid + i * WG;
+        if (f < NR * (HD / 4)) {
+            const int r = f / (HD / 4), c = (f % (HD / 4)) * 4;
+            const int qb = min(b0 + r / GM, a.n_tok - 1), h = r % GM;
+            qv[i] = *reinterpret_cast<const float4 *>(
+                a.q + (size_t)qb * a.q_stride + (size_t)(g * G + min(h, G - 1)) * HD + c);
+        }
+    }
+    float mx[GM];
+#pragma unroll
+    for (int h = 0; h < GM; h++) mx[h] = -INFINITY;
+    float *srow = &ss[wave * GM * SP];
+    for (int kt = 0; kt < nkt; kt++) {
+        const int kt0 = kt * PF_KT;
+        if (kt > 0) __syncthreads();   // every wave has scored the previous tile
+        stage_rows<HD, F16>(ks, KP, a.kc, a.kv_dim, (size_t)g * HD, kt0, kend, tid);
+        if (kt == 0) {
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                const int f = tid + i * WG;
+                if (f < NR * (HD / 4))
+                    *reinterpret_cast<float4 *>(&qs[(f / (HD / 4)) * HD + (f % (HD / 4)) * 4]) = qv[i];
+            }
+        }
+        __syncthreads();
+        float acc[GM];
+#pragma unroll
+        for (int h = 0; h < GM; h++) acc[h] = 0.0f;
+        const float *kr = &ks[lane * KP];
+        const float *qw = &qs[wave * GM * HD];
+#pragma unroll(HD > 64 ? 1 : 4)
+        for (int d = 0; d < HD; d += 4) {
+            const float4 kf = *reinterpret_cast<const float4 *>(kr + d);
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                const float4 qf = *reinterpret_cast<const float4 *>(qw + h * HD + d);
+                float s = acc[h];               // dims in order, multiply and add rounded apart
+                s = s + qf.x * kf.x;
+                s = s + qf.y * kf.y;
+                s = s + qf.z * kf.z;
+                s = s + qf.w * kf.w;
+                acc[h] = s;
+            }
+        }
+        const int t = kt0 + lane;
+#pragma unroll
+        for (int h = 0; h < GM; h++) {
+            const float sv = acc[h] * a.inv_sqrt;
+            srow[h * SP + t] = sv;
+            if (t < len) mx[h] = fmaxf(mx[h], sv);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GM; h++) mx[h] = wave_max(mx[h]);
+    // exponentials of the wave's own rows (positions past the length: 0)
+    const int npos = nkt * PF_KT;
+#pragma unroll
+    for (int h = 0; h < GM; h++)
+        for (int t = lane; t < npos; t += 64) {
+            float *e = &srow[h * SP + t];
+            *e = t < len ? expf(*e - mx[h]) : 0.0f;
+        }
+    __syncthreads();
+    // lane h adds row h's exponentials in position order
+    float inv = 0.0f;
+    if (lane < GM && len > 0) {
+        const float *er = &srow[lane * SP];
+        float sum = 0.0f;
+        for (int t = 0; t < len; t += 4) {
+            const float4 e = *reinterpret_cast<const float4 *>(er + t);
+            sum = sum + e.x;
+            sum = sum + e.y;
+            sum = sum + e.z;
+            sum = sum + e.w;
+        }
+        inv = 1.0f / sum;
+    }
+    if (!tok_ok) return;
+#pragma unroll
+    for (int h = 0; h < GM; h++) {
+        const float ih = __shfl(inv, h);
+        if (h >= G) continue;
+        float *prow = a.scores + ((size_t)(g * G + h) * a.n_tok + b) * a.ldk;
+        for (int t = lane; t < len; t += 64) prow[t] = srow[h * SP + t] * ih;   // model.c:62-63
+    }
+}
+
 // grid (n_heads * n_tok / 64 rounded up), 64 rows per workgroup (rows of one
 // head, consecutive tokens, so their lengths differ by at most 63).  The four
 // waves compute the exponentials of a 64-position tile of all 64 rows into
@@ -320,14 +437,16 @@ __global__ __launch_bounds__(WG) void k_pf_pv(AttnArgs a) {
 // tile's global loads are issued before the current tile's products.  Every
 // (row, dim) sums its positions in order, multiply and add rounded apart;
 // positions past a row's length carry probability 0 (see k_pf_pv).
-template <int HD, int GM, bool F16, int DS>
+// PRE: the score rows already hold the probabilities (k_pf_softmax), which
+// are staged as they are.
+template <int HD, int GM, bool F16, int DS, bool PRE>
 __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     constexpr int HDS = HD / DS;                    // this workgroup's dims: blockIdx.z * HDS ..
     constexpr int RW = 64, QT = RW / GM, DG = HDS / 4, RSETS = WG / DG, RPS = RW / RSETS;
     constexpr int VLD = PF_KT * HDS / 4 / WG;       // V float4 loads per thread per tile
     constexpr int SLD = RW * PF_KT / 4 / WG;        // score float4 loads per thread per tile
     constexpr int PP = RW + 4;                      // ps row pitch
-    static_assert(RW % RSETS == 0 && RPS % 2 == 0 && WG % DG == 0 && VLD >= 1, "layout");
+    static_assert(RW % RSETS == 0 && (RPS == 1 || RPS % 2 == 0) && WG % DG == 0 && VLD >= 1, "layout");
     __shared__ __align__(16) float vs[PF_KT * HDS];
     __shared__ __align__(16) float ps[PF_KT * PP];
     const int tid = threadIdx.x, dg = tid % DG, rs = tid / DG;
@@ -346,7 +465,7 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
     const bool sok = sb < a.n_tok && sh < G;
     const size_t sgrow = sok ? (size_t)(g * G + sh) * a.n_tok + sb : 0;
     const int slen = sok ? a.pos_base + sb + 1 : 0;
-    const float smx = sok ? a.rowmax[sgrow] : 0.0f, sinv = sok ? a.rowinv[sgrow] : 0.0f;
+    const float smx = sok && !PRE ? a.rowmax[sgrow] : 0.0f, sinv = sok && !PRE ? a.rowinv[sgrow] : 0.0f;
     const float *srowp = a.scores + sgrow * a.ldk;
     const int last4 = a.ldk - 4;
 
@@ -379,10 +498,17 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
         for (int i = 0; i < SLD; i++) {   // p = e * (1/sum), model.c:62-63
             const int c4 = (tid + i * WG) / RW, t = t0 + 4 * c4;
             const f32x4 e = sr[i];
-            ps[(4 * c4 + 0) * PP + srow] = t < slen ? expf(e.x - smx) * sinv : 0.0f;
-            ps[(4 * c4 + 1) * PP + srow] = t + 1 < slen ? expf(e.y - smx) * sinv : 0.0f;
-            ps[(4 * c4 + 2) * PP + srow] = t + 2 < slen ? expf(e.z - smx) * sinv : 0.0f;
-            ps[(4 * c4 + 3) * PP + srow] = t + 3 < slen ? expf(e.w - smx) * sinv : 0.0f;
+            if (PRE) {
+                ps[(4 * c4 + 0) * PP + srow] = t < slen ? e.x : 0.0f;
+                ps[(4 * c4 + 1) * PP + srow] = t + 1 < slen ? e.y : 0.0f;
+                ps[(4 * c4 + 2) * PP + srow] = t + 2 < slen ? e.z : 0.0f;
+                ps[(4 * c4 + 3) * PP + srow] = t + 3 < slen ? e.w : 0.0f;
+            } else {
+                ps[(4 * c4 + 0) * PP + srow] = t < slen ? expf(e.x - smx) * sinv : 0.0f;
+                ps[(4 * c4 + 1) * PP + srow] = t + 1 < slen ? expf(e.y - smx) * sinv : 0.0f;
+                ps[(4 * c4 + 2) * PP + srow] = t + 2 < slen ? expf(e.z - smx) * sinv : 0.0f;
+                ps[(4 * c4 + 3) * PP + srow] = t + 3 < slen ? expf(e.w - smx) * sinv : 0.0f;
+            }
         }
     };
 
@@ -403,7 +529,9 @@ __global__ __launch_bounds__(WG) void k_pf_pv2(AttnArgs a) {
         for (int t = 0; t < PF_KT; t++) {
             const float4 v = *reinterpret_cast<const float4 *>(vp + t * HDS);
             float p[RPS];
-            if constexpr (RPS % 4 == 0) {
+            if constexpr (RPS == 1) {
+                p[0] = pp[t * PP];
+            } else if constexpr (RPS % 4 == 0) {
 #pragma unroll
                 for (int k = 0; k < RPS; k += 4) {
                     const float4 q = *reinterpret_cast<const float4 *>(pp + t * PP + k);
@@ -723,6 +851,17 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
     constexpr int QT = 4 * PfRows<GM>::QW;
     const int ktiles = (a.pos_base + a.n_tok + PF_KT - 1) / PF_KT;
     const int qtiles = (a.n_tok + QT - 1) / QT;
+    if constexpr (HD == 64 || HD == 128) {
+        if (a.pos_base + a.n_tok <= PF_SM_KEYS) {
+            // scores and softmax in one kernel, then P.V over the stored
+            // probabilities with the head dims split 16 per workgroup
+            hipLaunchKernelGGL((k_pf_softmax<HD, GM, F16>), dim3((a.n_tok + 3) / 4, a.n_kv), dim3(WG), 0, st, a);
+            constexpr int QT2 = 64 / GM, DSPLIT = HD / 16;
+            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, DSPLIT, true>), dim3((a.n_tok + QT2 - 1) / QT2, a.n_kv, DSPLIT),
+                               dim3(WG), 0, st, a);
+            return;
+        }
+    }
     // short prompts: one token row per wave for four times the workgroups
     if (PfRows<GM>::QW > 1 && (long)ktiles * qtiles * a.n_kv < 1024)
         hipLaunchKernelGGL((k_pf_scores<HD, GM, F16, 1>), dim3(ktiles, (a.n_tok + 3) / 4, a.n_kv), dim3(WG), 0, st, a);
@@ -736,9 +875,9 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
         constexpr int QT2 = 64 / GM, DSPLIT = HD / 32;
         const dim3 g2((a.n_tok + QT2 - 1) / QT2, a.n_kv);
         if ((long)g2.x * g2.y < 1024)   // measured: up to pp2048 for 8 kv heads
-            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, DSPLIT>), dim3(g2.x, g2.y, DSPLIT), dim3(WG), 0, st, a);
+            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, DSPLIT, false>), dim3(g2.x, g2.y, DSPLIT), dim3(WG), 0, st, a);
         else
-            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, 1>), g2, dim3(WG), 0, st, a);
+            hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, 1, false>), g2, dim3(WG), 0, st, a);
     } else {
         hipLaunchKernelGGL((k_pf_pv<HD, GM, F16>), dim3(qtiles, a.n_kv), dim3(WG), 0, st, a);
     }

@@ -147,8 +147,16 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
 // position order by one lane per row (k_pf_rowsum's sequential sum: the
 // zeros leave it unchanged), and the probabilities e * (1/sum), which go to
 // the score rows for k_pf_pv2 to read instead of recomputing them.
-constexpr int PF_SM_KEYS = 512;
-template <int HD, int GM, bool F16>
+//
+// FUSE: the workgroup then also multiplies its rows' probabilities into V
+// (each (row, four dims) summing its positions in order, multiply and add
+// rounded apart, as k_pf_pv2 does; V tiles staged in the LDS the K tiles
+// used), writes the output, and, with a.qx, the output's Q8_0 blocks: eight
+// lanes hold a block's 32 dims, so its maximum and code sum are 8-lane DPP
+// reductions, with k_quant_rows's arithmetic.
+constexpr int PF_SM_KEYS = 512;    // keys of a pass the one-kernel softmax takes (LDS rows)
+constexpr int PF_FUSE_KEYS = 256;  // keys of a pass up to which it also takes P.V
+template <int HD, int GM, bool F16, bool FUSE>
 __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
     constexpr int QT = 4, KP = HD + 4, NR = QT * GM, SP = PF_SM_KEYS + 4;
     __shared__ __align__(16) float ks[PF_KT * KP];
@@ -244,13 +252,92 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
         }
         inv = 1.0f / sum;
     }
-    if (!tok_ok) return;
+    if constexpr (!FUSE) {
+        if (!tok_ok) return;
 #pragma unroll
-    for (int h = 0; h < GM; h++) {
-        const float ih = __shfl(inv, h);
-        if (h >= G) continue;
-        float *prow = a.scores + ((size_t)(g * G + h) * a.n_tok + b) * a.ldk;
-        for (int t = lane; t < len; t += 64) prow[t] = srow[h * SP + t] * ih;   // model.c:62-63
+        for (int h = 0; h < GM; h++) {
+            const float ih = __shfl(inv, h);
+            if (h >= G) continue;
+            float *prow = a.scores + ((size_t)(g * G + h) * a.n_tok + b) * a.ldk;
+            for (int t = lane; t < len; t += 64) prow[t] = srow[h * SP + t] * ih;   // model.c:62-63
+        }
+    } else {
+        // probabilities in place: p = e * (1/sum), 0 past the row's length
+#pragma unroll
+        for (int h = 0; h < GM; h++) {
+            const float ih = __shfl(inv, h);
+            for (int t = lane; t < npos; t += 64) {
+                float *e = &srow[h * SP + t];
+                *e = t < len ? *e * ih : 0.0f;
+            }
+        }
+        // P.V: thread slot rq = tid + i * WG is (row rq / QPR, dims 4 (rq % QPR) ..)
+        constexpr int QPR = HD / 4, NRQ = (NR * QPR + WG - 1) / WG;
+        f32x4 acc[NRQ];
+#pragma unroll
+        for (int i = 0; i < NRQ; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kt = 0; kt < nkt; kt++) {
+            const int kt0 = kt * PF_KT;
+            __syncthreads();   // scores / probabilities written, the previous V tile read
+            stage_rows<HD, F16>(ks, KP, a.vc, a.kv_dim, (size_t)g * HD, kt0, kend, tid);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NRQ; i++) {
+                const int rq = tid + i * WG;
+                if (rq >= NR * QPR) break;
+                const float *pr = &ss[(rq / QPR) * SP + kt0];
+                const float *vp = &ks[(rq % QPR) * 4];
+                f32x4 o = acc[i];
+#pragma unroll 4
+                for (int t = 0; t < PF_KT; t++) {   // positions in order, multiply and add rounded apart
+                    const float pv = pr[t];
+                    const float4 v = *reinterpret_cast<const float4 *>(vp + t * KP);
+                    o.x = o.x + pv * v.x;
+                    o.y = o.y + pv * v.y;
+                    o.z = o.z + pv * v.z;
+                    o.w = o.w + pv * v.w;
+                }
+                acc[i] = o;
+            }
+        }
+        const int nbk = a.n_heads * HD / QB;   // Q8_0 blocks per token row
+#pragma unroll
+        for (int i = 0; i < NRQ; i++) {
+            const int rq = tid + i * WG;
+            if (rq >= NR * QPR) break;         // uniform per 8-lane group (NR * QPR is a multiple of 8)
+            const int r = rq / QPR, dq = rq % QPR, rb = b0 + r / GM, h = r % GM;
+            const bool ok = rb < a.n_tok && h < G;
+            const size_t col = (size_t)(g * G + min(h, G - 1)) * HD + 4 * dq;
+            const f32x4 o = acc[i];
+            if (ok) *reinterpret_cast<float4 *>(a.out + (size_t)rb * a.n_heads * HD + col) = make_float4(o.x, o.y, o.z, o.w);
+            if (a.qx) {
+                // the block of dims 32 (dq / 8) .. of this row: 8 consecutive lanes
+                float mx = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0xb1, 0xf, 0xf, false)));
+                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x4e, 0xf, 0xf, false)));
+                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x141, 0xf, 0xf, false)));
+                const float d = mx / 127.0f;
+                const float id = d > 0.0f ? 1.0f / d : 0.0f;
+                const int c0 = (int)fminf(fmaxf(roundf(o.x * id), -127.0f), 127.0f);
+                const int c1 = (int)fminf(fmaxf(roundf(o.y * id), -127.0f), 127.0f);
+                const int c2 = (int)fminf(fmaxf(roundf(o.z * id), -127.0f), 127.0f);
+                const int c3 = (int)fminf(fmaxf(roundf(o.w * id), -127.0f), 127.0f);
+                int cs = c0 + c1 + c2 + c3;
+                cs += __builtin_amdgcn_mov_dpp(cs, 0xb1, 0xf, 0xf, false);
+                cs += __builtin_amdgcn_mov_dpp(cs, 0x4e, 0xf, 0xf, false);
+                cs += __builtin_amdgcn_mov_dpp(cs, 0x141, 0xf, 0xf, false);
+                if (ok) {
+                    *reinterpret_cast<uint32_t *>(a.qx + (size_t)rb * a.n_heads * HD + col) =
+                        ((uint32_t)c0 & 0xffu) | (((uint32_t)c1 & 0xffu) << 8) |
+                        (((uint32_t)c2 & 0xffu) << 16) | (((uint32_t)c3 & 0xffu) << 24);
+                    if ((dq & 7) == 0) {
+                        const size_t blk = (size_t)rb * nbk + col / QB;
+                        a.qdx[blk] = h2f(f2h(d));
+                        a.qxs[blk] = cs;
+                    }
+                }
+            }
+        }
     }
 }
 
@@ -847,15 +934,21 @@ int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a) {
 
 // --------------------------------------------------------------------------
 template <int HD, int GM, bool F16>
-static void pf_go(hipStream_t st, const AttnArgs &a) {
+static void pf_go(hipStream_t st, const AttnArgs &a, bool *quantized) {
     constexpr int QT = 4 * PfRows<GM>::QW;
     const int ktiles = (a.pos_base + a.n_tok + PF_KT - 1) / PF_KT;
     const int qtiles = (a.n_tok + QT - 1) / QT;
     if constexpr (HD == 64 || HD == 128) {
+        if (a.pos_base + a.n_tok <= PF_FUSE_KEYS) {
+            // the whole attention in one kernel (and the output's quantization)
+            hipLaunchKernelGGL((k_pf_softmax<HD, GM, F16, true>), dim3((a.n_tok + 3) / 4, a.n_kv), dim3(WG), 0, st, a);
+            if (quantized) *quantized = a.qx != nullptr;
+            return;
+        }
         if (a.pos_base + a.n_tok <= PF_SM_KEYS) {
             // scores and softmax in one kernel, then P.V over the stored
             // probabilities with the head dims split 16 per workgroup
-            hipLaunchKernelGGL((k_pf_softmax<HD, GM, F16>), dim3((a.n_tok + 3) / 4, a.n_kv), dim3(WG), 0, st, a);
+            hipLaunchKernelGGL((k_pf_softmax<HD, GM, F16, false>), dim3((a.n_tok + 3) / 4, a.n_kv), dim3(WG), 0, st, a);
             constexpr int QT2 = 64 / GM, DSPLIT = HD / 16;
             hipLaunchKernelGGL((k_pf_pv2<HD, GM, F16, DSPLIT, true>), dim3((a.n_tok + QT2 - 1) / QT2, a.n_kv, DSPLIT),
                                dim3(WG), 0, st, a);
@@ -884,24 +977,26 @@ static void pf_go(hipStream_t st, const AttnArgs &a) {
 }
 
 template <int HD, bool F16>
-static int pf_pick_g(hipStream_t st, const AttnArgs &a) {
+static int pf_pick_g(hipStream_t st, const AttnArgs &a, bool *quantized) {
     const int G = a.n_heads / a.n_kv;
-    if (G <= 1) pf_go<HD, 1, F16>(st, a);
-    else if (G <= 2) pf_go<HD, 2, F16>(st, a);
-    else if (G <= 4) pf_go<HD, 4, F16>(st, a);
-    else if (G <= 8) pf_go<HD, 8, F16>(st, a);
+    if (G <= 1) pf_go<HD, 1, F16>(st, a, quantized);
+    else if (G <= 2) pf_go<HD, 2, F16>(st, a, quantized);
+    else if (G <= 4) pf_go<HD, 4, F16>(st, a, quantized);
+    else if (G <= 8) pf_go<HD, 8, F16>(st, a, quantized);
     else return -1;
     return 0;
 }
 
-int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a) {
+int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized) {
+    if (quantized) *quantized = false;
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || !a.scores || !a.tmax || !a.rowmax || !a.rowinv)
         return -1;
     if (a.ldk < a.pos_base + a.n_tok || a.ldk % 4) return -1;
+    if (a.qx && (!a.qdx || !a.qxs || (a.n_heads * a.hd) % QB)) return -1;
     switch (a.hd) {
-        case 48: return f16kv ? pf_pick_g<48, true>(st, a) : pf_pick_g<48, false>(st, a);
-        case 64: return f16kv ? pf_pick_g<64, true>(st, a) : pf_pick_g<64, false>(st, a);
-        case 128: return f16kv ? pf_pick_g<128, true>(st, a) : pf_pick_g<128, false>(st, a);
+        case 48: return f16kv ? pf_pick_g<48, true>(st, a, quantized) : pf_pick_g<48, false>(st, a, quantized);
+        case 64: return f16kv ? pf_pick_g<64, true>(st, a, quantized) : pf_pick_g<64, false>(st, a, quantized);
+        case 128: return f16kv ? pf_pick_g<128, true>(st, a, quantized) : pf_pick_g<128, false>(st, a, quantized);
     }
     return -1;
 }

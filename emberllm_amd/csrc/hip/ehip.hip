@@ -1070,12 +1070,18 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
             at.ldk = attn_prefill_ldk(pos0, mt);
             const bool exact = s->pf_mode == PF_EXACT || (s->pf_mode == PF_AUTO && pos0 + mt <= PF_EXACT_KEYS);
-            rc |= exact ? launch_attention(s->st, s->f16kv, at) : launch_attention_mfma(s->st, s->f16kv, at);
+            // the short-pass attention can quantize its own output for wo
+            // (not for F32 weights, whose product reads the fp32 rows)
+            bool quantized = false;
+            if (!q.xf) { at.qx = s->qx; at.qdx = s->dxp; at.qxs = s->xsum; }
+            rc |= exact ? launch_attention(s->st, s->f16kv, at, &quantized) : launch_attention_mfma(s->st, s->f16kv, at);
             if (psnap(DBG_O, s->O, qd, qd)) return -1;
-            QuantRowsArgs q2{};
-            q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;
-            q2.xf = q.xf; q2.qx = s->qx; q2.dx = s->dxp; q2.xs = s->xsum;
-            rc |= launch_quant_rows(s->st, q2);
+            if (!quantized) {
+                QuantRowsArgs q2{};
+                q2.x = s->O; q2.x_stride = qd; q2.cols = qd; q2.n = mt;
+                q2.xf = q.xf; q2.qx = s->qx; q2.dx = s->dxp; q2.xs = s->xsum;
+                rc |= launch_quant_rows(s->st, q2);
+            }
             GemmArgs g2{};
             g2.W = y.wo; g2.units = c.dim; g2.n = mt; g2.qx = s->qx; g2.dx = s->dxp; g2.xs = s->xsum;
             g2.xf = q.xf; g2.out = s->X; g2.out_stride = c.dim;

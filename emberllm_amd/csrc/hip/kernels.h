@@ -81,9 +81,14 @@ struct AttnArgs {
     // 1/sum of the exponentials [n_heads][n_tok]
     float *scores, *tmax, *rowmax, *rowinv;
     int ldk;
+    // prefill, optional: the output's Q8_0 codes, fp16-rounded block scales
+    // and code sums ([n_tok][n_heads*hd / 32]), as the quantization kernel
+    // would make them from `out`; written when the launch reports it
+    int8_t *qx; float *qdx; int *qxs;
 };
-// prefill: q rows already normed and rotated, k/v already in the cache
-int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a);
+// prefill: q rows already normed and rotated, k/v already in the cache.
+// *quantized (if non-null) says whether the launch also wrote a.qx/qdx/qxs.
+int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized = nullptr);
 // prefill on fp32 matrix cores with a running softmax (no score scratch)
 int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a);
 inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }

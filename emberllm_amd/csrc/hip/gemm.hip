@@ -416,7 +416,10 @@ constexpr int GS_U = 32, GS_T = 32, GS_KB = 4;
 // the blocks, and adds their sums in pipeline order at the end.  The waves'
 // serial walk over K (each block's product feeds the next block's sum) is
 // then a SPLIT-th as long, and SPLIT times as many waves share each SIMD.
-template <int DT, int EPI, int SPLIT>
+// FULL: every pipeline's block range is a whole number of stages (nb a
+// multiple of 4 * SPLIT), so no load needs clamping and no stage is partial:
+// the loads walk precomputed pointers and the epilogue has no tail test.
+template <int DT, int EPI, int SPLIT, bool FULL>
 __global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
     constexpr int P = SPLIT > 1 ? 4 : 8;                       // register ring depth (stages)
     constexpr int WB = DT == DT_Q8 ? 32 : 16;                 // weight bytes per row and block
@@ -449,7 +452,26 @@ __global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
     uint16_t dwr[P];
     float dxr[P];
     int xsr[P];
+    // FULL: this thread's first-stage addresses; stage st adds st * GS_KB blocks
+    const int wrow = tid / (WROW / 16), wc = (tid % (WROW / 16)) * 16;
+    const int xrow = tid / (XROW / 16), xc = (tid % (XROW / 16)) * 16;
+    const int skb = tid / GS_U, sr = tid % GS_U;
+    const uint8_t *wp0 = a.W.q + (size_t)min(u0 + wrow, a.units - 1) * (nb * WB) + (size_t)kb0 * WB + wc;
+    const int8_t *xp0 = a.qx + (size_t)min(t0 + xrow, a.n - 1) * K + (size_t)kb0 * 32 + xc;
+    const uint16_t *dwp0 = a.W.d + (size_t)min(u0 + sr, a.units - 1) * nb + kb0 + skb;
+    const float *dxp0 = a.dx + (size_t)min(t0 + sr, a.n - 1) * nb + kb0 + skb;
+    const int *xsp0 = a.xs + (size_t)min(t0 + sr, a.n - 1) * nb + kb0 + skb;
     auto load = [&](int j, int st) {
+        if constexpr (FULL) {
+            if (tid < WCH) wr[j] = *reinterpret_cast<const i32x4 *>(wp0 + (size_t)st * GS_KB * WB);
+            xr[j] = *reinterpret_cast<const i32x4 *>(xp0 + (size_t)st * GS_KB * 32);
+            if (tid < NSC) {
+                dwr[j] = dwp0[st * GS_KB];
+                dxr[j] = dxp0[st * GS_KB];
+                if (DT == DT_Q4) xsr[j] = xsp0[st * GS_KB];
+            }
+            return;
+        }
         const int b0 = kb0 + st * GS_KB;
         if (tid < WCH) {
             const int row = tid / (WROW / 16), c = (tid % (WROW / 16)) * 16;
@@ -497,7 +519,7 @@ __global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
             // the stage's fragments and scales first, then its products, then
             // the epilogues in block order (blocks past the pipeline's end
             // contribute nothing)
-            const int nkb = min(GS_KB, kb1 - (kb0 + st * GS_KB));
+            const int nkb = FULL ? GS_KB : min(GS_KB, kb1 - (kb0 + st * GS_KB));
             long af[GS_KB], bf[GS_KB];
             float dx[GS_KB];
             f32x4 dw[GS_KB];
@@ -572,21 +594,21 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         const long g64 = (long)gu * ((a.n + 63) / 64);
         if (g64 < 256 || (a.units <= 1024 && g64 < 1024)) {
             const dim3 gs((a.units + GS_U - 1) / GS_U, (a.n + GS_T - 1) / GS_T);
-            const bool split = a.W.cols / QB >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT_MAX_GRID;
-#define GSF(DT)                                                                                          \
-            if (split) {                                                                                 \
-                if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, GS_SPLIT>), gs, dim3(WG * GS_SPLIT), 0, st, a); \
-                else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, GS_SPLIT>), gs, dim3(WG * GS_SPLIT), 0, st, a); \
-                else return -1;                                                                          \
-                return 0;                                                                                \
-            }                                                                                            \
-            if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, 1>), gs, dim3(WG), 0, st, a); \
-            else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, 1>), gs, dim3(WG), 0, st, a); \
+            const int nb = a.W.cols / QB;
+            const bool split = nb >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT_MAX_GRID;
+            const bool full = nb % (GS_KB * (split ? GS_SPLIT : 1)) == 0;
+#define GSL(DT, SP, FL)                                                                                  \
+            if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, SP, FL>), gs, dim3(WG * SP), 0, st, a); \
+            else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, SP, FL>), gs, dim3(WG * SP), 0, st, a); \
             else return -1;                                                                              \
             return 0;
+#define GSF(DT)                                                                                          \
+            if (split) { if (full) { GSL(DT, GS_SPLIT, true) } else { GSL(DT, GS_SPLIT, false) } }      \
+            if (full) { GSL(DT, 1, true) } else { GSL(DT, 1, false) }
             if (a.W.dtype == DT_Q8) { GSF(DT_Q8) }
             GSF(DT_Q4)
 #undef GSF
+#undef GSL
         }
         const bool t64 = (long)gu * ((a.n + 127) / 128) < 256;
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);

@@ -36,30 +36,43 @@ constexpr int PF_KT = 64;   // keys per tile
 // rows of (token, head) per lane or thread: tokens x heads <= 8
 template <int GM> struct PfRows { static constexpr int QW = GM >= 8 ? 1 : 8 / GM; };
 
+// One tile of PF_KT cache rows (hd elements of one kv head, widened to fp32)
+// held in registers between its loads and its LDS stores, so the loads of the
+// next tile can be in flight while the current one is used.
+template <int HD, bool F16> struct RowTile {
+    static constexpr int F4 = HD / 4, N = PF_KT * F4 / WG;
+    static_assert(PF_KT * F4 % WG == 0, "whole float4 chunks per thread");
+    f32x4 v[N];   // native vectors (HIP's float4 struct kept this array in scratch)
+    __device__ __forceinline__ void load(const void *cache, int kv_dim, size_t hoff, int t0, int tmax, int tid) {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const int f = tid + i * WG, t = f / F4, c = (f % F4) * 4;
+            const size_t off = (size_t)min(t0 + t, tmax) * kv_dim + hoff + c;
+            if (F16) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(cache) + off);
+                v[i] = f32x4{h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16)};
+            } else {
+                v[i] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(cache) + off);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float *dst, int pitch, int tid) const {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const int f = tid + i * WG;
+            *reinterpret_cast<f32x4 *>(dst + (f / F4) * pitch + (f % F4) * 4) = v[i];
+        }
+    }
+};
+
 template <int HD, bool F16>
 __device__ __forceinline__ void stage_rows(float *dst, int pitch, const void *cache, int kv_dim, size_t hoff,
                                            int t0, int tmax, int tid) {
     // PF_KT rows of hd elements of one kv head, widened to fp32, row t at dst + t * pitch;
     // every load of the thread is issued before the first store
-    constexpr int F4 = HD / 4, N = PF_KT * F4 / WG;
-    static_assert(PF_KT * F4 % WG == 0, "whole float4 chunks per thread");
-    float4 v[N];
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        const int f = tid + i * WG, t = f / F4, c = (f % F4) * 4;
-        const size_t off = (size_t)min(t0 + t, tmax) * kv_dim + hoff + c;
-        if (F16) {
-            const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(cache) + off);
-            v[i] = make_float4(h2f(u.x & 0xffff), h2f(u.x >> 16), h2f(u.y & 0xffff), h2f(u.y >> 16));
-        } else {
-            v[i] = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(cache) + off);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        const int f = tid + i * WG;
-        *reinterpret_cast<float4 *>(dst + (f / F4) * pitch + (f % F4) * 4) = v[i];
-    }
+    RowTile<HD, F16> r;
+    r.load(cache, kv_dim, hoff, t0, tmax, tid);
+    r.store(dst, pitch, tid);
 }
 
 // grid (key tiles, token tiles of 4*QW, kv groups); wave w carries tokens
@@ -76,7 +89,7 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
     if (b0 >= a.n_tok || kt0 > a.pos_base + blast) return;   // causal: no key of this tile is visible
     // the Q rows' loads go out with the K tile's, then both are stored
     constexpr int NQ = (QT * GM * (HD / 4) + WG - 1) / WG;
-    float4 qv[NQ];
+    f32x4 qv[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; i++) {
         const int f = tid + i * WG;
@@ -84,7 +97,7 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
             const int r = f / (HD / 4), c = (f % (HD / 4)) * 4;
             const int qb = r / GM, h = r % GM;
             const int b = min(b0 + qb, a.n_tok - 1);
-            qv[i] = *reinterpret_cast<const float4 *>(
+            qv[i] = *reinterpret_cast<const f32x4 *>(
                 a.q + (size_t)b * a.q_stride + (size_t)(g * G + min(h, G - 1)) * HD + c);
         }
     }
@@ -93,7 +106,7 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
     for (int i = 0; i < NQ; i++) {
         const int f = tid + i * WG;
         if (f < QT * GM * (HD / 4))
-            *reinterpret_cast<float4 *>(&qs[(f / (HD / 4)) * HD + (f % (HD / 4)) * 4]) = qv[i];
+            *reinterpret_cast<f32x4 *>(&qs[(f / (HD / 4)) * HD + (f % (HD / 4)) * 4]) = qv[i];
     }
     __syncthreads();
     float acc[QW][GM];
@@ -172,14 +185,14 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
     const bool tok_ok = b < a.n_tok;
     const int len = tok_ok ? a.pos_base + b + 1 : 0;             // keys visible to its rows
     constexpr int NQ = (NR * (HD / 4) + WG - 1) / WG;
-    float4 qv[NQ];
+    f32x4 qv[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; i++) {
         const int f = tid + i * WG;
         if (f < NR * (HD / 4)) {
             const int r = f / (HD / 4), c = (f % (HD / 4)) * 4;
             const int qb = min(b0 + r / GM, a.n_tok - 1), h = r % GM;
-            qv[i] = *reinterpret_cast<const float4 *>(
+            qv[i] = *reinterpret_cast<const f32x4 *>(
                 a.q + (size_t)qb * a.q_stride + (size_t)(g * G + min(h, G - 1)) * HD + c);
         }
     }
@@ -187,16 +200,22 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < GM; h++) mx[h] = -INFINITY;
     float *srow = &ss[wave * GM * SP];
+    // the next tile's rows are loaded into registers while the current one is
+    // scored: K tiles, then (FUSE) the first V tile during the softmax
+    RowTile<HD, F16> nxt;
+    nxt.load(a.kc, a.kv_dim, (size_t)g * HD, 0, kend, tid);
     for (int kt = 0; kt < nkt; kt++) {
         const int kt0 = kt * PF_KT;
         if (kt > 0) __syncthreads();   // every wave has scored the previous tile
-        stage_rows<HD, F16>(ks, KP, a.kc, a.kv_dim, (size_t)g * HD, kt0, kend, tid);
+        nxt.store(ks, KP, tid);
+        if (kt + 1 < nkt) nxt.load(a.kc, a.kv_dim, (size_t)g * HD, kt0 + PF_KT, kend, tid);
+        else if (FUSE) nxt.load(a.vc, a.kv_dim, (size_t)g * HD, 0, kend, tid);
         if (kt == 0) {
 #pragma unroll
             for (int i = 0; i < NQ; i++) {
                 const int f = tid + i * WG;
                 if (f < NR * (HD / 4))
-                    *reinterpret_cast<float4 *>(&qs[(f / (HD / 4)) * HD + (f % (HD / 4)) * 4]) = qv[i];
+                    *reinterpret_cast<f32x4 *>(&qs[(f / (HD / 4)) * HD + (f % (HD / 4)) * 4]) = qv[i];
             }
         }
         __syncthreads();
@@ -279,7 +298,8 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
         for (int kt = 0; kt < nkt; kt++) {
             const int kt0 = kt * PF_KT;
             __syncthreads();   // scores / probabilities written, the previous V tile read
-            stage_rows<HD, F16>(ks, KP, a.vc, a.kv_dim, (size_t)g * HD, kt0, kend, tid);
+            nxt.store(ks, KP, tid);
+            if (kt + 1 < nkt) nxt.load(a.vc, a.kv_dim, (size_t)g * HD, kt0 + PF_KT, kend, tid);
             __syncthreads();
 #pragma unroll
             for (int i = 0; i < NRQ; i++) {

@@ -5,8 +5,8 @@
 // (src/model.c:305-351).
 //
 // k_quant_rows: one workgroup per token row builds the Q8_0 activation codes
-// (optionally after the embedding lookup, an RMSNorm or the SwiGLU gate), one
-// lane per 32-element block.
+// (optionally after the embedding lookup, an RMSNorm or the SwiGLU gate),
+// eight lanes per 32-element block.
 // k_gemm_mfma (Q8_0 / Q4_0 weights): int8 matrix cores, one
 // v_mfma_i32_32x32x32_i8 per 32-weight quant block, so each block's integer
 // dot product is exact and separately available; the fp32 epilogue of every
@@ -20,8 +20,8 @@
 namespace ehip {
 
 // The row is staged in LDS with each 32-element block padded to QP floats,
-// so that the quantizing lanes (one whole block each, in registers) read
-// their blocks with fewer bank conflicts.  Element i lives at xs[lds_at(i)].
+// so that the quantizing lanes' 16-byte reads of consecutive blocks spread
+// over the banks.  Element i lives at xs[lds_at(i)].
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int QP = 36;
 __device__ __forceinline__ int lds_at(int i) { return i + (i / QB) * (QP - QB); }
@@ -69,40 +69,34 @@ __global__ __launch_bounds__(WG) void k_quant_rows(QuantRowsArgs a) {
     if (a.xf)
         for (int i = tid; i < K; i += WG) a.xf[(size_t)b * K + i] = xs[lds_at(i)];
     if (a.qx) {
-        // one lane per block: the quant_q8_lane arithmetic (d = amax/127, the
-        // inverse of the unrounded d, round half away from zero, clamp) with
-        // the block in registers, so no lane exchanges are needed
-        for (int blk = tid; blk < nb; blk += WG) {
-            float v[QB];
-            const float4 *src = reinterpret_cast<const float4 *>(xs + blk * QP);
-#pragma unroll
-            for (int i = 0; i < QB / 4; i++) {
-                const float4 t = src[i];
-                v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-            }
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < QB; i++) amax = fmaxf(amax, fabsf(v[i]));
-            const float d = amax / 127.0f;
+        // eight lanes per block, four elements each: the quant_q8_lane
+        // arithmetic (d = amax/127, the inverse of the unrounded d, round half
+        // away from zero, clamp), the block's maximum and code sum as 8-lane
+        // DPP reductions
+        const int part = tid & 7;
+        for (int blk = tid >> 3; blk < nb; blk += WG / 8) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(xs + blk * QP + 4 * part);
+            float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0xb1, 0xf, 0xf, false)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x4e, 0xf, 0xf, false)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x141, 0xf, 0xf, false)));
+            const float d = mx / 127.0f;
             const float id = d > 0.0f ? 1.0f / d : 0.0f;
-            int sum = 0;
-            uint32_t packed[QB / 4];
-#pragma unroll
-            for (int i = 0; i < QB / 4; i++) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int q = (int)fminf(fmaxf(roundf(v[4 * i + j] * id), -127.0f), 127.0f);
-                    sum += q;
-                    w |= ((uint32_t)q & 0xffu) << (8 * j);
-                }
-                packed[i] = w;
+            const int c0 = (int)fminf(fmaxf(roundf(v.x * id), -127.0f), 127.0f);
+            const int c1 = (int)fminf(fmaxf(roundf(v.y * id), -127.0f), 127.0f);
+            const int c2 = (int)fminf(fmaxf(roundf(v.z * id), -127.0f), 127.0f);
+            const int c3 = (int)fminf(fmaxf(roundf(v.w * id), -127.0f), 127.0f);
+            int sum = c0 + c1 + c2 + c3;
+            sum += __builtin_amdgcn_mov_dpp(sum, 0xb1, 0xf, 0xf, false);
+            sum += __builtin_amdgcn_mov_dpp(sum, 0x4e, 0xf, 0xf, false);
+            sum += __builtin_amdgcn_mov_dpp(sum, 0x141, 0xf, 0xf, false);
+            *reinterpret_cast<uint32_t *>(a.qx + (size_t)b * K + (size_t)blk * QB + 4 * part) =
+                ((uint32_t)c0 & 0xffu) | (((uint32_t)c1 & 0xffu) << 8) | (((uint32_t)c2 & 0xffu) << 16) |
+                (((uint32_t)c3 & 0xffu) << 24);
+            if (part == 0) {
+                a.dx[(size_t)b * nb + blk] = h2f(f2h(d));
+                a.xs[(size_t)b * nb + blk] = sum;
             }
-            i32x4 *dst = reinterpret_cast<i32x4 *>(a.qx + (size_t)b * K + (size_t)blk * QB);
-            dst[0] = i32x4{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
-            dst[1] = i32x4{(int)packed[4], (int)packed[5], (int)packed[6], (int)packed[7]};
-            a.dx[(size_t)b * nb + blk] = h2f(f2h(d));
-            a.xs[(size_t)b * nb + blk] = sum;
         }
     }
 }

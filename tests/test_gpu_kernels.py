@@ -5,8 +5,8 @@ Every decode kernel (q|k|v matvec with its RMSNorm prologue, QK-norm / RoPE
 w2 + residual, final norm + lm_head) and every prefill kernel (row
 quantization, the int8 MFMA GEMMs in both tile sizes and the short-prompt
 GEMM, QK post-processing, the prefill attention in both forms: the
-exact-order kernels up to 512 keys and the fp32 matrix-core kernel beyond,
-or forced at pp512) is captured on the GPU and
+exact-order kernels up to 512 keys (one kernel up to 256) and the fp32
+matrix-core kernel beyond, or forced at pp512) is captured on the GPU and
 recomputed in float64 from the model file on the GPU's own inputs
 (tests/kernel_check.py, itself pinned against the oracle on the CPU by
 tests/test_kernel_check.py).  Bound: 1e-6 of the sum of |terms| for
@@ -15,7 +15,8 @@ whose rounding an ulp decides.
 
 Workloads (the benchmark configurations): stories110M @128, SmolLM2 @1024,
 Qwen2.5-0.5B @256, Qwen3-0.6B Q8_0 @4096 (both decode-attention schedules),
-Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings; and a
+Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings and of
+128 / 256 / 200 tokens on the Qwen3 / Qwen2.5 / SmolLM2 shapes; and a
 2-layer Qwen3-width model prefilling 2,300 tokens (one 2048-token pass with
 128-token MFMA tiles, then a 252-token pass at position 2048), also compared
 end to end with the oracle (logits, at the reference builds' own noise floor
@@ -130,6 +131,18 @@ def test_prefill_kernels_512(name):
     """pp512 at the Qwen3-0.6B shape: q|k|v and w1|w3 on the 64-token-tile
     MFMA GEMM, wo and w2 on the 32x32-tile GEMM, Q8_0 and Q4_0 weights."""
     ok, text = _prefill_kernels(name, 512, [(0, 0), (27, 0)])
+    assert ok, text
+
+
+@pytest.mark.parametrize("name,n", [("qwen3_06b", 128), ("qwen25_05b", 256), ("smollm2_135m", 200)],
+                         ids=["qwen3_06b-128", "qwen25_05b-256", "smollm2_135m-200"])
+def test_prefill_kernels_short(name, n):
+    """Short prompts: the one-kernel exact-order attention (scores, softmax,
+    P.V and the wo input's Q8_0 blocks; 2, 7 and 3 query heads per kv head,
+    head_dim 128 and 64) and the 32x32-tile GEMM with and without whole
+    stages and the K split."""
+    last = configs.ALL[name]["n_layers"] - 1
+    ok, text = _prefill_kernels(name, n, [(0, 0), (last, 0)])
     assert ok, text
 
 

@@ -681,35 +681,42 @@ __device__ __forceinline__ void rope_pair(float *v, int i, int hd, float2 cs, in
 }
 
 // ---- prefill QK-norm + RoPE + KV store -----------------------------------
-// One wave per (token, head vector).  Every global load (the vector, its
-// norm weights, the RoPE table row, and for a key the value row) is issued at
-// the start, so the wave waits for memory once.
+// One wave per (token, head vector), QKP_W head vectors of a token per
+// workgroup (fewer, fuller workgroups to dispatch).  Every global load (the
+// vector, its norm weights, the RoPE table row, and for a key the value row)
+// is issued at the start, so the wave waits for memory once.
+constexpr int QKP_W = 4;
 template <int HD, bool F16>
-__global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
+__global__ __launch_bounds__(64 * QKP_W) void k_qkpost(QkPostArgs a) {
     constexpr int ND = (HD + 63) / 64, NP = (HD / 2 + 63) / 64;   // elements / pairs per lane
-    __shared__ float v[HD];
-    const int lane = threadIdx.x, b = blockIdx.x, vh = blockIdx.y;
+    __shared__ float vsh[QKP_W][HD];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, b = blockIdx.x;
+    const int vh = blockIdx.y * QKP_W + w;
+    // (waves past the last head vector have nothing to do; every wave still
+    // reaches the barriers)
+    const bool live = vh < a.n_heads + a.n_kv;
+    float *v = vsh[w];
     const int qd = a.n_heads * HD, pos = a.pos_base + b;
     const bool isq = vh < a.n_heads;
     const int g = vh - a.n_heads;
     float *row = a.qkv + (size_t)b * a.stride + (isq ? (size_t)vh * HD : (size_t)qd + (size_t)g * HD);
     const float *vrow = a.qkv + (size_t)b * a.stride + qd + a.kv_dim + (size_t)max(g, 0) * HD;
     const float *nw = isq ? a.q_norm : a.k_norm;
-    float x[ND], w[ND], vv[ND];
+    float x[ND], nwv[ND], vv[ND];
     float2 cs[NP];
 #pragma unroll
     for (int k = 0; k < ND; k++) {
         const int d = lane + 64 * k;
-        if (d < HD) {
+        if (live && d < HD) {
             x[k] = row[d];
-            if (a.q_norm) w[k] = nw[d];
+            if (a.q_norm) nwv[k] = nw[d];
             if (!isq) vv[k] = vrow[d];
         }
     }
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int i = lane + 64 * k;
-        if (i < HD / 2) cs[k] = a.rope[(size_t)pos * (HD / 2) + i];
+        if (live && i < HD / 2) cs[k] = a.rope[(size_t)pos * (HD / 2) + i];
     }
     if (a.q_norm) {   // RMSNorm of the head vector (model.c:50-55): lane sums d = lane, lane + 64
         float ss = 0.0f;
@@ -719,7 +726,7 @@ __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
         ss = wave_sum(ss);
         const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
 #pragma unroll
-        for (int k = 0; k < ND; k++) x[k] = x[k] * scale * w[k];
+        for (int k = 0; k < ND; k++) x[k] = x[k] * scale * nwv[k];
     }
 #pragma unroll
     for (int k = 0; k < ND; k++)
@@ -729,6 +736,7 @@ __global__ __launch_bounds__(64) void k_qkpost(QkPostArgs a) {
     for (int k = 0; k < NP; k++)
         if (lane + 64 * k < HD / 2) rope_pair(v, lane + 64 * k, HD, cs[k], a.rope_style);
     __syncthreads();
+    if (!live) return;
     if (isq) {
         for (int d = lane; d < HD; d += 64) row[d] = v[d];
         return;
@@ -1022,12 +1030,12 @@ int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quanti
 }
 
 int launch_qkpost(hipStream_t st, bool f16kv, const QkPostArgs &a) {
-    dim3 grid(a.n_tok, a.n_heads + a.n_kv);
+    dim3 grid(a.n_tok, (a.n_heads + a.n_kv + QKP_W - 1) / QKP_W);
     switch (a.hd) {
 #define QKP(H)                                                                              \
     case H:                                                                                 \
-        if (f16kv) hipLaunchKernelGGL((k_qkpost<H, true>), grid, dim3(64), 0, st, a);       \
-        else hipLaunchKernelGGL((k_qkpost<H, false>), grid, dim3(64), 0, st, a);            \
+        if (f16kv) hipLaunchKernelGGL((k_qkpost<H, true>), grid, dim3(64 * QKP_W), 0, st, a); \
+        else hipLaunchKernelGGL((k_qkpost<H, false>), grid, dim3(64 * QKP_W), 0, st, a);    \
         return 0;
         QKP(48) QKP(64) QKP(128)
 #undef QKP

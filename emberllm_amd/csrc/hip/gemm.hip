@@ -576,6 +576,10 @@ __global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
 // keeps 256-thread workgroups (two rounds of split workgroups measured
 // slower: q|k|v 12.7 against 11.1 us, w1|w3 17.8 against 13.2 at 128 tokens)
 constexpr int GS_SPLIT = 4, GS_SPLIT_MIN_BLOCKS = 32, GS_SPLIT_MAX_GRID = 256;
+// Grids of up to GS_SPLIT2_MAX_GRID workgroups split K in two (512-thread
+// workgroups, two or three per CU): half the serial walk per output for two
+// pipelines' instructions per SIMD.
+constexpr int GS_SPLIT2_MAX_GRID = 1024;
 
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
@@ -590,7 +594,8 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
             const dim3 gs((a.units + GS_U - 1) / GS_U, (a.n + GS_T - 1) / GS_T);
             const int nb = a.W.cols / QB;
             const bool split = nb >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT_MAX_GRID;
-            const bool full = nb % (GS_KB * (split ? GS_SPLIT : 1)) == 0;
+            const bool split2 = !split && nb >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT2_MAX_GRID;
+            const bool full = nb % (GS_KB * (split ? GS_SPLIT : split2 ? 2 : 1)) == 0;
 #define GSL(DT, SP, FL)                                                                                  \
             if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, SP, FL>), gs, dim3(WG * SP), 0, st, a); \
             else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, SP, FL>), gs, dim3(WG * SP), 0, st, a); \
@@ -598,6 +603,7 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
             return 0;
 #define GSF(DT)                                                                                          \
             if (split) { if (full) { GSL(DT, GS_SPLIT, true) } else { GSL(DT, GS_SPLIT, false) } }      \
+            if (split2) { if (full) { GSL(DT, 2, true) } else { GSL(DT, 2, false) } }                    \
             if (full) { GSL(DT, 1, true) } else { GSL(DT, 1, false) }
             if (a.W.dtype == DT_Q8) { GSF(DT_Q8) }
             GSF(DT_Q4)

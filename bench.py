@@ -231,6 +231,9 @@ def main():
     ap.add_argument("--sampled-only", action="store_true",
                     help="profiling aid: fill the cache to --depth, run only the device sampling loop "
                          "(T 0.8, top-k 40, top-p 0.9) and print its rate; no JSON line")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="profiling aid: only prefill --depth tokens (1 untimed and --steps timed runs) "
+                         "and print the rate; no JSON line")
     ap.add_argument("--read-sweep", action="store_true",
                     help="only measure the streaming read bandwidth over buffers of 16 MiB to 4 GiB "
                          "(repeated passes over one buffer: what fits in the 256 MB Infinity Cache is "
@@ -293,6 +296,16 @@ def main():
     rng = np.random.default_rng(4096)
     V = c["vocab_size"]
     out = {"load_s": load_s}
+    if args.prefill_only:
+        ids = rng.integers(0, V, depth).astype(np.int32)
+        eng.prefill(ids)
+        t = time.perf_counter()
+        for _ in range(K):
+            eng.prefill(ids)
+        dt = (time.perf_counter() - t) / K
+        log(f"prefill pp{depth}: {dt * 1e3:.3f} ms, {depth / dt:.1f} tok/s (mean of {K})")
+        eng.close()
+        return
 
     # ---- prefill --------------------------------------------------------
     def prefill_rate(n, reps=5, warm=1):

@@ -224,7 +224,7 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
         for (int h = 0; h < GM; h++) acc[h] = 0.0f;
         const float *kr = &ks[lane * KP];
         const float *qw = &qs[wave * GM * HD];
-#pragma unroll(HD > 64 ? 1 : 4)
+#pragma unroll 4   // 16 dims per step: their LDS reads are in flight together
         for (int d = 0; d < HD; d += 4) {
             const float4 kf = *reinterpret_cast<const float4 *>(kr + d);
 #pragma unroll
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
                 const float *pr = &ss[(rq / QPR) * SP + kt0];
                 const float *vp = &ks[(rq % QPR) * 4];
                 f32x4 o = acc[i];
-#pragma unroll 4
+#pragma unroll 8
                 for (int t = 0; t < PF_KT; t++) {   // positions in order, multiply and add rounded apart
                     const float pv = pr[t];
                     const float4 v = *reinterpret_cast<const float4 *>(vp + t * KP);

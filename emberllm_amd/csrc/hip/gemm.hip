@@ -403,147 +403,209 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 // row), B[8 (l / 16) .. +7][l % 16] (of a token row), and outputs
 // D[4 (l / 16) + r][l % 16], r = 0..3.  The epilogue is the same
 // sum += ((float)isum * dw) * dx in block order.
-constexpr int GS_U = 32, GS_T = 32, GS_KB = 4;
+constexpr int GS_T = 32, GS_KB = 4;
 
-// SPLIT > 1 (K of at least 1024): the workgroup runs SPLIT of the 4-wave
-// pipelines above side by side, pipeline q over the q-th contiguous part of
-// the blocks, and adds their sums in pipeline order at the end.  The waves'
+// SPLIT > 1 (K of at least 1024): the workgroup runs SPLIT of the pipelines
+// above side by side, pipeline q over the q-th contiguous part of the
+// blocks, and adds their sums in pipeline order at the end.  The waves'
 // serial walk over K (each block's product feeds the next block's sum) is
 // then a SPLIT-th as long, and SPLIT times as many waves share each SIMD.
 // FULL: every pipeline's block range is a whole number of stages (nb a
 // multiple of 4 * SPLIT), so no load needs clamping and no stage is partial:
 // the loads walk precomputed pointers and the epilogue has no tail test.
-template <int DT, int EPI, int SPLIT, bool FULL>
-__global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
-    constexpr int P = SPLIT > 1 ? 4 : 8;                       // register ring depth (stages)
+// U: units per workgroup, 32 (four waves per pipeline, 2 x 2 tiles) or 16
+// (two waves, the tokens' two tiles): 16-unit tiles give the narrow products
+// twice the workgroups, so they spread over every CU instead of doubling the
+// waves, LDS traffic and epilogues of half of them.
+// Register ring depth (stages) of a pipeline.
+__host__ __device__ constexpr int gs_ring(int split, int u) { return split > 1 && u == 32 ? 4 : 8; }
+// ONE: the pipeline's stages fit the ring (nst <= gs_ring), so all of them
+// are loaded at the start and the stages run as straight-line code; a loop
+// header would merge the ring's states and make the compiler wait for every
+// load there, and the two forms in one kernel cost both their registers.
+// Two-pipeline 32-unit workgroups run two or three per CU: at most 128
+// VGPRs (four waves per SIMD).
+template <int DT, int EPI, int SPLIT, bool FULL, int U, bool ONE>
+__global__ __launch_bounds__(64 * (U / 16) * (GS_T / 16) * SPLIT, SPLIT == 2 && U == 32 ? 4 : 1)
+void k_gemm_small(GemmArgs a) {
+    constexpr int NWP = (U / 16) * (GS_T / 16), NTP = 64 * NWP;   // waves, threads per pipeline
+    constexpr int P = gs_ring(SPLIT, U);
     constexpr int WB = DT == DT_Q8 ? 32 : 16;                 // weight bytes per row and block
     constexpr int WROW = GS_KB * WB, XROW = GS_KB * 32;        // stage bytes per row
     constexpr int WP = WROW + 16, XP = XROW + 16;              // LDS row pitches
-    constexpr int WCH = GS_U * WROW / 16, XCH = GS_T * XROW / 16;   // 16-byte chunks per stage
-    constexpr int NSC = GS_KB * GS_U;                          // scales of each kind per stage
-    static_assert(GS_U == GS_T && WCH <= WG && XCH == WG && NSC <= WG, "one chunk per thread and stage");
-    __shared__ __align__(16) uint8_t ws[SPLIT][2][GS_U * WP];
+    constexpr int WCH = U * WROW / 16, XCH = GS_T * XROW / 16; // 16-byte chunks per stage
+    constexpr int XPT = XCH / NTP;                             // X chunks per thread and stage
+    constexpr int NSW = GS_KB * U, NSX = GS_KB * GS_T;         // weight / token scales per stage
+    static_assert(WCH <= NTP && XCH % NTP == 0 && NSW <= NTP && NSX <= NTP, "chunks and scales per thread");
+    __shared__ __align__(16) uint8_t ws[SPLIT][2][U * WP];
     __shared__ __align__(16) int8_t xsm[SPLIT][2][GS_T * XP];
-    __shared__ __align__(16) float dws[SPLIT][2][GS_KB][GS_U], dxs[SPLIT][2][GS_KB][GS_T];
+    __shared__ __align__(16) float dws[SPLIT][2][GS_KB][U], dxs[SPLIT][2][GS_KB][GS_T];
     __shared__ int sxs[SPLIT][2][GS_KB][GS_T];
-    __shared__ __align__(16) float red[SPLIT > 1 ? SPLIT - 1 : 1][NWAVE][64][4];
-    const int tid = threadIdx.x % WG, q = threadIdx.x / WG;    // thread of pipeline q
+    __shared__ __align__(16) float red[SPLIT > 1 ? SPLIT - 1 : 1][NWP][64][4];
+    const int tid = threadIdx.x % NTP, q = threadIdx.x / NTP;   // thread of pipeline q
     const int lane = tid & 63, wave = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;
-    const int u0 = blockIdx.x * GS_U, t0 = blockIdx.y * GS_T;
+    const int u0 = blockIdx.x * U, t0 = blockIdx.y * GS_T;
     const int K = a.W.cols, nb = K / QB;
     const int nbq = (nb + SPLIT - 1) / SPLIT, kb0 = q * nbq, kb1 = min(nb, kb0 + nbq);   // this pipeline's blocks
     const int nst = (nbq + GS_KB - 1) / GS_KB;                // stages, the same in every pipeline
-    const int wu = (wave & 1) * 16, wt = (wave >> 1) * 16;
-    uint8_t (&wsq)[2][GS_U * WP] = ws[q];
+    const int wu = U == 32 ? (wave & 1) * 16 : 0, wt = U == 32 ? (wave >> 1) * 16 : wave * 16;
+    uint8_t (&wsq)[2][U * WP] = ws[q];
     int8_t (&xsq)[2][GS_T * XP] = xsm[q];
-    float (&dwq)[2][GS_KB][GS_U] = dws[q];
+    float (&dwq)[2][GS_KB][U] = dws[q];
     float (&dxq)[2][GS_KB][GS_T] = dxs[q];
     int (&sxq)[2][GS_KB][GS_T] = sxs[q];
 
+    // the epilogue's residual (or bias) values: their loads go out first, so
+    // the stores at the end do not wait for a round trip (not in the
+    // two-pipeline 32-unit kernel, whose registers are spoken for)
+    constexpr bool PRE = !(SPLIT == 2 && U == 32);
+    const int to = t0 + wt + fr;
+    float pre[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (PRE)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int u = min(u0 + wu + 4 * fg + r, a.units - 1);
+            if (EPI == EPI_RESID) pre[r] = a.out[(size_t)min(to, a.n - 1) * a.out_stride + u];
+            else pre[r] = a.bias ? a.bias[u] : 0.0f;
+        }
+
     // register ring: slot j holds a stage s with s % P == j
-    i32x4 wr[P], xr[P];
+    i32x4 wr[P], xr[P][XPT];
     uint16_t dwr[P];
     float dxr[P];
     int xsr[P];
     // FULL: this thread's first-stage addresses; stage st adds st * GS_KB blocks
-    const int wrow = tid / (WROW / 16), wc = (tid % (WROW / 16)) * 16;
-    const int xrow = tid / (XROW / 16), xc = (tid % (XROW / 16)) * 16;
-    const int skb = tid / GS_U, sr = tid % GS_U;
-    const uint8_t *wp0 = a.W.q + (size_t)min(u0 + wrow, a.units - 1) * (nb * WB) + (size_t)kb0 * WB + wc;
-    const int8_t *xp0 = a.qx + (size_t)min(t0 + xrow, a.n - 1) * K + (size_t)kb0 * 32 + xc;
-    const uint16_t *dwp0 = a.W.d + (size_t)min(u0 + sr, a.units - 1) * nb + kb0 + skb;
-    const float *dxp0 = a.dx + (size_t)min(t0 + sr, a.n - 1) * nb + kb0 + skb;
-    const int *xsp0 = a.xs + (size_t)min(t0 + sr, a.n - 1) * nb + kb0 + skb;
+    // ONE: threads past the last W chunk or scale repeat the last one (the
+    // same value to the same LDS word), so neither a load nor a store is
+    // conditional: the compiler would otherwise move a load next to its
+    // conditional store and wait for it there.  The looped form (whose header
+    // waits for every load anyway) skips them.
+    const bool ldw = ONE || tid < WCH, lsw = ONE || tid < NSW, lsx = ONE || tid < NSX;
+    const int wch = min(tid, WCH - 1);
+    const int wrow = wch / (WROW / 16), wc = (wch % (WROW / 16)) * 16;
+    const int skw = min(tid, NSW - 1) / U, srw = min(tid, NSW - 1) % U;
+    const int skx = min(tid, NSX - 1) / GS_T, srx = min(tid, NSX - 1) % GS_T;
+    // (the pipeline's base is uniform; the thread's part is a 32-bit offset,
+    // one register instead of a 64-bit address per stream)
+    const uint32_t wo0 = (uint32_t)(min(u0 + wrow, a.units - 1) * (nb * WB) + wc);
+    uint32_t xo0[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int c = tid + i * NTP, xrow = c / (XROW / 16), xc = (c % (XROW / 16)) * 16;
+        xo0[i] = (uint32_t)(min(t0 + xrow, a.n - 1) * K + xc);
+    }
+    const uint32_t dwo0 = (uint32_t)(min(u0 + srw, a.units - 1) * nb + skw);
+    const uint32_t dxo0 = (uint32_t)(min(t0 + srx, a.n - 1) * nb + skx);
     auto load = [&](int j, int st) {
         if constexpr (FULL) {
-            if (tid < WCH) wr[j] = *reinterpret_cast<const i32x4 *>(wp0 + (size_t)st * GS_KB * WB);
-            xr[j] = *reinterpret_cast<const i32x4 *>(xp0 + (size_t)st * GS_KB * 32);
-            if (tid < NSC) {
-                dwr[j] = dwp0[st * GS_KB];
-                dxr[j] = dxp0[st * GS_KB];
-                if (DT == DT_Q4) xsr[j] = xsp0[st * GS_KB];
+            const int b0 = kb0 + st * GS_KB;
+            if (ldw) wr[j] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)b0 * WB + wo0);
+#pragma unroll
+            for (int i = 0; i < XPT; i++) xr[j][i] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)b0 * 32 + xo0[i]);
+            if (lsw) dwr[j] = (a.W.d + b0)[dwo0];
+            if (lsx) {
+                dxr[j] = (a.dx + b0)[dxo0];
+                if (DT == DT_Q4) xsr[j] = (a.xs + b0)[dxo0];
             }
             return;
         }
         const int b0 = kb0 + st * GS_KB;
-        if (tid < WCH) {
-            const int row = tid / (WROW / 16), c = (tid % (WROW / 16)) * 16;
-            const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
-            wr[j] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
+        if (ldw) {
+            const int u = min(u0 + wrow, a.units - 1), blk = min(b0 + wc / WB, nb - 1);
+            wr[j] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + wc % WB);
         }
-        {
-            const int row = tid / (XROW / 16), c = (tid % (XROW / 16)) * 16;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int cc = tid + i * NTP, row = cc / (XROW / 16), c = (cc % (XROW / 16)) * 16;
             const int t = min(t0 + row, a.n - 1), blk = min(b0 + c / 32, nb - 1);
-            xr[j] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
+            xr[j][i] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + c % 32);
         }
-        if (tid < NSC) {
-            const int kb = tid / GS_U, r = tid % GS_U, blk = min(b0 + kb, nb - 1);
-            const int t = min(t0 + r, a.n - 1);
-            dwr[j] = a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + blk];
+        if (lsw) dwr[j] = a.W.d[(size_t)min(u0 + srw, a.units - 1) * nb + min(b0 + skw, nb - 1)];
+        if (lsx) {
+            const int t = min(t0 + srx, a.n - 1), blk = min(b0 + skx, nb - 1);
             dxr[j] = a.dx[(size_t)t * nb + blk];
             if (DT == DT_Q4) xsr[j] = a.xs[(size_t)t * nb + blk];
         }
     };
     auto store = [&](int j, int buf) {
-        if (tid < WCH)
-            *reinterpret_cast<i32x4 *>(wsq[buf] + (tid / (WROW / 16)) * WP + (tid % (WROW / 16)) * 16) = wr[j];
-        *reinterpret_cast<i32x4 *>(xsq[buf] + (tid / (XROW / 16)) * XP + (tid % (XROW / 16)) * 16) = xr[j];
-        if (tid < NSC) {
-            dwq[buf][tid / GS_U][tid % GS_U] = h2f(dwr[j]);
-            dxq[buf][tid / GS_T][tid % GS_T] = dxr[j];
-            if (DT == DT_Q4) sxq[buf][tid / GS_T][tid % GS_T] = xsr[j];
+        if (ldw) *reinterpret_cast<i32x4 *>(wsq[buf] + wrow * WP + wc) = wr[j];
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int c = tid + i * NTP;
+            *reinterpret_cast<i32x4 *>(xsq[buf] + (c / (XROW / 16)) * XP + (c % (XROW / 16)) * 16) = xr[j][i];
+        }
+        if (lsw) dwq[buf][skw][srw] = h2f(dwr[j]);
+        if (lsx) {
+            dxq[buf][skx][srx] = dxr[j];
+            if (DT == DT_Q4) sxq[buf][skx][srx] = xsr[j];
         }
     };
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // one stage: its registers to LDS, the ring's next load, its fragments
+    // and scales, then its products, then the epilogues in block order
+    // (blocks past the pipeline's end contribute nothing)
+    auto stage = [&](int j, int st, bool refill) {
+        const int buf = st & 1;
+        // every wave has finished the stage that last used this buffer
+        store(j, buf);
+        __syncthreads();
+        if (refill && st + P - 1 < nst) load((j + P - 1) % P, st + P - 1);
+        const int nkb = FULL ? GS_KB : min(GS_KB, kb1 - (kb0 + st * GS_KB));
+        long af[GS_KB], bf[GS_KB];
+        float dx[GS_KB];
+        f32x4 dw[GS_KB];
+        int xsum[GS_KB];
 #pragma unroll
-    for (int j = 0; j < P - 1; j++)
-        if (j < nst) load(j, j);
-    for (int s0 = 0; s0 < nst; s0 += P) {
+        for (int kb = 0; kb < GS_KB; kb++) {
+            const uint8_t *wp = wsq[buf] + (wu + fr) * WP + kb * WB;
+            if (DT == DT_Q8) {
+                af[kb] = *reinterpret_cast<const long *>(wp + 8 * fg);
+            } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
+                const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
+                af[kb] = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
+            }
+            bf[kb] = *reinterpret_cast<const long *>(xsq[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
+            dx[kb] = dxq[buf][kb][wt + fr];
+            dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wu + 4 * fg]);
+            xsum[kb] = DT == DT_Q4 ? sxq[buf][kb][wt + fr] : 0;
+        }
+        i32x4 d[GS_KB];
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++)
+            d[kb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[kb], bf[kb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++) {
+            if (kb >= nkb) break;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
+                acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+            }
+        }
+    };
+    if constexpr (ONE) {
+        // every stage in flight from the start; stages past the last one
+        // reload it (nothing reads them), so no load is conditional and the
+        // compiler's waits count exactly the loads issued after the stage
+        // being stored
+#pragma unroll
+        for (int j = 0; j < P; j++) load(j, min(j, nst - 1));
 #pragma unroll
         for (int j = 0; j < P; j++) {
-            const int st = s0 + j;
-            if (st >= nst) break;
-            const int buf = st & 1;
-            // every wave has finished the stage that last used this buffer
-            store(j, buf);
-            __syncthreads();
-            if (st + P - 1 < nst) load((j + P - 1) % P, st + P - 1);
-            // the stage's fragments and scales first, then its products, then
-            // the epilogues in block order (blocks past the pipeline's end
-            // contribute nothing)
-            const int nkb = FULL ? GS_KB : min(GS_KB, kb1 - (kb0 + st * GS_KB));
-            long af[GS_KB], bf[GS_KB];
-            float dx[GS_KB];
-            f32x4 dw[GS_KB];
-            int xsum[GS_KB];
+            if (j >= nst) break;
+            stage(j, j, false);
+        }
+    } else {
 #pragma unroll
-            for (int kb = 0; kb < GS_KB; kb++) {
-                const uint8_t *wp = wsq[buf] + (wu + fr) * WP + kb * WB;
-                if (DT == DT_Q8) {
-                    af[kb] = *reinterpret_cast<const long *>(wp + 8 * fg);
-                } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
-                    const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
-                    af[kb] = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
-                }
-                bf[kb] = *reinterpret_cast<const long *>(xsq[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
-                dx[kb] = dxq[buf][kb][wt + fr];
-                dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wu + 4 * fg]);
-                xsum[kb] = DT == DT_Q4 ? sxq[buf][kb][wt + fr] : 0;
-            }
-            i32x4 d[GS_KB];
+        for (int j = 0; j < P - 1; j++) load(j, j);
+        for (int s0 = 0; s0 < nst; s0 += P) {
 #pragma unroll
-            for (int kb = 0; kb < GS_KB; kb++)
-                d[kb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[kb], bf[kb], i32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int kb = 0; kb < GS_KB; kb++) {
-                if (kb >= nkb) break;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
-                    acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
-                }
+            for (int j = 0; j < P; j++) {
+                const int st = s0 + j;
+                if (st >= nst) break;
+                stage(j, st, true);
             }
         }
     }
@@ -558,15 +620,14 @@ __global__ __launch_bounds__(WG * SPLIT) void k_gemm_small(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[r] += red[p][wave][lane][r];
     }
-    const int t = t0 + wt + fr;
-    if (t >= a.n) return;
+    if (to >= a.n) return;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int u = u0 + wu + 4 * fg + r;
         if (u >= a.units) continue;
-        float *o = a.out + (size_t)t * a.out_stride + u;
-        if (EPI == EPI_STORE) *o = a.bias ? acc[r] + a.bias[u] : acc[r];
-        else *o += acc[r];
+        float *o = a.out + (size_t)to * a.out_stride + u;
+        if (EPI == EPI_STORE) *o = a.bias ? acc[r] + (PRE ? pre[r] : a.bias[u]) : acc[r];
+        else *o = (PRE ? pre[r] : *o) + acc[r];
     }
 }
 
@@ -580,6 +641,9 @@ constexpr int GS_SPLIT = 4, GS_SPLIT_MIN_BLOCKS = 32, GS_SPLIT_MAX_GRID = 256;
 // workgroups, two or three per CU): half the serial walk per output for two
 // pipelines' instructions per SIMD.
 constexpr int GS_SPLIT2_MAX_GRID = 1024;
+// 32-unit grids of up to GS_U16_MAX_GRID workgroups (at most half the CUs)
+// take 16-unit tiles instead.
+constexpr int GS_U16_MAX_GRID = 128;
 
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
@@ -591,24 +655,36 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         // wo / w2 products up to 4 x that grid (pp2048 +2%, pp4096 +1.5%)
         const long g64 = (long)gu * ((a.n + 63) / 64);
         if (g64 < 256 || (a.units <= 1024 && g64 < 1024)) {
-            const dim3 gs((a.units + GS_U - 1) / GS_U, (a.n + GS_T - 1) / GS_T);
+            // 16-unit tiles when 32-unit ones would leave half the CUs idle
+            const int ty = (a.n + GS_T - 1) / GS_T;
+            const bool u16 = (long)((a.units + 31) / 32) * ty <= GS_U16_MAX_GRID;
+            const dim3 gs((a.units + (u16 ? 15 : 31)) / (u16 ? 16 : 32), ty);
             const int nb = a.W.cols / QB;
             const bool split = nb >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT_MAX_GRID;
             const bool split2 = !split && nb >= GS_SPLIT_MIN_BLOCKS && (long)gs.x * gs.y <= GS_SPLIT2_MAX_GRID;
-            const bool full = nb % (GS_KB * (split ? GS_SPLIT : split2 ? 2 : 1)) == 0;
-#define GSL(DT, SP, FL)                                                                                  \
-            if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_small<DT, EPI_STORE, SP, FL>), gs, dim3(WG * SP), 0, st, a); \
-            else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_small<DT, EPI_RESID, SP, FL>), gs, dim3(WG * SP), 0, st, a); \
+            const int sp = split ? GS_SPLIT : split2 ? 2 : 1;
+            const bool full = nb % (GS_KB * sp) == 0;
+            const int nst = ((nb + sp - 1) / sp + GS_KB - 1) / GS_KB;   // stages per pipeline
+            const bool one = nst <= gs_ring(sp, u16 ? 16 : 32);
+#define GSK(DT, E, SP, FL, UU) \
+            if (one) hipLaunchKernelGGL((k_gemm_small<DT, E, SP, FL, UU, true>), gs, dim3(UU * 8 * SP), 0, st, a); \
+            else hipLaunchKernelGGL((k_gemm_small<DT, E, SP, FL, UU, false>), gs, dim3(UU * 8 * SP), 0, st, a);
+#define GSL(DT, SP, FL, UU)                                                                              \
+            if (epi == EPI_STORE) { GSK(DT, EPI_STORE, SP, FL, UU) }                                        \
+            else if (epi == EPI_RESID) { GSK(DT, EPI_RESID, SP, FL, UU) }                                   \
             else return -1;                                                                              \
             return 0;
+#define GSU(DT, SP, FL) if (u16) { GSL(DT, SP, FL, 16) } else { GSL(DT, SP, FL, 32) }
 #define GSF(DT)                                                                                          \
-            if (split) { if (full) { GSL(DT, GS_SPLIT, true) } else { GSL(DT, GS_SPLIT, false) } }      \
-            if (split2) { if (full) { GSL(DT, 2, true) } else { GSL(DT, 2, false) } }                    \
-            if (full) { GSL(DT, 1, true) } else { GSL(DT, 1, false) }
+            if (split) { if (full) { GSU(DT, GS_SPLIT, true) } else { GSU(DT, GS_SPLIT, false) } }      \
+            if (split2) { if (full) { GSU(DT, 2, true) } else { GSU(DT, 2, false) } }                    \
+            if (full) { GSU(DT, 1, true) } else { GSU(DT, 1, false) }
             if (a.W.dtype == DT_Q8) { GSF(DT_Q8) }
             GSF(DT_Q4)
 #undef GSF
+#undef GSU
 #undef GSL
+#undef GSK
         }
         const bool t64 = (long)gu * ((a.n + 127) / 128) < 256;
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);

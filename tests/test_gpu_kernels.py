@@ -134,13 +134,16 @@ def test_prefill_kernels_512(name):
     assert ok, text
 
 
-@pytest.mark.parametrize("name,n", [("qwen3_06b", 128), ("qwen25_05b", 256), ("smollm2_135m", 200)],
-                         ids=["qwen3_06b-128", "qwen25_05b-256", "smollm2_135m-200"])
+@pytest.mark.parametrize("name,n", [("qwen3_06b", 128), ("qwen3_06b_q4", 128), ("qwen25_05b", 256),
+                                    ("smollm2_135m", 200), ("stories110m", 128)],
+                         ids=["qwen3_06b-128", "qwen3_06b_q4-128", "qwen25_05b-256", "smollm2_135m-200",
+                              "stories110m-128"])
 def test_prefill_kernels_short(name, n):
     """Short prompts: the one-kernel exact-order attention (scores, softmax,
-    P.V and the wo input's Q8_0 blocks; 2, 7 and 3 query heads per kv head,
-    head_dim 128 and 64) and the 32x32-tile GEMM with and without whole
-    stages and the K split."""
+    P.V and the wo input's Q8_0 blocks; 1, 2, 7 and 3 query heads per kv
+    head, head_dim 128 and 64) and the short-prompt GEMM with 32- and
+    16-unit tiles, with and without whole stages and the K split, Q8_0 and
+    Q4_0 weights."""
     last = configs.ALL[name]["n_layers"] - 1
     ok, text = _prefill_kernels(name, n, [(0, 0), (last, 0)])
     assert ok, text

@@ -8,7 +8,7 @@ leg, as the checker or the timed CPU stand-in, never by the product.
                     optimized flags, for timing)
   Reference(...)    the reference library itself, compiled from its own
                     sources by ref.mk into oracle/_ref/ (present only where it
-                    was built; the GPU box receives the built file)
+                    was built; where it is run, the built file comes along)
 """
 import ctypes
 import os

@@ -1,6 +1,6 @@
 """Tolerances and comparison helpers for end-to-end GPU-vs-oracle parity.
 
-The north-star bar is per-step logits within 1e-2 max-abs and 1e-3 relative
+The target bar is per-step logits within 1e-2 max-abs and 1e-3 relative
 L2 of the reference CPU path, with >= 99% top-1 agreement under teacher
 forcing.  It holds on the small variant models (rel-L2 ~4e-8) and does NOT
 hold end to end on the deep benchmark shapes, where the GPU path differs from

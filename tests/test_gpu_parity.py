@@ -2,7 +2,7 @@
 against the oracle (the CPU restatement, bit-exact with the reference's
 deterministic build) on identical seeded weights and token streams.
 
-Tolerances: tests/parity.py (the north-star bar 1e-2 max-abs / 1e-3 rel-L2 /
+Tolerances: tests/parity.py (the target bar 1e-2 max-abs / 1e-3 rel-L2 /
 99% top-1, which the small variant models meet; on the deep benchmark shapes
 raised to 1.5x the reference's own optimized-vs-deterministic deviation,
 which is ~1e-2 relative L2 there: see parity.py, and test_gpu_kernels.py for

@@ -19,7 +19,7 @@ the noise floor of the reference's two builds measured over the very same
 workload protocol (the optimized build teacher forced on the deterministic
 build's tokens; tests/parity.py), whose top-1 agreement there is 0.992,
 1.000, 0.961, 0.946 and 0.984; the kernel-level bound (1e-6) is
-test_gpu_kernels'.  The north-star figures (1e-3 relative L2, 1e-2 max-abs,
+test_gpu_kernels'.  The target figures (1e-3 relative L2, 1e-2 max-abs,
 99% top-1) are printed beside the bars for every run.
 
 The device-held loops must also reproduce the C-API loop exactly: the greedy
@@ -45,11 +45,11 @@ def say(msg):
     sys.stdout.flush()
 
 
-def north_star(res):
+def target_view(res):
     rel = np.array([r["rel_l2"] for r in res])
     mab = np.array([r["max_abs"] for r in res])
     top = np.mean([r["agree"] for r in res])
-    return (f"north-star view: rel-L2 median {np.median(rel):.2e} (bar 1e-3), max-abs median "
+    return (f"target-bar view: rel-L2 median {np.median(rel):.2e} (bar 1e-3), max-abs median "
             f"{np.median(mab):.2e} (bar 1e-2), top-1 {top:.3f} (bar 0.99)")
 
 
@@ -98,7 +98,7 @@ def _run(name, prompt, steps, sampled=False):
     same = np.mean(np.asarray(got) == np.asarray(toks))
     say(f"{name}: device loop reproduces the API loop on {same * 100:.1f}% of {steps} tokens")
     assert same == 1.0, (list(got[:20]), toks[:20])
-    say(north_star(res))
+    say(target_view(res))
     # bars: the reference's optimized build against its deterministic build
     # over this same protocol (noise_floor.json, make_golden.py workload)
     say(check_run(res, f"{name}-pp{prompt}-tg{steps}"))

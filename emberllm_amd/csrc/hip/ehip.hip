@@ -401,6 +401,7 @@ struct EhipState {
     // prefill scratch
     float *X, *QKV, *O, *H, *xf, *dxp;
     int8_t *qx; int *xsum, *ids_d;
+    int8_t *qx2; float *dxp2; int *xsum2;   // the w2 input's codes when the w1|w3 product quantizes them
     // prefill attention scratch: scores [n_heads][pf_chunk][ldk], tile maxima
     // [n_heads][pf_chunk][attn_prefill_tiles(ldk)], row max and 1/sum [n_heads][pf_chunk]
     float *pf_scores, *pf_tmax, *pf_rowmax, *pf_rowinv;
@@ -596,6 +597,9 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->qx = (int8_t *)salloc(s, pfc * wide)) &&
               (s->dxp = (float *)salloc(s, 4 * pfc * (wide / QB + 1))) &&
               (s->xsum = (int *)salloc(s, 4 * pfc * (wide / QB + 1))) &&
+              (s->qx2 = (int8_t *)salloc(s, pfc * c.hidden_dim)) &&
+              (s->dxp2 = (float *)salloc(s, 4 * pfc * (c.hidden_dim / QB + 1))) &&
+              (s->xsum2 = (int *)salloc(s, 4 * pfc * (c.hidden_dim / QB + 1))) &&
               (s->ids_d = (int *)salloc(s, 4 * pfc)) &&
 
               (s->am_val = (float *)salloc(s, 4 * (size_t)std::max(ARGMAX_MAX_BLOCKS, MATVEC_MAX_GRID))) &&
@@ -1093,14 +1097,25 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             GemmArgs g3{};
             g3.W = y.w13; g3.units = 2 * hid; g3.n = mt; g3.qx = s->qx; g3.dx = s->dxp; g3.xs = s->xsum;
             g3.xf = q.xf; g3.out = s->H; g3.out_stride = 2 * hid;
-            rc |= launch_gemm(s->st, EPI_STORE, g3);
-            if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return -1;
-            QuantRowsArgs q4{};
-            q4.x = s->H; q4.x_stride = 2 * hid; q4.cols = hid; q4.n = mt; q4.swiglu = 1;
-            q4.xf = q.xf; q4.qx = s->qx; q4.dx = s->dxp; q4.xs = s->xsum;
-            rc |= launch_quant_rows(s->st, q4);
             GemmArgs g4{};
             g4.W = y.w2; g4.units = c.dim; g4.n = mt; g4.qx = s->qx; g4.dx = s->dxp; g4.xs = s->xsum;
+            // short prompts: the SwiGLU and its quantization in the w1|w3
+            // product's epilogue (the gate | up rows written only for a capture)
+            GemmArgs gs = g3;
+            gs.units = hid; gs.pair_off = hid; gs.oq = s->qx2; gs.odx = s->dxp2; gs.oxs = s->xsum2;
+            gs.out = snap ? s->H : nullptr;
+            if (!q.xf && gemm_swiglu_fits(gs)) {
+                rc |= launch_gemm_swiglu(s->st, gs);
+                if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return -1;
+                g4.qx = s->qx2; g4.dx = s->dxp2; g4.xs = s->xsum2;
+            } else {
+                rc |= launch_gemm(s->st, EPI_STORE, g3);
+                if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return -1;
+                QuantRowsArgs q4{};
+                q4.x = s->H; q4.x_stride = 2 * hid; q4.cols = hid; q4.n = mt; q4.swiglu = 1;
+                q4.xf = q.xf; q4.qx = s->qx; q4.dx = s->dxp; q4.xs = s->xsum;
+                rc |= launch_quant_rows(s->st, q4);
+            }
             g4.xf = q.xf; g4.out = s->X; g4.out_stride = c.dim;
             rc |= launch_gemm(s->st, EPI_RESID, g4);
             if (psnap(DBG_XOUT, s->X, c.dim, c.dim)) return -1;

@@ -631,6 +631,184 @@ void k_gemm_small(GemmArgs a) {
     }
 }
 
+// k_gemm_swq: the w1|w3 product of a short prompt with the SwiGLU and the
+// Q8_0 quantization of its rows in the epilogue (replacing k_quant_rows's
+// SwiGLU pass and its launch).  A workgroup takes SW_U = 32 hidden units
+// (their 32 gate and 32 up weight rows) x SW_T = 16 tokens, so each token's
+// 32 SwiGLU values of the tile are one Q8_0 block; wave w computes the 16 x 16
+// tile of rows 32 (w / 2) + 16 (w % 2) with the stage machinery of
+// k_gemm_small's straight-line form (every stage in flight from the start;
+// SPLIT pipelines over K added in pipeline order).  The gate and up sums meet
+// in LDS; then eight lanes per token apply g / (1 + expf(-g)) * u
+// (model.c:403-406) and quantize the block with k_quant_rows's arithmetic.
+constexpr int SW_U = 32, SW_T = 16;
+__host__ __device__ constexpr int sw_ring(int split) { return split > 1 ? 4 : 8; }
+template <int DT, int SPLIT, bool FULL>
+__global__ __launch_bounds__(256 * SPLIT, SPLIT == 2 ? 4 : 1) void k_gemm_swq(GemmArgs a) {
+    constexpr int NTP = 256, P = sw_ring(SPLIT), RW = 2 * SW_U;   // threads per pipeline, ring, weight rows
+    constexpr int WB = DT == DT_Q8 ? 32 : 16;
+    constexpr int WROW = GS_KB * WB, XROW = GS_KB * 32, WP = WROW + 16, XP = XROW + 16;
+    constexpr int WCH = RW * WROW / 16, WPT = (WCH + NTP - 1) / NTP;   // weight chunks (per thread)
+    constexpr int XCH = SW_T * XROW / 16;                      // token chunks (threads past them repeat the last)
+    constexpr int NSW = GS_KB * RW, NSX = GS_KB * SW_T;        // weight / token scales per stage
+    static_assert(WCH % NTP == 0 || WCH < NTP, "weight chunks per thread");
+    static_assert(XCH <= NTP && NSW <= NTP && NSX <= NTP, "one token chunk and scale per thread");
+    __shared__ __align__(16) uint8_t ws[SPLIT][2][RW * WP];
+    __shared__ __align__(16) int8_t xsm[SPLIT][2][SW_T * XP];
+    __shared__ __align__(16) float dws[SPLIT][2][GS_KB][RW], dxs[SPLIT][2][GS_KB][SW_T];
+    __shared__ int sxs[SPLIT][2][GS_KB][SW_T];
+    __shared__ __align__(16) float red[SPLIT > 1 ? SPLIT - 1 : 1][4][64][4];
+    __shared__ float hs[SW_T][RW + 1];                         // [token][gate 0..31 | up 32..63]
+    const int tid = threadIdx.x % NTP, q = threadIdx.x / NTP;
+    const int lane = tid & 63, wave = tid >> 6, fr = lane & 15, fg = lane >> 4;
+    const int wr0 = (wave >> 1) * SW_U + (wave & 1) * 16;     // the wave's first tile row
+    const int u0 = blockIdx.x * SW_U, t0 = blockIdx.y * SW_T;
+    const int K = a.W.cols, nb = K / QB;
+    const int nbq = (nb + SPLIT - 1) / SPLIT, kb0 = q * nbq, kb1 = min(nb, kb0 + nbq);
+    const int nst = (nbq + GS_KB - 1) / GS_KB;                // <= P (checked by the launcher)
+    uint8_t (&wsq)[2][RW * WP] = ws[q];
+    int8_t (&xsq)[2][SW_T * XP] = xsm[q];
+    float (&dwq)[2][GS_KB][RW] = dws[q];
+    float (&dxq)[2][GS_KB][SW_T] = dxs[q];
+    int (&sxq)[2][GS_KB][SW_T] = sxs[q];
+    // weight row of tile row r: gate rows u0.., then up rows pair_off + u0..
+    auto wrow_of = [&](int r) { return (r < SW_U ? 0 : a.pair_off) + min(u0 + r % SW_U, a.units - 1); };
+
+    i32x4 wr[P][WPT], xr[P];
+    uint16_t dwr[P];
+    float dxr[P];
+    int xsr[P];
+    // every load and store is unconditional: threads past the last chunk or
+    // scale repeat it (the same value to the same LDS word)
+    int wrow[WPT], wc[WPT];
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+        const int c = min(tid + i * NTP, WCH - 1);
+        wrow[i] = c / (WROW / 16);
+        wc[i] = (c % (WROW / 16)) * 16;
+    }
+    const int xcn = min(tid, XCH - 1), xrow = xcn / (XROW / 16), xc = (xcn % (XROW / 16)) * 16;
+    const int skw = min(tid, NSW - 1) / RW, srw = min(tid, NSW - 1) % RW;
+    const int skx = min(tid, NSX - 1) / SW_T, srx = min(tid, NSX - 1) % SW_T;
+    auto load = [&](int j, int st) {
+        const int b0 = kb0 + st * GS_KB;
+#pragma unroll
+        for (int i = 0; i < WPT; i++) {
+            const int blk = FULL ? b0 + wc[i] / WB : min(b0 + wc[i] / WB, nb - 1);
+            wr[j][i] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)wrow_of(wrow[i]) * (nb * WB) +
+                                                        (size_t)blk * WB + wc[i] % WB);
+        }
+        {
+            const int t = min(t0 + xrow, a.n - 1), blk = FULL ? b0 + xc / 32 : min(b0 + xc / 32, nb - 1);
+            xr[j] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + xc % 32);
+        }
+        dwr[j] = a.W.d[(size_t)wrow_of(srw) * nb + (FULL ? b0 + skw : min(b0 + skw, nb - 1))];
+        {
+            const int t = min(t0 + srx, a.n - 1), blk = FULL ? b0 + skx : min(b0 + skx, nb - 1);
+            dxr[j] = a.dx[(size_t)t * nb + blk];
+            if (DT == DT_Q4) xsr[j] = a.xs[(size_t)t * nb + blk];
+        }
+    };
+    auto store = [&](int j, int buf) {
+#pragma unroll
+        for (int i = 0; i < WPT; i++) *reinterpret_cast<i32x4 *>(wsq[buf] + wrow[i] * WP + wc[i]) = wr[j][i];
+        *reinterpret_cast<i32x4 *>(xsq[buf] + xrow * XP + xc) = xr[j];
+        dwq[buf][skw][srw] = h2f(dwr[j]);
+        dxq[buf][skx][srx] = dxr[j];
+        if (DT == DT_Q4) sxq[buf][skx][srx] = xsr[j];
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < P; j++) load(j, min(j, nst - 1));
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        if (j >= nst) break;
+        const int buf = j & 1;
+        store(j, buf);
+        __syncthreads();
+        const int nkb = FULL ? GS_KB : min(GS_KB, kb1 - (kb0 + j * GS_KB));
+        long af[GS_KB], bf[GS_KB];
+        float dx[GS_KB];
+        f32x4 dw[GS_KB];
+        int xsum[GS_KB];
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++) {
+            const uint8_t *wp = wsq[buf] + (wr0 + fr) * WP + kb * WB;
+            if (DT == DT_Q8) {
+                af[kb] = *reinterpret_cast<const long *>(wp + 8 * fg);
+            } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
+                const unsigned long long raw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
+                af[kb] = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
+            }
+            bf[kb] = *reinterpret_cast<const long *>(xsq[buf] + fr * XP + kb * 32 + 8 * fg);
+            dx[kb] = dxq[buf][kb][fr];
+            dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wr0 + 4 * fg]);
+            xsum[kb] = DT == DT_Q4 ? sxq[buf][kb][fr] : 0;
+        }
+        i32x4 d[GS_KB];
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++)
+            d[kb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[kb], bf[kb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++) {
+            if (kb >= nkb) break;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
+                acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+            }
+        }
+    }
+    if constexpr (SPLIT > 1) {   // the pipelines' sums, added in pipeline order
+        if (q > 0)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[q - 1][wave][lane][r] = acc[r];
+        __syncthreads();
+        if (q == 0)
+#pragma unroll
+            for (int p = 0; p < SPLIT - 1; p++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] += red[p][wave][lane][r];
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) hs[fr][wr0 + 4 * fg + r] = acc[r];
+        if (a.out && t0 + fr < a.n)   // the gate | up products themselves, where asked for
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tr = wr0 + 4 * fg + r, u = u0 + tr % SW_U;
+                if (u < a.units) a.out[(size_t)(t0 + fr) * a.out_stride + (tr < SW_U ? 0 : a.pair_off) + u] = acc[r];
+            }
+    }
+    __syncthreads();
+    if (q > 0 || tid >= SW_T * 8) return;
+    // token tid / 8, hidden units 4 (tid % 8) .. + 3 of the tile
+    const int tt = tid >> 3, hp = (tid & 7) * 4;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float g = hs[tt][hp + i], u = hs[tt][SW_U + hp + i];
+        v[i] = g / (1.0f + expf(-g)) * u;
+    }
+    const float mx = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    const float dq = mx / 127.0f;
+    const float id = dq > 0.0f ? 1.0f / dq : 0.0f;
+    int c[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) c[i] = (int)fminf(fmaxf(roundf(v[i] * id), -127.0f), 127.0f);
+    const int cs = sum8(c[0] + c[1] + c[2] + c[3]);
+    const int t = t0 + tt;
+    if (t >= a.n || u0 + hp >= a.units) return;
+    const int nbo = a.units / QB;
+    *reinterpret_cast<uint32_t *>(a.oq + (size_t)t * a.units + u0 + hp) =
+        ((uint32_t)c[0] & 0xffu) | (((uint32_t)c[1] & 0xffu) << 8) | (((uint32_t)c[2] & 0xffu) << 16) |
+        (((uint32_t)c[3] & 0xffu) << 24);
+    if (hp == 0) {
+        a.odx[(size_t)t * nbo + u0 / QB] = h2f(f2h(dq));
+        a.oxs[(size_t)t * nbo + u0 / QB] = cs;
+    }
+}
+
 // K of at least 1024 (32 blocks) splits into 4 pipelines when the grid fits
 // the GPU at one 1024-thread workgroup per CU (the split's LDS); shorter K
 // keeps the blocks of every output in one sequential sum, and a larger grid
@@ -708,6 +886,33 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     G(DT_Q8) G(DT_Q4) G(DT_F32)
 #undef G
     return -1;
+}
+
+
+bool gemm_swiglu_fits(const GemmArgs &a) {
+    if ((a.W.dtype != DT_Q8 && a.W.dtype != DT_Q4) || a.n <= 0 || a.units % SW_U != 0 || a.W.cols % QB != 0)
+        return false;
+    if (!a.oq || !a.odx || !a.oxs || a.pair_off < a.units) return false;
+    // the shapes whose w1|w3 product launch_gemm gives the short-prompt kernel
+    const long g64 = (long)((2 * a.units + GM_U - 1) / GM_U) * ((a.n + 63) / 64);
+    if (!(g64 < 256 || (2 * a.units <= 1024 && g64 < 1024))) return false;
+    const int nb = a.W.cols / QB, sp = nb >= GS_SPLIT_MIN_BLOCKS ? 2 : 1;
+    return ((nb + sp - 1) / sp + GS_KB - 1) / GS_KB <= sw_ring(sp);
+}
+
+int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a) {
+    if (!gemm_swiglu_fits(a)) return -1;
+    const int nb = a.W.cols / QB, sp = nb >= GS_SPLIT_MIN_BLOCKS ? 2 : 1;
+    const bool full = nb % (GS_KB * sp) == 0;
+    const dim3 g(a.units / SW_U, (a.n + SW_T - 1) / SW_T), b(256 * sp);
+#define SWL(DT)                                                                            \
+    if (sp == 2) { if (full) hipLaunchKernelGGL((k_gemm_swq<DT, 2, true>), g, b, 0, st, a); \
+                   else hipLaunchKernelGGL((k_gemm_swq<DT, 2, false>), g, b, 0, st, a); }   \
+    else if (full) hipLaunchKernelGGL((k_gemm_swq<DT, 1, true>), g, b, 0, st, a);           \
+    else hipLaunchKernelGGL((k_gemm_swq<DT, 1, false>), g, b, 0, st, a);
+    if (a.W.dtype == DT_Q8) { SWL(DT_Q8) } else { SWL(DT_Q4) }
+#undef SWL
+    return 0;
 }
 
 }  // namespace ehip

@@ -156,8 +156,18 @@ struct GemmArgs {
     const float *xf;                                     // fp32 X (F32 weights)
     float *out; int out_stride;
     const float *bias;
+    // launch_gemm_swiglu: the SwiGLU rows' Q8_0 codes [n][units], fp16-rounded
+    // block scales and code sums [n][units / 32], for the next product
+    int8_t *oq; float *odx; int *oxs;
 };
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a);
+// The w1|w3 product of a short prompt with the SwiGLU and its Q8_0
+// quantization in the epilogue: W holds the gate rows, then the up rows at
+// pair_off; units = hidden units (a multiple of 32).  out, when set, also
+// receives the gate | up products (out_stride floats per token).  Returns -1
+// where gemm_swiglu_fits() is false.
+bool gemm_swiglu_fits(const GemmArgs &a);
+int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a);
 
 // ---------------------------------------------------------------- sample --
 // Greedy selection (first maximum) over n logits; writes tokpos[0] = token,

@@ -1060,15 +1060,21 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             GemmArgs g{};
             g.W = y.qkv; g.units = stride; g.n = mt; g.qx = s->qx; g.dx = s->dxp; g.xs = s->xsum; g.xf = q.xf;
             g.out = s->QKV; g.out_stride = stride; g.bias = y.bias_qkv;
-            rc |= launch_gemm(s->st, EPI_STORE, g);
-            if (psnap(DBG_QKV, s->QKV, stride, stride)) return -1;
             QkPostArgs p{};
             p.qkv = s->QKV; p.stride = stride; p.q_norm = y.q_norm; p.k_norm = y.k_norm;
             p.rope = s->rope; p.eps = c.norm_eps; p.rope_style = c.rope_style;
             AttnArgs at = attn_args(s, l);
             p.kc = at.kc; p.vc = at.vc; p.kv_dim = kvd; p.hd = hd; p.n_heads = c.n_heads;
             p.n_kv = c.n_kv_heads; p.pos_base = pos0; p.n_tok = mt;
-            rc |= launch_qkpost(s->st, s->f16kv, p);
+            if (!q.xf && gemm_qkv_fits(g, p)) {
+                // short prompts: the QK-norm, RoPE and cache stores in the
+                // product's epilogue (the raw product goes straight to a capture)
+                rc |= launch_gemm_qkv(s->st, s->f16kv, g, p, snap ? s->pdbg[DBG_QKV] : nullptr);
+            } else {
+                rc |= launch_gemm(s->st, EPI_STORE, g);
+                if (psnap(DBG_QKV, s->QKV, stride, stride)) return -1;
+                rc |= launch_qkpost(s->st, s->f16kv, p);
+            }
             at.q = s->QKV; at.q_stride = stride; at.pos_base = pos0; at.n_tok = mt;
             at.out = s->O;
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;

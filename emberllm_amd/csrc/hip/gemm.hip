@@ -809,6 +809,226 @@ __global__ __launch_bounds__(256 * SPLIT, SPLIT == 2 ? 4 : 1) void k_gemm_swq(Ge
     }
 }
 
+// k_gemm_qkv: the q|k|v product of a short prompt with k_qkpost's work in
+// the epilogue (replacing that kernel and its launch).  A workgroup takes one
+// head vector (HD units: a q, k or v head) x QV_T = 16 tokens, wave w the
+// 16 x 16 tile of units 16 w, with the stage machinery of k_gemm_small's
+// straight-line form.  The tile (with the bias) meets in LDS; then a wave
+// per token does what k_qkpost does for it, with the same lane layout (lane
+// l holds elements l, l + 64) and so the same sums: the RMSNorm of q and k
+// heads (model.c:386-389), RoPE from the host table (model.c:66-80), q back
+// into its q|k|v row, k and v into the cache (model.c:39-48).
+constexpr int QV_T = 16;
+__host__ __device__ constexpr int qv_ring(int split) { return split > 1 ? 4 : 8; }
+template <int DT, int SPLIT, bool FULL, int HD, bool F16>
+__global__ __launch_bounds__(64 * (HD / 16) * SPLIT) void k_gemm_qkv(GemmArgs a, QkPostArgs p, float *raw) {
+    constexpr int NWP = HD / 16, NTP = 64 * NWP, P = qv_ring(SPLIT);
+    constexpr int WB = DT == DT_Q8 ? 32 : 16;
+    constexpr int WROW = GS_KB * WB, XROW = GS_KB * 32, WP = WROW + 16, XP = XROW + 16;
+    constexpr int WCH = HD * WROW / 16, WPT = (WCH + NTP - 1) / NTP;
+    constexpr int XCH = QV_T * XROW / 16;
+    constexpr int NSW = GS_KB * HD, NSX = GS_KB * QV_T;
+    constexpr int ND = HD / 64, TPW = QV_T / NWP;             // elements per lane, tokens per wave
+    static_assert(WCH % NTP == 0 || WCH < NTP, "weight chunks per thread");
+    static_assert(XCH <= NTP && NSW <= NTP && NSX <= NTP && HD % 64 == 0, "one token chunk and scale per thread");
+    __shared__ __align__(16) uint8_t ws[SPLIT][2][HD * WP];
+    __shared__ __align__(16) int8_t xsm[SPLIT][2][QV_T * XP];
+    __shared__ __align__(16) float dws[SPLIT][2][GS_KB][HD], dxs[SPLIT][2][GS_KB][QV_T];
+    __shared__ int sxs[SPLIT][2][GS_KB][QV_T];
+    __shared__ __align__(16) float red[SPLIT > 1 ? SPLIT - 1 : 1][NWP][64][4];
+    __shared__ float hs[QV_T][HD + 1];
+    const int tid = threadIdx.x % NTP, q = threadIdx.x / NTP;
+    const int lane = tid & 63, wave = tid >> 6, fr = lane & 15, fg = lane >> 4;
+    const int vh = blockIdx.x, u0 = vh * HD, t0 = blockIdx.y * QV_T, wu = wave * 16;
+    const int K = a.W.cols, nb = K / QB;
+    const int nbq = (nb + SPLIT - 1) / SPLIT, kb0 = q * nbq, kb1 = min(nb, kb0 + nbq);
+    const int nst = (nbq + GS_KB - 1) / GS_KB;                // <= P (checked by the launcher)
+    uint8_t (&wsq)[2][HD * WP] = ws[q];
+    int8_t (&xsq)[2][QV_T * XP] = xsm[q];
+    float (&dwq)[2][GS_KB][HD] = dws[q];
+    float (&dxq)[2][GS_KB][QV_T] = dxs[q];
+    int (&sxq)[2][GS_KB][QV_T] = sxs[q];
+
+    // the epilogue's per-head inputs, loaded first: head kind, norm weights,
+    // bias and the RoPE rows of the wave's tokens
+    const bool isq = vh < p.n_heads, isk = !isq && vh < p.n_heads + p.n_kv;
+    const int g = vh - p.n_heads - (isk || isq ? 0 : p.n_kv);  // kv head of a k or v head
+    const bool neox = p.rope_style == ROPE_NEOX;
+    const float *nwp = isq ? p.q_norm : p.k_norm;
+    float nwv[ND];
+    float2 cs[TPW][ND];
+#pragma unroll
+    for (int k = 0; k < ND; k++) {
+        const int d = lane + 64 * k, i = neox ? d % (HD / 2) : d / 2;
+        nwv[k] = p.q_norm && (isq || isk) ? nwp[d] : 1.0f;
+#pragma unroll
+        for (int j = 0; j < TPW; j++) {
+            const int t = min(t0 + wave * TPW + j, a.n - 1);
+            cs[j][k] = p.rope[(size_t)(p.pos_base + t) * (HD / 2) + i];
+        }
+    }
+    float bias[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) bias[r] = a.bias ? a.bias[u0 + wu + 4 * fg + r] : 0.0f;
+
+    i32x4 wr[P][WPT], xr[P];
+    uint16_t dwr[P];
+    float dxr[P];
+    int xsr[P];
+    // every load and store is unconditional: threads past the last chunk or
+    // scale repeat it (the same value to the same LDS word)
+    int wrow[WPT], wc[WPT];
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+        const int c = min(tid + i * NTP, WCH - 1);
+        wrow[i] = c / (WROW / 16);
+        wc[i] = (c % (WROW / 16)) * 16;
+    }
+    const int xcn = min(tid, XCH - 1), xrow = xcn / (XROW / 16), xc = (xcn % (XROW / 16)) * 16;
+    const int skw = min(tid, NSW - 1) / HD, srw = min(tid, NSW - 1) % HD;
+    const int skx = min(tid, NSX - 1) / QV_T, srx = min(tid, NSX - 1) % QV_T;
+    auto load = [&](int j, int st) {
+        const int b0 = kb0 + st * GS_KB;
+#pragma unroll
+        for (int i = 0; i < WPT; i++) {
+            const int blk = FULL ? b0 + wc[i] / WB : min(b0 + wc[i] / WB, nb - 1);
+            wr[j][i] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)(u0 + wrow[i]) * (nb * WB) +
+                                                        (size_t)blk * WB + wc[i] % WB);
+        }
+        {
+            const int t = min(t0 + xrow, a.n - 1), blk = FULL ? b0 + xc / 32 : min(b0 + xc / 32, nb - 1);
+            xr[j] = *reinterpret_cast<const i32x4 *>(a.qx + (size_t)t * K + (size_t)blk * 32 + xc % 32);
+        }
+        dwr[j] = a.W.d[(size_t)(u0 + srw) * nb + (FULL ? b0 + skw : min(b0 + skw, nb - 1))];
+        {
+            const int t = min(t0 + srx, a.n - 1), blk = FULL ? b0 + skx : min(b0 + skx, nb - 1);
+            dxr[j] = a.dx[(size_t)t * nb + blk];
+            if (DT == DT_Q4) xsr[j] = a.xs[(size_t)t * nb + blk];
+        }
+    };
+    auto store = [&](int j, int buf) {
+#pragma unroll
+        for (int i = 0; i < WPT; i++) *reinterpret_cast<i32x4 *>(wsq[buf] + wrow[i] * WP + wc[i]) = wr[j][i];
+        *reinterpret_cast<i32x4 *>(xsq[buf] + xrow * XP + xc) = xr[j];
+        dwq[buf][skw][srw] = h2f(dwr[j]);
+        dxq[buf][skx][srx] = dxr[j];
+        if (DT == DT_Q4) sxq[buf][skx][srx] = xsr[j];
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < P; j++) load(j, min(j, nst - 1));
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        if (j >= nst) break;
+        const int buf = j & 1;
+        store(j, buf);
+        __syncthreads();
+        const int nkb = FULL ? GS_KB : min(GS_KB, kb1 - (kb0 + j * GS_KB));
+        long af[GS_KB], bf[GS_KB];
+        float dx[GS_KB];
+        f32x4 dw[GS_KB];
+        int xsum[GS_KB];
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++) {
+            const uint8_t *wp = wsq[buf] + (wu + fr) * WP + kb * WB;
+            if (DT == DT_Q8) {
+                af[kb] = *reinterpret_cast<const long *>(wp + 8 * fg);
+            } else {   // nibbles: low = weights 0..15, high = 16..31 of the block
+                const unsigned long long rw = *reinterpret_cast<const unsigned long long *>(wp + 8 * (fg & 1));
+                af[kb] = (long)((rw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
+            }
+            bf[kb] = *reinterpret_cast<const long *>(xsq[buf] + fr * XP + kb * 32 + 8 * fg);
+            dx[kb] = dxq[buf][kb][fr];
+            dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wu + 4 * fg]);
+            xsum[kb] = DT == DT_Q4 ? sxq[buf][kb][fr] : 0;
+        }
+        i32x4 d[GS_KB];
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++)
+            d[kb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[kb], bf[kb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int kb = 0; kb < GS_KB; kb++) {
+            if (kb >= nkb) break;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
+                acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+            }
+        }
+    }
+    if constexpr (SPLIT > 1) {   // the pipelines' sums, added in pipeline order
+        if (q > 0)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[q - 1][wave][lane][r] = acc[r];
+        __syncthreads();
+        if (q == 0)
+#pragma unroll
+            for (int s2 = 0; s2 < SPLIT - 1; s2++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] += red[s2][wave][lane][r];
+    }
+    if (q == 0) {   // the product with its bias (EPI_STORE's order: sum, then + bias)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float v = a.bias ? acc[r] + bias[r] : acc[r];
+            hs[fr][wu + 4 * fg + r] = v;
+            if (raw && t0 + fr < a.n) raw[(size_t)(t0 + fr) * p.stride + u0 + wu + 4 * fg + r] = v;
+        }
+    }
+    __syncthreads();
+    if (q > 0) return;
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int tt = wave * TPW + j, t = t0 + tt;              // uniform over the wave
+        if (t >= a.n) break;
+        const int pos = p.pos_base + t;
+        float x[ND];
+#pragma unroll
+        for (int k = 0; k < ND; k++) x[k] = hs[tt][lane + 64 * k];
+        if (!isq && !isk) {   // a v head: to the cache as it is
+            const size_t off = (size_t)pos * p.kv_dim + (size_t)g * HD;
+#pragma unroll
+            for (int k = 0; k < ND; k++) {
+                if (F16) reinterpret_cast<uint16_t *>(p.vc)[off + lane + 64 * k] = f2h(x[k]);
+                else reinterpret_cast<float *>(p.vc)[off + lane + 64 * k] = x[k];
+            }
+            continue;
+        }
+        if (p.q_norm) {   // RMSNorm of the head vector (model.c:50-55)
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < ND; k++) ss += x[k] * x[k];
+            ss = wave_sum(ss);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+            for (int k = 0; k < ND; k++) x[k] = x[k] * scale * nwv[k];
+        }
+        // RoPE: the first element of a pair becomes v0 * cos - v1 * sin, the
+        // second v0 * sin + v1 * cos
+        float y[ND];
+#pragma unroll
+        for (int k = 0; k < ND; k++) {
+            const int d = lane + 64 * k;
+            const bool first = neox ? d < HD / 2 : (d & 1) == 0;
+            float xp;
+            if (HD == 128 && neox) xp = x[k ^ 1];
+            else xp = __shfl(x[k], (neox ? (d < HD / 2 ? d + HD / 2 : d - HD / 2) : d ^ 1) % 64);
+            y[k] = first ? x[k] * cs[j][k].x - xp * cs[j][k].y : xp * cs[j][k].y + x[k] * cs[j][k].x;
+        }
+        if (isq) {
+#pragma unroll
+            for (int k = 0; k < ND; k++) p.qkv[(size_t)t * p.stride + u0 + lane + 64 * k] = y[k];
+        } else {
+            const size_t off = (size_t)pos * p.kv_dim + (size_t)g * HD;
+#pragma unroll
+            for (int k = 0; k < ND; k++) {
+                if (F16) reinterpret_cast<uint16_t *>(p.kc)[off + lane + 64 * k] = f2h(y[k]);
+                else reinterpret_cast<float *>(p.kc)[off + lane + 64 * k] = y[k];
+            }
+        }
+    }
+}
+
 // K of at least 1024 (32 blocks) splits into 4 pipelines when the grid fits
 // the GPU at one 1024-thread workgroup per CU (the split's LDS); shorter K
 // keeps the blocks of every output in one sequential sum, and a larger grid
@@ -912,6 +1132,36 @@ int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a) {
     else hipLaunchKernelGGL((k_gemm_swq<DT, 1, false>), g, b, 0, st, a);
     if (a.W.dtype == DT_Q8) { SWL(DT_Q8) } else { SWL(DT_Q4) }
 #undef SWL
+    return 0;
+}
+
+
+bool gemm_qkv_fits(const GemmArgs &g, const QkPostArgs &p) {
+    if ((g.W.dtype != DT_Q8 && g.W.dtype != DT_Q4) || g.n <= 0 || g.W.cols % QB != 0) return false;
+    if ((p.hd != 64 && p.hd != 128) || g.units != (p.n_heads + 2 * p.n_kv) * p.hd || p.n_tok != g.n) return false;
+    // the shapes whose q|k|v product launch_gemm gives the short-prompt kernel
+    const long g64 = (long)((g.units + GM_U - 1) / GM_U) * ((g.n + 63) / 64);
+    if (!(g64 < 256 || (g.units <= 1024 && g64 < 1024))) return false;
+    const int nb = g.W.cols / QB, sp = nb >= GS_SPLIT_MIN_BLOCKS ? 2 : 1;
+    return ((nb + sp - 1) / sp + GS_KB - 1) / GS_KB <= qv_ring(sp);
+}
+
+int launch_gemm_qkv(hipStream_t st, bool f16kv, const GemmArgs &g, const QkPostArgs &p, float *raw) {
+    if (!gemm_qkv_fits(g, p)) return -1;
+    const int nb = g.W.cols / QB, sp = nb >= GS_SPLIT_MIN_BLOCKS ? 2 : 1;
+    const bool full = nb % (GS_KB * sp) == 0;
+    const dim3 grid(p.n_heads + 2 * p.n_kv, (g.n + QV_T - 1) / QV_T), blk(4 * p.hd * sp);
+#define QVK(DT, SP, FL, H)                                                                                         \
+    if (f16kv) hipLaunchKernelGGL((k_gemm_qkv<DT, SP, FL, H, true>), grid, blk, 0, st, g, p, raw);              \
+    else hipLaunchKernelGGL((k_gemm_qkv<DT, SP, FL, H, false>), grid, blk, 0, st, g, p, raw);
+#define QVH(DT, SP, FL) if (p.hd == 128) { QVK(DT, SP, FL, 128) } else { QVK(DT, SP, FL, 64) }
+#define QVD(DT)                                                                                                    \
+    if (sp == 2) { if (full) { QVH(DT, 2, true) } else { QVH(DT, 2, false) } }                                    \
+    else if (full) { QVH(DT, 1, true) } else { QVH(DT, 1, false) }
+    if (g.W.dtype == DT_Q8) { QVD(DT_Q8) } else { QVD(DT_Q4) }
+#undef QVD
+#undef QVH
+#undef QVK
     return 0;
 }
 

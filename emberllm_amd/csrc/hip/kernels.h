@@ -168,6 +168,14 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a);
 // where gemm_swiglu_fits() is false.
 bool gemm_swiglu_fits(const GemmArgs &a);
 int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a);
+// The q|k|v product of a short prompt with launch_qkpost's work (bias, then
+// QK-norm and RoPE of the q and k heads, q written back into p.qkv, k and v
+// stored to the cache) in the epilogue: one head vector per workgroup.  g is
+// the product (units = (n_heads + 2 n_kv) hd, out unused); raw, when set,
+// receives the product with its bias ([n][p.stride]).  Returns -1 where
+// gemm_qkv_fits() is false.
+bool gemm_qkv_fits(const GemmArgs &g, const QkPostArgs &p);
+int launch_gemm_qkv(hipStream_t st, bool f16kv, const GemmArgs &g, const QkPostArgs &p, float *raw);
 
 // ---------------------------------------------------------------- sample --
 // Greedy selection (first maximum) over n logits; writes tokpos[0] = token,

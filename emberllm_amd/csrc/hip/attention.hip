@@ -168,7 +168,6 @@ __global__ __launch_bounds__(WG) void k_pf_scores(AttnArgs a) {
 // lanes hold a block's 32 dims, so its maximum and code sum are 8-lane DPP
 // reductions, with k_quant_rows's arithmetic.
 constexpr int PF_SM_KEYS = 512;    // keys of a pass the one-kernel softmax takes (LDS rows)
-constexpr int PF_FUSE_KEYS = 256;  // keys of a pass up to which it also takes P.V
 template <int HD, int GM, bool F16, bool FUSE>
 __global__ __launch_bounds__(WG) void k_pf_softmax(AttnArgs a) {
     constexpr int QT = 4, KP = HD + 4, NR = QT * GM, SP = PF_SM_KEYS + 4;
@@ -944,10 +943,358 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
     }
 }
 
-int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a) {
+// --------------------------------------------------------------------------
+// k_pf_flash16: the same attention with every fp32 product carried by fp16
+// matrix cores (v_mfma_f32_16x16x32_f16, eight times the fp32 products' work
+// in half their cycles).  Each fp32 operand x is scaled by a power of two so
+// that its group's largest magnitude lies in [2^14, 2^15), then split as
+// hi = fp16(x), lo = fp16(x - hi) (|x - hi - lo| <= 2^-22 |x|); a product is
+// lo.hi + hi.lo + hi.hi, the dropped lo.lo term below 2^-22 of it.  Products
+// and sums are fp32 in the matrix cores, and the power-of-two scales are
+// removed exactly (ldexp), so the scores and outputs carry about four times
+// the fp32 rounding of k_pf_flash.  Scales: one per Q row (its four lanes'
+// maximum), one per K row and per V row (the eight staging lanes of the
+// row's key pair); the probabilities p <= 1 of a tile are multiplied by
+// 2^(14 + E - e_v) with E the smallest V-row exponent of the tile, so the
+// output accumulator holds 2^(14 + E) sum p v and is rescaled by 2^(E - E')
+// with the running softmax when E changes.  An fp16 cache needs neither the
+// K/V scales nor lo planes: its values are fp16 already.
+//
+// Layout per 64-key tile:
+//   K planes ksm[plane][row][dim], key 32t + 8a + 4b + r at row
+//   32t + 16b + 4a + r (fl_krow), so score product kk = 2t + b reads 16
+//   consecutive rows and lane quarter q receives keys 32t + 8q + 4b + r:
+//   eight consecutive keys per lane and 32-key half tile;
+//   V^T planes vsm[plane][dim][key]: the P.V product over keys
+//   32t + 8q .. +7 (lane quarter q, element 4b + r) reads them as one
+//   16-byte row piece, and the lane's own probabilities are its B operand.
+// Staging: wave w takes key pairs 8w .. 8w + 7, lane l key pair
+// 8w + (l & 7) and dim quads (l >> 3) + 8c; a row's maximum is a reduction
+// over the eight lanes of its pair.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ int fl_krow(int k) {
+    return (k & ~31) | ((k & 4) << 2) | ((k & 24) >> 1) | (k & 3);
+}
+// maximum over lanes i, i ^ 8, i ^ 16, ... (the lanes of one key pair)
+__device__ __forceinline__ float fl_pair_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false)));   // row_ror:8
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// power-of-two exponent that brings a group maximum m into [2^14, 2^15)
+__device__ __forceinline__ int fl_exp(float m) { return 15 - __builtin_amdgcn_frexp_expf(m); }
+__device__ __forceinline__ uint32_t fl_pack(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+template <int HD, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
+    constexpr int NP = F16 ? 1 : 2;     // planes: hi, and lo for an fp32 cache
+    constexpr int NQ = HD / 32;         // 32-dim steps of a score product
+    constexpr int ND = HD / 16;         // 16-dim output products
+    constexpr int NC = HD / 32;         // dim quads per staging lane and key
+    constexpr int KPH = HD + 8;         // K plane pitch (halves): 16 rows' 16-byte reads on distinct banks
+    constexpr int VPH = FL_BK + 8;      // V^T plane pitch (halves)
+    static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64, "tile shape");
+    __shared__ __align__(16) _Float16 ksm[NP][FL_BK * KPH];
+    __shared__ __align__(16) _Float16 vsm[NP][HD * VPH];
+    __shared__ __align__(16) int kex[FL_BK], vex[FL_BK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 15, q = lane >> 4;
+    const int g = blockIdx.x;
+    const int G = a.n_heads / a.n_kv, nrows = a.n_tok * G;
+    const int r0 = (gridDim.y - 1 - blockIdx.y) * FL_BR;
+    const int R = min(r0 + wave * 16 + i, nrows - 1);   // this lane's row (padding rows repeat the last)
+    const int b = R / G, h = R % G;
+    const int pos = a.pos_base + b;                       // keys [0, pos] are visible to the row
+    const int kend = a.pos_base + (min(r0 + FL_BR, nrows) - 1) / G;   // the workgroup's last visible key
+    const size_t hoff = (size_t)g * HD;
+
+    // the Q row: lane quarter q holds dims 32s + 8q .. + 7 of step s
+    f16x8 qh[NQ], ql[NQ];
+    int eq;
+    {
+        const float *qr = a.q + (size_t)b * a.q_stride + (size_t)(g * G + h) * HD + 8 * q;
+        f32x4 qv[NQ][2];
+        float mx = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NQ; s++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                qv[s][u] = *reinterpret_cast<const f32x4 *>(qr + 32 * s + 4 * u);
+#pragma unroll
+                for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(qv[s][u][e]));
+            }
+        eq = fl_exp(fl_quarter_max(mx));
+#pragma unroll
+        for (int s = 0; s < NQ; s++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = __builtin_amdgcn_ldexpf(qv[s][e >> 2][e & 3], eq);
+                qh[s][e] = (_Float16)x;
+                ql[s][e] = (_Float16)(x - (float)qh[s][e]);
+            }
+    }
+    const float sscale = a.inv_sqrt * 1.4426950408889634f;
+    float m = -INFINITY, lsum = 0.0f;
+    int ecur = 0;   // the accumulator holds 2^(14 + ecur) * sum p v
+    f32x4 o[ND];
+#pragma unroll
+    for (int d = 0; d < ND; d++) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int kp = 8 * wave + (lane & 7), dq0 = lane >> 3;
+
+    const int nkt = kend / FL_BK + 1;
+    for (int kt = 0; kt < nkt; kt++) {
+        const int k0 = kt * FL_BK;
+        __syncthreads();   // the previous tile has been read
+        // ---- stage: keys 2kp, 2kp + 1 (past kend: row kend), dim quads dq0 + 8c
+        if constexpr (F16) {
+            uint2 kr[2][NC], vr[2][NC];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const size_t off = (size_t)min(k0 + 2 * kp + j, kend) * a.kv_dim + hoff + 4 * (dq0 + 8 * c);
+                    kr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
+                    vr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
+                }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int c = 0; c < NC; c++)
+                    *reinterpret_cast<uint2 *>(&ksm[0][fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c)]) = kr[j][c];
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const int d0 = 4 * (dq0 + 8 * c);
+                uint32_t *vp = reinterpret_cast<uint32_t *>(&vsm[0][d0 * VPH + 2 * kp]);
+                vp[0] = (vr[0][c].x & 0xffffu) | (vr[1][c].x << 16);
+                vp[VPH / 2] = (vr[0][c].x >> 16) | (vr[1][c].x & 0xffff0000u);
+                vp[VPH] = (vr[0][c].y & 0xffffu) | (vr[1][c].y << 16);
+                vp[3 * VPH / 2] = (vr[0][c].y >> 16) | (vr[1][c].y & 0xffff0000u);
+            }
+        } else {
+            f32x4 kr[2][NC], vr[2][NC];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const size_t off = (size_t)min(k0 + 2 * kp + j, kend) * a.kv_dim + hoff + 4 * (dq0 + 8 * c);
+                    kr[j][c] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.kc) + off);
+                    vr[j][c] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.vc) + off);
+                }
+            int ek[2], ev[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                float km = 0.0f, vm = 0.0f;
+#pragma unroll
+                for (int c = 0; c < NC; c++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        km = fmaxf(km, fabsf(kr[j][c][e]));
+                        vm = fmaxf(vm, fabsf(vr[j][c][e]));
+                    }
+                ek[j] = fl_exp(fl_pair_max(km));
+                ev[j] = fl_exp(fl_pair_max(vm));
+            }
+            if (dq0 == 0) {
+                kex[2 * kp] = ek[0]; kex[2 * kp + 1] = ek[1];
+                vex[2 * kp] = ev[0]; vex[2 * kp + 1] = ev[1];
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    _Float16 hi[4], lo[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x = __builtin_amdgcn_ldexpf(kr[j][c][e], ek[j]);
+                        hi[e] = (_Float16)x;
+                        lo[e] = (_Float16)(x - (float)hi[e]);
+                    }
+                    const int at = fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c);
+                    *reinterpret_cast<uint2 *>(&ksm[0][at]) = make_uint2(fl_pack(hi[0], hi[1]), fl_pack(hi[2], hi[3]));
+                    *reinterpret_cast<uint2 *>(&ksm[1][at]) = make_uint2(fl_pack(lo[0], lo[1]), fl_pack(lo[2], lo[3]));
+                }
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float x0 = __builtin_amdgcn_ldexpf(vr[0][c][e], ev[0]);
+                    const float x1 = __builtin_amdgcn_ldexpf(vr[1][c][e], ev[1]);
+                    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                    const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+                    const int at = (4 * (dq0 + 8 * c) + e) * VPH + 2 * kp;
+                    *reinterpret_cast<uint32_t *>(&vsm[0][at]) = fl_pack(h0, h1);
+                    *reinterpret_cast<uint32_t *>(&vsm[1][at]) = fl_pack(l0, l1);
+                }
+        }
+        __syncthreads();
+
+        // ---- S'^T: sc[2t + b][r] = S'[row i][key k0 + 32t + 8q + 4b + r]
+        f32x4 sc[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) sc[kk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < NQ; s++) {
+            f16x8 kh[4], kl[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                kh[kk] = *reinterpret_cast<const f16x8 *>(&ksm[0][(16 * kk + i) * KPH + 32 * s + 8 * q]);
+                if constexpr (!F16) kl[kk] = *reinterpret_cast<const f16x8 *>(&ksm[NP - 1][(16 * kk + i) * KPH + 32 * s + 8 * q]);
+            }
+            if constexpr (!F16) {
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[kk], qh[s], sc[kk], 0, 0, 0);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[kk], ql[s], sc[kk], 0, 0, 0);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[kk], qh[s], sc[kk], 0, 0, 0);
+        }
+        // the per-key exponents of this lane's 16 keys
+        int kx[2][8], vx[2][8];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                if constexpr (F16) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) kx[t][4 * u + e] = vx[t][4 * u + e] = 0;
+                } else {
+                    const int4 ka = *reinterpret_cast<const int4 *>(&kex[32 * t + 8 * q + 4 * u]);
+                    const int4 va = *reinterpret_cast<const int4 *>(&vex[32 * t + 8 * q + 4 * u]);
+                    kx[t][4 * u] = ka.x; kx[t][4 * u + 1] = ka.y; kx[t][4 * u + 2] = ka.z; kx[t][4 * u + 3] = ka.w;
+                    vx[t][4 * u] = va.x; vx[t][4 * u + 1] = va.y; vx[t][4 * u + 2] = va.z; vx[t][4 * u + 3] = va.w;
+                }
+            }
+        // running softmax of the row (log2 units); keys past the row's position are masked
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = kk >> 1, jj = 4 * (kk & 1) + r;
+                const int key = k0 + 32 * t + 8 * q + jj;
+                const float v = key <= pos ? __builtin_amdgcn_ldexpf(sc[kk][r], -(eq + kx[t][jj])) * sscale : -INFINITY;
+                sc[kk][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        const float mn = fmaxf(m, fl_quarter_max(mx));   // finite: key 0 is in the first tile
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first tile (m = -inf)
+        m = mn;
+        lsum *= alpha;
+        // the tile's smallest V-row exponent (keys <-> lanes)
+        const int emin = F16 ? 0 : -(int)wave_max(-(float)vex[lane]);
+        const float of = __builtin_amdgcn_ldexpf(alpha, emin - ecur);
+        ecur = emin;
+#pragma unroll
+        for (int d = 0; d < ND; d++) o[d] *= of;
+        f16x8 ph[2], pl[2];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = kk >> 1, jj = 4 * (kk & 1) + r;
+                const float p = __builtin_amdgcn_exp2f(sc[kk][r] - mn);   // masked: 2^-inf = 0
+                lsum += p;
+                const float x = __builtin_amdgcn_ldexpf(p, 14 + emin - vx[t][jj]);
+                ph[t][jj] = (_Float16)x;
+                pl[t][jj] = (_Float16)(x - (float)ph[t][jj]);
+            }
+        // ---- O''^T += V'^T . P''^T over keys 32t + 8q + jj
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            f16x8 vh[ND], vl[ND];
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                vh[d] = *reinterpret_cast<const f16x8 *>(&vsm[0][(16 * d + i) * VPH + 32 * t + 8 * q]);
+                if constexpr (!F16) vl[d] = *reinterpret_cast<const f16x8 *>(&vsm[NP - 1][(16 * d + i) * VPH + 32 * t + 8 * q]);
+            }
+            if constexpr (!F16) {
+#pragma unroll
+                for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[d], ph[t], o[d], 0, 0, 0);
+            }
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[d], pl[t], o[d], 0, 0, 0);
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[d], ph[t], o[d], 0, 0, 0);
+        }
+    }
+    // o[d][r] = 2^(14 + ecur) O^T[dim 16d + 4q + r][row i]
+    const float inv = 1.0f / fl_quarter_sum(lsum);
+    const int un = -(14 + ecur);
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[d][r] = __builtin_amdgcn_ldexpf(o[d][r], un) * inv;
+    const bool live = r0 + wave * 16 + i < nrows;
+    const size_t col = (size_t)(g * G + h) * HD + 4 * q;
+    const size_t row = (size_t)b * a.n_heads * HD;
+    if (live) {
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+            *reinterpret_cast<float4 *>(a.out + row + col + 16 * d) = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+    }
+    if (!a.qx) return;
+    // the output's Q8_0 blocks for wo, with k_quant_rows's arithmetic: block
+    // bk (dims 32bk ..) is o[2bk], o[2bk + 1] of the row's four lanes
+    const int nbk = a.n_heads * HD / QB;
+#pragma unroll
+    for (int bk = 0; bk < ND / 2; bk++) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, fabsf(o[2 * bk + u][r]));
+        mx = fl_quarter_max(mx);
+        const float dsc = mx / 127.0f;
+        const float id = dsc > 0.0f ? 1.0f / dsc : 0.0f;
+        int cs = 0;
+        uint32_t pk[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            pk[u] = 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int cq = (int)fminf(fmaxf(roundf(o[2 * bk + u][r] * id), -127.0f), 127.0f);
+                cs += cq;
+                pk[u] |= ((uint32_t)cq & 0xffu) << (8 * r);
+            }
+        }
+        cs = (int)fl_quarter_sum((float)cs);   // exact: |sum| <= 32 * 127
+        if (live) {
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+                *reinterpret_cast<uint32_t *>(a.qx + row + col + 16 * (2 * bk + u)) = pk[u];
+            if (q == 0) {
+                const size_t blk = (size_t)b * nbk + ((size_t)(g * G + h) * HD) / QB + bk;
+                a.qdx[blk] = h2f(f2h(dsc));
+                a.qxs[blk] = cs;
+            }
+        }
+    }
+}
+
+int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized) {
+    if (quantized) *quantized = false;
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || a.q_stride % 4) return -1;
+    if (a.qx && (!a.qdx || !a.qxs)) return -1;
     const int G = a.n_heads / a.n_kv;
     const dim3 grid(a.n_kv, (a.n_tok * G + FL_BR - 1) / FL_BR);
+    if (a.hd == 64 || a.hd == 128) {
+        if (quantized) *quantized = a.qx != nullptr;
+        if (a.hd == 64) {
+            if (f16kv) hipLaunchKernelGGL((k_pf_flash16<64, true>), grid, dim3(WG), 0, st, a);
+            else hipLaunchKernelGGL((k_pf_flash16<64, false>), grid, dim3(WG), 0, st, a);
+        } else {
+            if (f16kv) hipLaunchKernelGGL((k_pf_flash16<128, true>), grid, dim3(WG), 0, st, a);
+            else hipLaunchKernelGGL((k_pf_flash16<128, false>), grid, dim3(WG), 0, st, a);
+        }
+        return 0;
+    }
     switch (a.hd) {
 #define FLL(H)                                                                                  \
     case H:                                                                                     \

@@ -355,11 +355,20 @@ extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *
 // ---------------------------------------------------------------- state ----
 constexpr int PF_CHUNK = 2048;  // prefill tokens per pass through the layers (at most)
 constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores per pass (at most)
-// Prefill passes whose keys (start + tokens) fit in this many positions keep
-// the reference's summation order in the attention: there it costs little,
-// and the small models then match the reference's deterministic build to
-// rounding.  Longer passes run the attention on matrix cores.
+// Prefill attention in the reference's summation order (the exact-order
+// kernels) or on matrix cores (a running softmax over fp16 products of split
+// operands).  A model whose every product has fewer than GEMM_SPLIT_MIN_K
+// inputs keeps one sequential block sum per output in the prefill GEMMs, so
+// with exact-order attention its prefill matches the reference's
+// deterministic build to rounding: its passes of up to PF_EXACT_KEYS keys
+// use the exact-order kernels.  Wider models split their longer block sums
+// over pipelines (and sum decode products across lanes), so they run at the
+// reference builds' own noise floor in any case: their attention uses the
+// one-kernel exact form where it is the faster (passes of up to
+// PF_FUSE_KEYS keys over at least PF_FUSE_MIN_WG workgroups) and matrix
+// cores otherwise.
 constexpr int PF_EXACT_KEYS = 512;
+constexpr int PF_FUSE_MIN_WG = 256;
 constexpr int PF_GRAPHS = 8;   // prefill pass graphs kept per state
 enum { PF_AUTO = 0, PF_EXACT = 1, PF_MFMA = 2 };
 
@@ -411,6 +420,7 @@ struct EhipState {
     // the matrix-core kernel with a running softmax beyond (PF_AUTO);
     // EHIP_PF_ATTN=exact or =mfma forces one of them for every pass
     int pf_mode;
+    bool pf_seq;        // every product has fewer than GEMM_SPLIT_MIN_K inputs
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
@@ -580,6 +590,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     const size_t ex_rows = s->pf_mode == PF_EXACT ? pfc : std::min<size_t>(pfc, PF_EXACT_KEYS);
     const size_t ex_ldk = s->pf_mode == PF_EXACT ? ldk_max : (size_t)attn_prefill_ldk(0, std::min(PF_EXACT_KEYS, ctx));
     const int wide = std::max(std::max(c.dim, c.hidden_dim), qd);
+    s->pf_seq = wide < GEMM_SPLIT_MIN_K;
     bool ok = (s->kc = salloc(s, kvb, true)) && (s->vc = salloc(s, kvb, true)) &&
               (s->tokpos_d = (int *)salloc(s, 16, true)) &&
               (s->x = (float *)salloc(s, 4 * (size_t)c.dim)) &&
@@ -1079,12 +1090,16 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             at.out = s->O;
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
             at.ldk = attn_prefill_ldk(pos0, mt);
-            const bool exact = s->pf_mode == PF_EXACT || (s->pf_mode == PF_AUTO && pos0 + mt <= PF_EXACT_KEYS);
-            // the short-pass attention can quantize its own output for wo
-            // (not for F32 weights, whose product reads the fp32 rows)
+            bool exact = s->pf_mode == PF_EXACT;
+            if (s->pf_mode == PF_AUTO)
+                exact = s->pf_seq ? pos0 + mt <= PF_EXACT_KEYS
+                                  : pos0 + mt <= PF_FUSE_KEYS && (long)c.n_kv_heads * ((mt + 3) / 4) >= PF_FUSE_MIN_WG;
+            // the attention can quantize its own output for wo (not for F32
+            // weights, whose product reads the fp32 rows)
             bool quantized = false;
             if (!q.xf) { at.qx = s->qx; at.qdx = s->dxp; at.qxs = s->xsum; }
-            rc |= exact ? launch_attention(s->st, s->f16kv, at, &quantized) : launch_attention_mfma(s->st, s->f16kv, at);
+            rc |= exact ? launch_attention(s->st, s->f16kv, at, &quantized)
+                        : launch_attention_mfma(s->st, s->f16kv, at, &quantized);
             if (psnap(DBG_O, s->O, qd, qd)) return -1;
             if (!quantized) {
                 QuantRowsArgs q2{};

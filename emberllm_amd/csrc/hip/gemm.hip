@@ -1034,7 +1034,7 @@ __global__ __launch_bounds__(64 * (HD / 16) * SPLIT) void k_gemm_qkv(GemmArgs a,
 // keeps the blocks of every output in one sequential sum, and a larger grid
 // keeps 256-thread workgroups (two rounds of split workgroups measured
 // slower: q|k|v 12.7 against 11.1 us, w1|w3 17.8 against 13.2 at 128 tokens)
-constexpr int GS_SPLIT = 4, GS_SPLIT_MIN_BLOCKS = 32, GS_SPLIT_MAX_GRID = 256;
+constexpr int GS_SPLIT = 4, GS_SPLIT_MIN_BLOCKS = GEMM_SPLIT_MIN_K / QB, GS_SPLIT_MAX_GRID = 256;
 // Grids of up to GS_SPLIT2_MAX_GRID workgroups split K in two (512-thread
 // workgroups, two or three per CU): half the serial walk per output for two
 // pipelines' instructions per SIMD.

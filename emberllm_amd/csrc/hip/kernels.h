@@ -89,8 +89,16 @@ struct AttnArgs {
 // prefill: q rows already normed and rotated, k/v already in the cache.
 // *quantized (if non-null) says whether the launch also wrote a.qx/qdx/qxs.
 int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized = nullptr);
-// prefill on fp32 matrix cores with a running softmax (no score scratch)
-int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a);
+// prefill on matrix cores with a running softmax (no score scratch): fp16
+// matrix cores with split operands for head_dim 64 / 128 (which also write
+// a.qx/qdx/qxs when set, reported in *quantized), fp32 ones for 48
+int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized = nullptr);
+// passes whose keys fit in PF_FUSE_KEYS run the whole exact-order attention
+// (and the output's quantization) in one kernel
+constexpr int PF_FUSE_KEYS = 256;
+// products over at least GEMM_SPLIT_MIN_K inputs may split their block sums
+// over pipelines (prefill GEMM); shorter ones keep one sequential sum
+constexpr int GEMM_SPLIT_MIN_K = 1024;
 inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }
 // tile-maximum slots per prefill score row (64-key tiles, padded to 4)
 __host__ __device__ inline int attn_prefill_tiles(int ldk) { return ((ldk + 63) / 64 + 3) & ~3; }

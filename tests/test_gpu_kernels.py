@@ -4,9 +4,11 @@ Every decode kernel (q|k|v matvec with its RMSNorm prologue, QK-norm / RoPE
 / KV store, split-K attention and its merge, wo + residual, w1|w3 + SwiGLU,
 w2 + residual, final norm + lm_head) and every prefill kernel (row
 quantization, the int8 MFMA GEMMs in both tile sizes and the short-prompt
-GEMM, QK post-processing, the prefill attention in both forms: the
-exact-order kernels up to 512 keys (one kernel up to 256) and the fp32
-matrix-core kernel beyond, or forced at pp512) is captured on the GPU and
+GEMM, QK post-processing, the prefill attention in each form: the
+exact-order kernels (one kernel up to 256 keys, scores + P.V up to 512), the
+matrix-core kernel on fp16 products of split operands with its fused Q8_0
+output (fp32 and fp16 caches), and the fp32 matrix-core kernel that head_dim
+48 uses) is captured on the GPU and
 recomputed in float64 from the model file on the GPU's own inputs
 (tests/kernel_check.py, itself pinned against the oracle on the CPU by
 tests/test_kernel_check.py).  Bound: 1e-6 of the sum of |terms| for
@@ -15,8 +17,11 @@ whose rounding an ulp decides.
 
 Workloads (the benchmark configurations): stories110M @128, SmolLM2 @1024,
 Qwen2.5-0.5B @256, Qwen3-0.6B Q8_0 @4096 (both decode-attention schedules),
-Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings and of
-128 / 256 / 200 tokens on the Qwen3 / Qwen2.5 / SmolLM2 shapes; and a
+Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings (and
+with an fp16 cache, and forced to the exact-order kernels), of 128 / 256 /
+200 tokens on the Qwen3 / Qwen2.5 / SmolLM2 shapes (default and exact-order
+attention), of the small variant models with the attention forced onto
+matrix cores; and a
 2-layer Qwen3-width model prefilling 2,300 tokens (one 2048-token pass with
 128-token MFMA tiles, then a 252-token pass at position 2048), also compared
 end to end with the oracle (logits, at the reference builds' own noise floor
@@ -97,14 +102,15 @@ def test_decode_kernels_fp16_cache():
     assert ok, text
 
 
-def _prefill_kernels(name, n_prompt, captures):
+def _prefill_kernels(name, n_prompt, captures, kv16=False, attention_only=False):
     """Prefill n_prompt tokens once per (layer, pass) in `captures`, checking
-    that pass's kernels of that layer."""
+    that pass's kernels of that layer (or only its KV stores and attention:
+    the product checks do not cover F32 weights)."""
     path = configs.model_path(name, threads=16)
     mf = kc.ModelFile(path)
     rng = np.random.default_rng(n_prompt)
     ids = rng.integers(0, mf.V, n_prompt)
-    eng = emberllm.Engine(path, ctx=n_prompt + 8)
+    eng = emberllm.Engine(path, ctx=n_prompt + 8, kv_fp16=kv16)
     lines, ok = [], True
     for layer, pas in captures:
         say(f"prefill kernels {name} n={n_prompt} layer {layer} pass {pas}")
@@ -116,8 +122,15 @@ def _prefill_kernels(name, n_prompt, captures):
             slots.append(rows)
         n = slots[0].shape[0]
         k, v = layer_cache(eng, mf, layer, pos0 + n)
-        rep = kc.Report(f"{name} prefill {n_prompt} pass {pas} (tokens {pos0}..{pos0 + n - 1})")
-        kc.check_prefill_layer(rep, mf, layer, slots, pos0, k, v, False)
+        rep = kc.Report(f"{name} prefill {n_prompt} pass {pas} (tokens {pos0}..{pos0 + n - 1}) kv16={kv16}")
+        if attention_only:
+            pos = pos0 + np.arange(n)
+            qkv = np.asarray(slots[1], dtype=np.float32)
+            kc.check_kv_rows(rep, f"L{layer} kv store", mf, layer, qkv, pos, k, v, kv16)
+            kc.check_attention(rep, f"L{layer} attention", mf, layer, qkv, pos, k[:pos0 + n], v[:pos0 + n],
+                               np.asarray(slots[2], dtype=np.float32))
+        else:
+            kc.check_prefill_layer(rep, mf, layer, slots, pos0, k, v, kv16)
         lines.append(str(rep))
         ok &= rep.ok
     eng.debug_capture_prefill(-1, 0)
@@ -126,35 +139,58 @@ def _prefill_kernels(name, n_prompt, captures):
     return ok, "\n".join(lines)
 
 
-@pytest.mark.parametrize("name", ["qwen3_06b", "qwen3_06b_q4"])
-def test_prefill_kernels_512(name):
+@pytest.mark.parametrize("name,kv16", [("qwen3_06b", False), ("qwen3_06b_q4", False), ("qwen3_06b", True)],
+                         ids=["qwen3_06b", "qwen3_06b_q4", "qwen3_06b-f16kv"])
+def test_prefill_kernels_512(name, kv16):
     """pp512 at the Qwen3-0.6B shape: q|k|v and w1|w3 on the 64-token-tile
-    MFMA GEMM, wo and w2 on the 32x32-tile GEMM, Q8_0 and Q4_0 weights."""
-    ok, text = _prefill_kernels(name, 512, [(0, 0), (27, 0)])
+    MFMA GEMM, wo and w2 on the 32x32-tile GEMM, Q8_0 and Q4_0 weights; the
+    attention on fp16 matrix cores with split operands (fp32 and fp16
+    caches) and its fused Q8_0 output for wo."""
+    ok, text = _prefill_kernels(name, 512, [(0, 0), (27, 0)], kv16)
     assert ok, text
 
 
-@pytest.mark.parametrize("name,n", [("qwen3_06b", 128), ("qwen3_06b_q4", 128), ("qwen25_05b", 256),
-                                    ("smollm2_135m", 200), ("stories110m", 128)],
-                         ids=["qwen3_06b-128", "qwen3_06b_q4-128", "qwen25_05b-256", "smollm2_135m-200",
-                              "stories110m-128"])
-def test_prefill_kernels_short(name, n):
+SHORT = [("qwen3_06b", 128, ""), ("qwen3_06b_q4", 128, ""), ("qwen25_05b", 256, ""), ("smollm2_135m", 200, ""),
+         ("stories110m", 128, ""), ("qwen25_05b", 256, "exact"), ("smollm2_135m", 200, "exact")]
+
+
+@pytest.mark.parametrize("name,n,mode", SHORT, ids=[f"{n}-{k}{'-' + m if m else ''}" for n, k, m in SHORT])
+def test_prefill_kernels_short(name, n, mode, monkeypatch):
     """Short prompts: the one-kernel exact-order attention (scores, softmax,
     P.V and the wo input's Q8_0 blocks; 1, 2, 7 and 3 query heads per kv
-    head, head_dim 128 and 64) and the short-prompt GEMM with 32- and
+    head, head_dim 128 and 64: Qwen2.5's and SmolLM2's short passes have too
+    few workgroups for it and default to the matrix-core kernel, so they are
+    also run with EHIP_PF_ATTN=exact) and the short-prompt GEMM with 32- and
     16-unit tiles, with and without whole stages and the K split, Q8_0 and
     Q4_0 weights."""
+    if mode:
+        monkeypatch.setenv("EHIP_PF_ATTN", mode)
     last = configs.ALL[name]["n_layers"] - 1
     ok, text = _prefill_kernels(name, n, [(0, 0), (last, 0)])
     assert ok, text
 
 
-def test_prefill_kernels_512_matrix_cores(monkeypatch):
-    """pp512 at the Qwen3-0.6B shape with the attention forced onto the fp32
-    matrix-core kernel (EHIP_PF_ATTN=mfma; by default passes of up to 512
-    keys keep the reference's summation order)."""
-    monkeypatch.setenv("EHIP_PF_ATTN", "mfma")
+def test_prefill_kernels_512_exact_order(monkeypatch):
+    """pp512 at the Qwen3-0.6B shape with the attention forced onto the
+    exact-order kernels (EHIP_PF_ATTN=exact: scores and softmax in one kernel,
+    P.V with the head dims split over workgroups), which the small variant
+    models use for every pass of up to 512 keys."""
+    monkeypatch.setenv("EHIP_PF_ATTN", "exact")
     ok, text = _prefill_kernels("qwen3_06b", 512, [(0, 0), (27, 0)])
+    assert ok, text
+
+
+SMALL_MC = [("t_f32", 56), ("t_gqa", 56), ("t_g7", 300)]
+
+
+@pytest.mark.parametrize("name,n", SMALL_MC, ids=[f"{n}-{k}" for n, k in SMALL_MC])
+def test_prefill_kernels_matrix_cores_small(name, n, monkeypatch):
+    """The small variant models with the attention forced onto matrix cores
+    (EHIP_PF_ATTN=mfma; by default they keep the exact-order kernels): the
+    fp32 kernel of head_dim 48 with F32 weights, the split-operand fp16
+    kernel with 3 and 7 query heads per kv head at head_dim 64."""
+    monkeypatch.setenv("EHIP_PF_ATTN", "mfma")
+    ok, text = _prefill_kernels(name, n, [(0, 0), (1, 0)], attention_only=name == "t_f32")
     assert ok, text
 
 

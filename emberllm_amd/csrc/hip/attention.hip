@@ -953,25 +953,31 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
 // and sums are fp32 in the matrix cores, and the power-of-two scales are
 // removed exactly (ldexp), so the scores and outputs carry about four times
 // the fp32 rounding of k_pf_flash.  Scales: one per Q row (its four lanes'
-// maximum), one per K row and per V row (the eight staging lanes of the
-// row's key pair); the probabilities p <= 1 of a tile are multiplied by
-// 2^(14 + E - e_v) with E the smallest V-row exponent of the tile, so the
-// output accumulator holds 2^(14 + E) sum p v and is rescaled by 2^(E - E')
-// with the running softmax when E changes.  An fp16 cache needs neither the
-// K/V scales nor lo planes: its values are fp16 already.
+// maximum), one per K row and per V row; a row's probabilities p <= 1 of a
+// tile are multiplied by 2^(14 + E - e_v) with E the smallest V-row
+// exponent among the keys the row sees in that tile, so the row's output
+// accumulator holds 2^(14 + E) sum p v and is rescaled by 2^(E - E') with
+// the running softmax when E changes.  An fp16 cache needs neither the K/V
+// scales nor lo planes: its values are fp16 already.
 //
-// Layout per 64-key tile:
-//   K planes ksm[plane][row][dim], key 32t + 8a + 4b + r at row
-//   32t + 16b + 4a + r (fl_krow), so score product kk = 2t + b reads 16
-//   consecutive rows and lane quarter q receives keys 32t + 8q + 4b + r:
+// k_pf_kvsplit converts the pass's keys once per layer: per (kv head, 64-key
+// tile) it writes the tile's LDS image (below) to HBM, so every row tile of
+// k_pf_flash16 stages a tile with plain 16-byte copies instead of converting
+// it again (at pp4096 each K/V row was otherwise converted by up to 32
+// workgroups).  The image, per tile:
+//   K planes [plane][row][dim] (pitch HD + 8 halves), key 32t + 8a + 4b + r
+//   at row 32t + 16b + 4a + r (fl_krow), so score product kk = 2t + b reads
+//   16 consecutive rows and lane quarter q receives keys 32t + 8q + 4b + r:
 //   eight consecutive keys per lane and 32-key half tile;
-//   V^T planes vsm[plane][dim][key]: the P.V product over keys
-//   32t + 8q .. +7 (lane quarter q, element 4b + r) reads them as one
-//   16-byte row piece, and the lane's own probabilities are its B operand.
-// Staging: wave w takes key pairs 8w .. 8w + 7, lane l key pair
+//   V^T planes [plane][dim][key] (pitch 72 halves): the P.V product over keys
+//   32t + 8q .. +7 (lane quarter q, element 4b + r) reads them as one 16-byte
+//   row piece, and the lane's own probabilities are its B operand;
+//   the per-key exponents of K and V (fp32 cache).
+// Conversion: wave w takes key pairs 8w .. 8w + 7, lane l key pair
 // 8w + (l & 7) and dim quads (l >> 3) + 8c; a row's maximum is a reduction
-// over the eight lanes of its pair.
+// over the eight lanes of its pair.  Keys past the pass's last repeat it.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16-byte image piece (kept in registers)
 
 __device__ __forceinline__ int fl_krow(int k) {
     return (k & ~31) | ((k & 4) << 2) | ((k & 24) >> 1) | (k & 3);
@@ -990,18 +996,142 @@ __device__ __forceinline__ uint32_t fl_pack(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// geometry of one (kv head, tile) image, in bytes; the LDS holds one image
+template <int HD, bool F16> struct FlImg {
+    static constexpr int NP = F16 ? 1 : 2;                 // planes: hi, and lo for an fp32 cache
+    static constexpr int KPH = HD + 8;                     // K plane pitch (halves): 16 rows' 16-byte reads on distinct banks
+    static constexpr int VPH = FL_BK + 8;                  // V^T plane pitch (halves)
+    static constexpr int KOFF = 0;
+    static constexpr int VOFF = KOFF + NP * FL_BK * KPH * 2;
+    static constexpr int EOFF = VOFF + NP * HD * VPH * 2;  // int kex[64], vex[64] (fp32 cache)
+    static constexpr int BYTES = EOFF + (F16 ? 0 : 2 * FL_BK * 4);
+    static_assert(VOFF % 16 == 0 && EOFF % 16 == 0 && BYTES % 16 == 0, "16-byte pieces");
+};
+
+size_t attn_kvimg_bytes(int hd, bool f16kv, int ctx, int n_kv) {
+    const size_t tiles = (size_t)(ctx + FL_BK - 1) / FL_BK * (size_t)n_kv;
+    switch (hd) {
+        case 64: return tiles * (f16kv ? FlImg<64, true>::BYTES : FlImg<64, false>::BYTES);
+        case 128: return tiles * (f16kv ? FlImg<128, true>::BYTES : FlImg<128, false>::BYTES);
+    }
+    return 0;
+}
+
+// grid (kv heads, tiles of the pass's keys [0, pos_base + n_tok))
+template <int HD, bool F16>
+__global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
+    using I = FlImg<HD, F16>;
+    constexpr int NC = HD / 32;         // dim quads per lane and key
+    constexpr int KPH = I::KPH, VPH = I::VPH;
+    __shared__ __align__(16) uint8_t img[I::BYTES];
+    _Float16 *ksm = reinterpret_cast<_Float16 *>(img + I::KOFF);
+    _Float16 *vsm = reinterpret_cast<_Float16 *>(img + I::VOFF);
+    int *kex = reinterpret_cast<int *>(img + I::EOFF), *vex = kex + FL_BK;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = blockIdx.x, kt = blockIdx.y;
+    const int klast = a.pos_base + a.n_tok - 1;
+    const size_t hoff = (size_t)g * HD;
+    const int k0 = kt * FL_BK;
+    const int kp = 8 * wave + (lane & 7), dq0 = lane >> 3;
+    if constexpr (F16) {
+        uint2 kr[2][NC], vr[2][NC];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const size_t off = (size_t)min(k0 + 2 * kp + j, klast) * a.kv_dim + hoff + 4 * (dq0 + 8 * c);
+                kr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
+                vr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
+            }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+                *reinterpret_cast<uint2 *>(&ksm[fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c)]) = kr[j][c];
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int d0 = 4 * (dq0 + 8 * c);
+            uint32_t *vp = reinterpret_cast<uint32_t *>(&vsm[d0 * VPH + 2 * kp]);
+            vp[0] = (vr[0][c].x & 0xffffu) | (vr[1][c].x << 16);
+            vp[VPH / 2] = (vr[0][c].x >> 16) | (vr[1][c].x & 0xffff0000u);
+            vp[VPH] = (vr[0][c].y & 0xffffu) | (vr[1][c].y << 16);
+            vp[3 * VPH / 2] = (vr[0][c].y >> 16) | (vr[1][c].y & 0xffff0000u);
+        }
+    } else {
+        f32x4 kr[2][NC], vr[2][NC];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const size_t off = (size_t)min(k0 + 2 * kp + j, klast) * a.kv_dim + hoff + 4 * (dq0 + 8 * c);
+                kr[j][c] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.kc) + off);
+                vr[j][c] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.vc) + off);
+            }
+        int ek[2], ev[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            float km = 0.0f, vm = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    km = fmaxf(km, fabsf(kr[j][c][e]));
+                    vm = fmaxf(vm, fabsf(vr[j][c][e]));
+                }
+            ek[j] = fl_exp(fl_pair_max(km));
+            ev[j] = fl_exp(fl_pair_max(vm));
+        }
+        if (dq0 == 0) {
+            kex[2 * kp] = ek[0]; kex[2 * kp + 1] = ek[1];
+            vex[2 * kp] = ev[0]; vex[2 * kp + 1] = ev[1];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                _Float16 hi[4], lo[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float x = __builtin_amdgcn_ldexpf(kr[j][c][e], ek[j]);
+                    hi[e] = (_Float16)x;
+                    lo[e] = (_Float16)(x - (float)hi[e]);
+                }
+                const int at = fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c);
+                *reinterpret_cast<uint2 *>(&ksm[at]) = make_uint2(fl_pack(hi[0], hi[1]), fl_pack(hi[2], hi[3]));
+                *reinterpret_cast<uint2 *>(&ksm[FL_BK * KPH + at]) = make_uint2(fl_pack(lo[0], lo[1]), fl_pack(lo[2], lo[3]));
+            }
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x0 = __builtin_amdgcn_ldexpf(vr[0][c][e], ev[0]);
+                const float x1 = __builtin_amdgcn_ldexpf(vr[1][c][e], ev[1]);
+                const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+                const int at = (4 * (dq0 + 8 * c) + e) * VPH + 2 * kp;
+                *reinterpret_cast<uint32_t *>(&vsm[at]) = fl_pack(h0, h1);
+                *reinterpret_cast<uint32_t *>(&vsm[HD * VPH + at]) = fl_pack(l0, l1);
+            }
+    }
+    __syncthreads();
+    // the image to HBM (the padding halves included: a straight copy back)
+    u32x4 *dst = reinterpret_cast<u32x4 *>(a.kvimg + ((size_t)g * a.kvimg_tiles + kt) * I::BYTES);
+    for (int p = tid; p < I::BYTES / 16; p += WG) dst[p] = reinterpret_cast<const u32x4 *>(img)[p];
+}
+
 template <int HD, bool F16>
 __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
-    constexpr int NP = F16 ? 1 : 2;     // planes: hi, and lo for an fp32 cache
+    using I = FlImg<HD, F16>;
+    constexpr int NP = I::NP;
     constexpr int NQ = HD / 32;         // 32-dim steps of a score product
     constexpr int ND = HD / 16;         // 16-dim output products
-    constexpr int NC = HD / 32;         // dim quads per staging lane and key
-    constexpr int KPH = HD + 8;         // K plane pitch (halves): 16 rows' 16-byte reads on distinct banks
-    constexpr int VPH = FL_BK + 8;      // V^T plane pitch (halves)
+    constexpr int KPH = I::KPH, VPH = I::VPH;
+    constexpr int NPC = (I::BYTES / 16 + WG - 1) / WG;   // image pieces per thread
     static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64, "tile shape");
-    __shared__ __align__(16) _Float16 ksm[NP][FL_BK * KPH];
-    __shared__ __align__(16) _Float16 vsm[NP][HD * VPH];
-    __shared__ __align__(16) int kex[FL_BK], vex[FL_BK];
+    __shared__ __align__(16) uint8_t img[I::BYTES];
+    const _Float16 *ksm = reinterpret_cast<const _Float16 *>(img + I::KOFF);
+    const _Float16 *vsm = reinterpret_cast<const _Float16 *>(img + I::VOFF);
+    const int *kex = reinterpret_cast<const int *>(img + I::EOFF), *vex = kex + FL_BK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = lane & 15, q = lane >> 4;
     const int g = blockIdx.x;
@@ -1011,7 +1141,6 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     const int b = R / G, h = R % G;
     const int pos = a.pos_base + b;                       // keys [0, pos] are visible to the row
     const int kend = a.pos_base + (min(r0 + FL_BR, nrows) - 1) / G;   // the workgroup's last visible key
-    const size_t hoff = (size_t)g * HD;
 
     // the Q row: lane quarter q holds dims 32s + 8q .. + 7 of step s
     f16x8 qh[NQ], ql[NQ];
@@ -1040,98 +1169,26 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     }
     const float sscale = a.inv_sqrt * 1.4426950408889634f;
     float m = -INFINITY, lsum = 0.0f;
-    int ecur = 0;   // the accumulator holds 2^(14 + ecur) * sum p v
+    int ecur = 0;   // the row's accumulator holds 2^(14 + ecur) * sum p v
     f32x4 o[ND];
 #pragma unroll
     for (int d = 0; d < ND; d++) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int kp = 8 * wave + (lane & 7), dq0 = lane >> 3;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.kvimg + (size_t)g * a.kvimg_tiles * I::BYTES);
 
     const int nkt = kend / FL_BK + 1;
     for (int kt = 0; kt < nkt; kt++) {
         const int k0 = kt * FL_BK;
-        __syncthreads();   // the previous tile has been read
-        // ---- stage: keys 2kp, 2kp + 1 (past kend: row kend), dim quads dq0 + 8c
-        if constexpr (F16) {
-            uint2 kr[2][NC], vr[2][NC];
+        {   // the tile's image: loads first, then the LDS stores
+            u32x4 pc[NPC];
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int u = 0; u < NPC; u++) pc[u] = src[min(tid + u * WG, I::BYTES / 16 - 1)];
+            src += I::BYTES / 16;
+            __syncthreads();   // the previous tile has been read
 #pragma unroll
-                for (int c = 0; c < NC; c++) {
-                    const size_t off = (size_t)min(k0 + 2 * kp + j, kend) * a.kv_dim + hoff + 4 * (dq0 + 8 * c);
-                    kr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
-                    vr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
-                }
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int c = 0; c < NC; c++)
-                    *reinterpret_cast<uint2 *>(&ksm[0][fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c)]) = kr[j][c];
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const int d0 = 4 * (dq0 + 8 * c);
-                uint32_t *vp = reinterpret_cast<uint32_t *>(&vsm[0][d0 * VPH + 2 * kp]);
-                vp[0] = (vr[0][c].x & 0xffffu) | (vr[1][c].x << 16);
-                vp[VPH / 2] = (vr[0][c].x >> 16) | (vr[1][c].x & 0xffff0000u);
-                vp[VPH] = (vr[0][c].y & 0xffffu) | (vr[1][c].y << 16);
-                vp[3 * VPH / 2] = (vr[0][c].y >> 16) | (vr[1][c].y & 0xffff0000u);
-            }
-        } else {
-            f32x4 kr[2][NC], vr[2][NC];
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int c = 0; c < NC; c++) {
-                    const size_t off = (size_t)min(k0 + 2 * kp + j, kend) * a.kv_dim + hoff + 4 * (dq0 + 8 * c);
-                    kr[j][c] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.kc) + off);
-                    vr[j][c] = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.vc) + off);
-                }
-            int ek[2], ev[2];
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                float km = 0.0f, vm = 0.0f;
-#pragma unroll
-                for (int c = 0; c < NC; c++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        km = fmaxf(km, fabsf(kr[j][c][e]));
-                        vm = fmaxf(vm, fabsf(vr[j][c][e]));
-                    }
-                ek[j] = fl_exp(fl_pair_max(km));
-                ev[j] = fl_exp(fl_pair_max(vm));
-            }
-            if (dq0 == 0) {
-                kex[2 * kp] = ek[0]; kex[2 * kp + 1] = ek[1];
-                vex[2 * kp] = ev[0]; vex[2 * kp + 1] = ev[1];
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int c = 0; c < NC; c++) {
-                    _Float16 hi[4], lo[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const float x = __builtin_amdgcn_ldexpf(kr[j][c][e], ek[j]);
-                        hi[e] = (_Float16)x;
-                        lo[e] = (_Float16)(x - (float)hi[e]);
-                    }
-                    const int at = fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c);
-                    *reinterpret_cast<uint2 *>(&ksm[0][at]) = make_uint2(fl_pack(hi[0], hi[1]), fl_pack(hi[2], hi[3]));
-                    *reinterpret_cast<uint2 *>(&ksm[1][at]) = make_uint2(fl_pack(lo[0], lo[1]), fl_pack(lo[2], lo[3]));
-                }
-#pragma unroll
-            for (int c = 0; c < NC; c++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float x0 = __builtin_amdgcn_ldexpf(vr[0][c][e], ev[0]);
-                    const float x1 = __builtin_amdgcn_ldexpf(vr[1][c][e], ev[1]);
-                    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-                    const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
-                    const int at = (4 * (dq0 + 8 * c) + e) * VPH + 2 * kp;
-                    *reinterpret_cast<uint32_t *>(&vsm[0][at]) = fl_pack(h0, h1);
-                    *reinterpret_cast<uint32_t *>(&vsm[1][at]) = fl_pack(l0, l1);
-                }
+            for (int u = 0; u < NPC; u++)
+                if (tid + u * WG < I::BYTES / 16) reinterpret_cast<u32x4 *>(img)[tid + u * WG] = pc[u];
+            __syncthreads();
         }
-        __syncthreads();
 
         // ---- S'^T: sc[2t + b][r] = S'[row i][key k0 + 32t + 8q + 4b + r]
         f32x4 sc[4];
@@ -1142,8 +1199,8 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
             f16x8 kh[4], kl[4];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                kh[kk] = *reinterpret_cast<const f16x8 *>(&ksm[0][(16 * kk + i) * KPH + 32 * s + 8 * q]);
-                if constexpr (!F16) kl[kk] = *reinterpret_cast<const f16x8 *>(&ksm[NP - 1][(16 * kk + i) * KPH + 32 * s + 8 * q]);
+                kh[kk] = *reinterpret_cast<const f16x8 *>(&ksm[(16 * kk + i) * KPH + 32 * s + 8 * q]);
+                if constexpr (!F16) kl[kk] = *reinterpret_cast<const f16x8 *>(&ksm[(FL_BK + 16 * kk + i) * KPH + 32 * s + 8 * q]);
             }
             if constexpr (!F16) {
 #pragma unroll
@@ -1172,22 +1229,24 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
             }
         // running softmax of the row (log2 units); keys past the row's position are masked
         float mx = -INFINITY;
+        int el = 1 << 20;   // the smallest V-row exponent among the row's visible keys of the tile
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int t = kk >> 1, jj = 4 * (kk & 1) + r;
-                const int key = k0 + 32 * t + 8 * q + jj;
-                const float v = key <= pos ? __builtin_amdgcn_ldexpf(sc[kk][r], -(eq + kx[t][jj])) * sscale : -INFINITY;
+                const bool vis = k0 + 32 * t + 8 * q + jj <= pos;
+                const float v = vis ? __builtin_amdgcn_ldexpf(sc[kk][r], -(eq + kx[t][jj])) * sscale : -INFINITY;
                 sc[kk][r] = v;
                 mx = fmaxf(mx, v);
+                if (vis) el = min(el, vx[t][jj]);
             }
         const float mn = fmaxf(m, fl_quarter_max(mx));   // finite: key 0 is in the first tile
         const float alpha = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first tile (m = -inf)
         m = mn;
         lsum *= alpha;
-        // the tile's smallest V-row exponent (keys <-> lanes)
-        const int emin = F16 ? 0 : -(int)wave_max(-(float)vex[lane]);
+        int emin = -(int)fl_quarter_max(-(float)el);
+        if (emin == (1 << 20)) emin = ecur;   // no visible key in this tile
         const float of = __builtin_amdgcn_ldexpf(alpha, emin - ecur);
         ecur = emin;
 #pragma unroll
@@ -1210,8 +1269,8 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
             f16x8 vh[ND], vl[ND];
 #pragma unroll
             for (int d = 0; d < ND; d++) {
-                vh[d] = *reinterpret_cast<const f16x8 *>(&vsm[0][(16 * d + i) * VPH + 32 * t + 8 * q]);
-                if constexpr (!F16) vl[d] = *reinterpret_cast<const f16x8 *>(&vsm[NP - 1][(16 * d + i) * VPH + 32 * t + 8 * q]);
+                vh[d] = *reinterpret_cast<const f16x8 *>(&vsm[(16 * d + i) * VPH + 32 * t + 8 * q]);
+                if constexpr (!F16) vl[d] = *reinterpret_cast<const f16x8 *>(&vsm[(HD + 16 * d + i) * VPH + 32 * t + 8 * q]);
             }
             if constexpr (!F16) {
 #pragma unroll
@@ -1285,14 +1344,19 @@ int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *q
     const int G = a.n_heads / a.n_kv;
     const dim3 grid(a.n_kv, (a.n_tok * G + FL_BR - 1) / FL_BR);
     if (a.hd == 64 || a.hd == 128) {
+        const int nkt = (a.pos_base + a.n_tok + FL_BK - 1) / FL_BK;
+        if (!a.kvimg || a.kvimg_tiles < nkt) return -1;
         if (quantized) *quantized = a.qx != nullptr;
+        const dim3 sgrid(a.n_kv, nkt);
+#define FL16(H, F)                                                                         \
+    hipLaunchKernelGGL((k_pf_kvsplit<H, F>), sgrid, dim3(WG), 0, st, a);                  \
+    hipLaunchKernelGGL((k_pf_flash16<H, F>), grid, dim3(WG), 0, st, a);
         if (a.hd == 64) {
-            if (f16kv) hipLaunchKernelGGL((k_pf_flash16<64, true>), grid, dim3(WG), 0, st, a);
-            else hipLaunchKernelGGL((k_pf_flash16<64, false>), grid, dim3(WG), 0, st, a);
+            if (f16kv) { FL16(64, true) } else { FL16(64, false) }
         } else {
-            if (f16kv) hipLaunchKernelGGL((k_pf_flash16<128, true>), grid, dim3(WG), 0, st, a);
-            else hipLaunchKernelGGL((k_pf_flash16<128, false>), grid, dim3(WG), 0, st, a);
+            if (f16kv) { FL16(128, true) } else { FL16(128, false) }
         }
+#undef FL16
         return 0;
     }
     switch (a.hd) {

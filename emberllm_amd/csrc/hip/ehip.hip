@@ -414,6 +414,8 @@ struct EhipState {
     // prefill attention scratch: scores [n_heads][pf_chunk][ldk], tile maxima
     // [n_heads][pf_chunk][attn_prefill_tiles(ldk)], row max and 1/sum [n_heads][pf_chunk]
     float *pf_scores, *pf_tmax, *pf_rowmax, *pf_rowinv;
+    uint8_t *pf_kvimg;  // K/V tile images of the matrix-core prefill attention
+    int pf_kvimg_tiles;
     int pf_chunk;       // tokens per prefill pass
     // prefill attention: the reference's summation order (three kernels and
     // the score scratch above) for passes whose keys fit in PF_EXACT_KEYS,
@@ -626,6 +628,10 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->smp_wcum = (float *)salloc(s, 4 * (size_t)c.vocab_size)) &&
               (s->smp_wk = (unsigned long long *)salloc(s, 8 * 2 * (size_t)sample_wide_pad(c.vocab_size)));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
+    if (ok && s->pf_mode != PF_EXACT && attn_kvimg_bytes(hd, s->f16kv, ctx, c.n_kv_heads) > 0) {
+        s->pf_kvimg_tiles = (ctx + 63) / 64;
+        ok = (s->pf_kvimg = (uint8_t *)salloc(s, attn_kvimg_bytes(hd, s->f16kv, ctx, c.n_kv_heads))) != nullptr;
+    }
     if (ok && s->pf_mode != PF_MFMA)
         ok = (s->pf_scores = (float *)salloc(s, 4 * ex_rows * ex_ldk * c.n_heads)) &&
              (s->pf_rowinv = (float *)salloc(s, 4 * ex_rows * c.n_heads)) &&
@@ -1089,6 +1095,7 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             at.q = s->QKV; at.q_stride = stride; at.pos_base = pos0; at.n_tok = mt;
             at.out = s->O;
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
+            at.kvimg = s->pf_kvimg; at.kvimg_tiles = s->pf_kvimg_tiles;
             at.ldk = attn_prefill_ldk(pos0, mt);
             bool exact = s->pf_mode == PF_EXACT;
             if (s->pf_mode == PF_AUTO)

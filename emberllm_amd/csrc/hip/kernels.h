@@ -85,6 +85,10 @@ struct AttnArgs {
     // and code sums ([n_tok][n_heads*hd / 32]), as the quantization kernel
     // would make them from `out`; written when the launch reports it
     int8_t *qx; float *qdx; int *qxs;
+    // prefill on matrix cores (head_dim 64 / 128): the pass's K/V converted
+    // once into per-(kv head, 64-key tile) images, kvimg_tiles tiles per head
+    // (attn_kvimg_bytes)
+    uint8_t *kvimg; int kvimg_tiles;
 };
 // prefill: q rows already normed and rotated, k/v already in the cache.
 // *quantized (if non-null) says whether the launch also wrote a.qx/qdx/qxs.
@@ -93,6 +97,9 @@ int launch_attention(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quanti
 // matrix cores with split operands for head_dim 64 / 128 (which also write
 // a.qx/qdx/qxs when set, reported in *quantized), fp32 ones for 48
 int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized = nullptr);
+// bytes of the K/V tile images the matrix-core prefill attention needs for
+// ctx positions (0: head_dim without images)
+size_t attn_kvimg_bytes(int hd, bool f16kv, int ctx, int n_kv);
 // passes whose keys fit in PF_FUSE_KEYS run the whole exact-order attention
 // (and the output's quantization) in one kernel
 constexpr int PF_FUSE_KEYS = 256;

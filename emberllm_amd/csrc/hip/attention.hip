@@ -996,7 +996,10 @@ __device__ __forceinline__ uint32_t fl_pack(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// geometry of one (kv head, tile) image, in bytes; the LDS holds one image
+// geometry of one (kv head, tile) image, in bytes.  The LDS layout pads the
+// plane rows (bank spread); the HBM image is the same data without the
+// padding, moved in 16-byte pieces: piece p of the HBM image lands at LDS
+// byte lds_at(p).
 template <int HD, bool F16> struct FlImg {
     static constexpr int NP = F16 ? 1 : 2;                 // planes: hi, and lo for an fp32 cache
     static constexpr int KPH = HD + 8;                     // K plane pitch (halves): 16 rows' 16-byte reads on distinct banks
@@ -1004,15 +1007,30 @@ template <int HD, bool F16> struct FlImg {
     static constexpr int KOFF = 0;
     static constexpr int VOFF = KOFF + NP * FL_BK * KPH * 2;
     static constexpr int EOFF = VOFF + NP * HD * VPH * 2;  // int kex[64], vex[64] (fp32 cache)
-    static constexpr int BYTES = EOFF + (F16 ? 0 : 2 * FL_BK * 4);
+    static constexpr int BYTES = EOFF + (F16 ? 0 : 2 * FL_BK * 4);     // LDS bytes
+    static constexpr int KP = NP * FL_BK * HD / 8;         // HBM pieces: K planes
+    static constexpr int VP = NP * HD * FL_BK / 8;         //             V^T planes
+    static constexpr int PIECES = KP + VP + (F16 ? 0 : 2 * FL_BK / 4);
+    static constexpr int HBYTES = 16 * PIECES;             // HBM bytes per image
     static_assert(VOFF % 16 == 0 && EOFF % 16 == 0 && BYTES % 16 == 0, "16-byte pieces");
+    static __device__ __forceinline__ int lds_at(int p) {
+        if (p < KP) {   // K plane p / (64 HD/8), row (p / (HD/8)) % 64, piece p % (HD/8)
+            constexpr int RP = HD / 8;
+            return KOFF + 2 * KPH * (p / RP) + 16 * (p % RP);
+        }
+        if (p < KP + VP) {   // V^T plane, row, piece of 8 keys
+            const int v = p - KP;
+            return VOFF + 2 * VPH * (v / 8) + 16 * (v % 8);
+        }
+        return EOFF + 16 * (p - KP - VP);
+    }
 };
 
 size_t attn_kvimg_bytes(int hd, bool f16kv, int ctx, int n_kv) {
     const size_t tiles = (size_t)(ctx + FL_BK - 1) / FL_BK * (size_t)n_kv;
     switch (hd) {
-        case 64: return tiles * (f16kv ? FlImg<64, true>::BYTES : FlImg<64, false>::BYTES);
-        case 128: return tiles * (f16kv ? FlImg<128, true>::BYTES : FlImg<128, false>::BYTES);
+        case 64: return tiles * (f16kv ? FlImg<64, true>::HBYTES : FlImg<64, false>::HBYTES);
+        case 128: return tiles * (f16kv ? FlImg<128, true>::HBYTES : FlImg<128, false>::HBYTES);
     }
     return 0;
 }
@@ -1114,11 +1132,13 @@ __global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
             }
     }
     __syncthreads();
-    // the image to HBM (the padding halves included: a straight copy back)
-    u32x4 *dst = reinterpret_cast<u32x4 *>(a.kvimg + ((size_t)g * a.kvimg_tiles + kt) * I::BYTES);
-    for (int p = tid; p < I::BYTES / 16; p += WG) dst[p] = reinterpret_cast<const u32x4 *>(img)[p];
+    // the image to HBM without the rows' padding
+    u32x4 *dst = reinterpret_cast<u32x4 *>(a.kvimg + ((size_t)g * a.kvimg_tiles + kt) * I::HBYTES);
+    for (int p = tid; p < I::PIECES; p += WG) dst[p] = *reinterpret_cast<const u32x4 *>(img + I::lds_at(p));
 }
 
+// 64 rows per workgroup, two workgroups per CU: one's staging overlaps the
+// other's products (128 rows per workgroup, one per CU, measured slower)
 template <int HD, bool F16>
 __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     using I = FlImg<HD, F16>;
@@ -1126,7 +1146,8 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     constexpr int NQ = HD / 32;         // 32-dim steps of a score product
     constexpr int ND = HD / 16;         // 16-dim output products
     constexpr int KPH = I::KPH, VPH = I::VPH;
-    constexpr int NPC = (I::BYTES / 16 + WG - 1) / WG;   // image pieces per thread
+    constexpr int NT = WG, BR = FL_BR;                   // threads, rows per workgroup
+    constexpr int NPC = (I::PIECES + NT - 1) / NT;       // image pieces per thread
     static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64, "tile shape");
     __shared__ __align__(16) uint8_t img[I::BYTES];
     const _Float16 *ksm = reinterpret_cast<const _Float16 *>(img + I::KOFF);
@@ -1136,11 +1157,11 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     const int i = lane & 15, q = lane >> 4;
     const int g = blockIdx.x;
     const int G = a.n_heads / a.n_kv, nrows = a.n_tok * G;
-    const int r0 = (gridDim.y - 1 - blockIdx.y) * FL_BR;
+    const int r0 = (gridDim.y - 1 - blockIdx.y) * BR;
     const int R = min(r0 + wave * 16 + i, nrows - 1);   // this lane's row (padding rows repeat the last)
     const int b = R / G, h = R % G;
     const int pos = a.pos_base + b;                       // keys [0, pos] are visible to the row
-    const int kend = a.pos_base + (min(r0 + FL_BR, nrows) - 1) / G;   // the workgroup's last visible key
+    const int kend = a.pos_base + (min(r0 + BR, nrows) - 1) / G;   // the workgroup's last visible key
 
     // the Q row: lane quarter q holds dims 32s + 8q .. + 7 of step s
     f16x8 qh[NQ], ql[NQ];
@@ -1173,7 +1194,7 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     f32x4 o[ND];
 #pragma unroll
     for (int d = 0; d < ND; d++) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.kvimg + (size_t)g * a.kvimg_tiles * I::BYTES);
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.kvimg + (size_t)g * a.kvimg_tiles * I::HBYTES);
 
     const int nkt = kend / FL_BK + 1;
     for (int kt = 0; kt < nkt; kt++) {
@@ -1181,12 +1202,12 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
         {   // the tile's image: loads first, then the LDS stores
             u32x4 pc[NPC];
 #pragma unroll
-            for (int u = 0; u < NPC; u++) pc[u] = src[min(tid + u * WG, I::BYTES / 16 - 1)];
-            src += I::BYTES / 16;
+            for (int u = 0; u < NPC; u++) pc[u] = src[min(tid + u * NT, I::PIECES - 1)];
+            src += I::PIECES;
             __syncthreads();   // the previous tile has been read
 #pragma unroll
             for (int u = 0; u < NPC; u++)
-                if (tid + u * WG < I::BYTES / 16) reinterpret_cast<u32x4 *>(img)[tid + u * WG] = pc[u];
+                if (tid + u * NT < I::PIECES) *reinterpret_cast<u32x4 *>(img + I::lds_at(tid + u * NT)) = pc[u];
             __syncthreads();
         }
 

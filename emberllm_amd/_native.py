@@ -147,6 +147,7 @@ PROTOTYPES = {
                                              ctypes.POINTER(EmberSampler), _IP, _FP]),
     "ehip_time_kernel": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _FP]),
     "ehip_measure_read_bw": (ctypes.c_int, [_P, ctypes.c_uint64, ctypes.c_int, _FP]),
+    "ehip_libm_expf": (None, [_FP, _FP, ctypes.c_long]),
     "ehip_sample_noalloc": (ctypes.c_int, [_P, ctypes.c_int, ctypes.POINTER(EmberSampler), _P, _P, _P, _P, _P]),
     "ehip_noalloc_setup": (ctypes.c_int, []),
     "ehip_quantize_rows": (ctypes.c_int, [ctypes.POINTER(EhipQuantJob), ctypes.c_int]),

@@ -25,6 +25,7 @@
 #include "../../../include/ember.h"
 #include "../../../include/ehip.h"
 #include "kernels.h"
+#include "libm_expf.h"
 #include "staging.h"
 
 using namespace ehip;
@@ -423,6 +424,12 @@ struct EhipState {
     // EHIP_PF_ATTN=exact or =mfma forces one of them for every pass
     int pf_mode;
     bool pf_seq;        // every product has fewer than GEMM_SPLIT_MIN_K inputs
+    // EHIP_ORDER=reference: every decode kernel in the reference's floating-
+    // point order (reforder.hip), prefill as one decode step per token (the
+    // reference's prefill computes exactly its forward steps); att_ref is the
+    // attention's score scratch [n_heads][ctx]
+    bool ref_order;
+    float *att_ref;
     // device greedy loop: argmax partials, counter, generated tokens [ctx]
     float *am_val; int *am_idx; int *gen_tok;
     hipGraph_t graph; hipGraphExec_t gexec;
@@ -508,7 +515,7 @@ static int env_int(const char *name, int dflt) {
 static int xm_probe(EhipState *s) {
     const int nkv = s->m->cfg.n_kv_heads, gx = 8 * s->xm_slots;
     s->xm_on = false;
-    if (!env_int("EHIP_XMERGE", 1)) return 0;
+    if (!env_int("EHIP_XMERGE", 1) || s->ref_order) return 0;
     std::vector<int> h((size_t)gx, -1);
     int *d = nullptr;
     HCHK(hipMalloc(&d, 4 * h.size()), -1);
@@ -593,6 +600,10 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     const size_t ex_ldk = s->pf_mode == PF_EXACT ? ldk_max : (size_t)attn_prefill_ldk(0, std::min(PF_EXACT_KEYS, ctx));
     const int wide = std::max(std::max(c.dim, c.hidden_dim), qd);
     s->pf_seq = wide < GEMM_SPLIT_MIN_K;
+    {
+        const char *ord = getenv("EHIP_ORDER");
+        s->ref_order = ord && !strcmp(ord, "reference");
+    }
     bool ok = (s->kc = salloc(s, kvb, true)) && (s->vc = salloc(s, kvb, true)) &&
               (s->tokpos_d = (int *)salloc(s, 16, true)) &&
               (s->x = (float *)salloc(s, 4 * (size_t)c.dim)) &&
@@ -628,6 +639,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->smp_wcum = (float *)salloc(s, 4 * (size_t)c.vocab_size)) &&
               (s->smp_wk = (unsigned long long *)salloc(s, 8 * 2 * (size_t)sample_wide_pad(c.vocab_size)));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
+    if (ok && s->ref_order) ok = (s->att_ref = (float *)salloc(s, 4 * (size_t)c.n_heads * ctx)) != nullptr;
     if (ok && s->pf_mode != PF_EXACT && attn_kvimg_bytes(hd, s->f16kv, ctx, c.n_kv_heads) > 0) {
         s->pf_kvimg_tiles = (ctx + 63) / 64;
         ok = (s->pf_kvimg = (uint8_t *)salloc(s, attn_kvimg_bytes(hd, s->f16kv, ctx, c.n_kv_heads))) != nullptr;
@@ -691,9 +703,18 @@ static AttnArgs attn_args(EhipState *s, int l) {
     return a;
 }
 
+// a decode-step matvec: the fast kernel, or the reference-order one
+static int mv(EhipState *s, int pro, int epi, const MatvecArgs &a) {
+    return s->ref_order ? launch_matvec_ref(s->st, pro, epi, a) : launch_matvec(s->st, pro, epi, a);
+}
+
 static int enq_attn_decode(EhipState *s, int l, bool with_merge = true) {
     AttnArgs a = attn_args(s, l);
     a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
+    if (s->ref_order) {
+        a.out = s->o;
+        return launch_attn_ref(s->st, s->f16kv, a, s->att_ref);
+    }
     a.part = s->part; a.max_chunks = s->mc_dec;
     if (s->xm_on) {
         const int nkv = s->m->cfg.n_kv_heads;
@@ -716,7 +737,7 @@ static MatvecArgs head_args(EhipState *s, const float *xin) {
 }
 
 static int enq_head(EhipState *s, const float *xin) {
-    return launch_matvec(s->st, PRO_NORM, EPI_STORE, head_args(s, xin));
+    return mv(s, PRO_NORM, EPI_STORE, head_args(s, xin));
 }
 
 static int enq_w13(EhipState *s, int l) {
@@ -725,7 +746,7 @@ static int enq_w13(EhipState *s, int l) {
     MatvecArgs a{};
     a.W = y.w13; a.units = m->cfg.hidden_dim; a.pair_off = m->cfg.hidden_dim;
     a.in = s->x; a.norm_w = y.ffn_norm; a.eps = m->cfg.norm_eps; a.out = s->h;
-    return launch_matvec(s->st, PRO_NORM, EPI_SWIGLU, a);
+    return mv(s, PRO_NORM, EPI_SWIGLU, a);
 }
 
 // The layer launches of one decode step (the tokpos copy is the caller's).
@@ -745,20 +766,20 @@ static int enq_layers(EhipState *s) {
         a.W = y.qkv; a.units = qd + 2 * kvd; a.in = s->x; a.norm_w = y.attn_norm; a.eps = c.norm_eps;
         a.tokpos = s->tokpos_d; a.emb = m->emb; a.x_out = s->x; a.out = s->qkv; a.bias = y.bias_qkv;
         if (l > 0 && snap(l, DBG_XIN, s->x, c.dim)) return -1;
-        if (launch_matvec(s->st, l == 0 ? PRO_EMBED_NORM : PRO_NORM, EPI_STORE, a)) return -1;
+        if (mv(s, l == 0 ? PRO_EMBED_NORM : PRO_NORM, EPI_STORE, a)) return -1;
         if (l == 0 && snap(l, DBG_XIN, s->x, c.dim)) return -1;   // the embedding row it gathered
         if (snap(l, DBG_QKV, s->qkv, qd + 2 * kvd)) return -1;
         if (enq_attn_decode(s, l)) return -1;
         if (snap(l, DBG_O, s->o, qd)) return -1;
         MatvecArgs b{};
         b.W = y.wo; b.units = c.dim; b.in = s->o; b.out = s->x;
-        if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, b)) return -1;
+        if (mv(s, PRO_PLAIN, EPI_RESID, b)) return -1;
         if (snap(l, DBG_XMID, s->x, c.dim)) return -1;
         if (enq_w13(s, l)) return -1;
         if (snap(l, DBG_H, s->h, c.hidden_dim)) return -1;
         MatvecArgs d{};
         d.W = y.w2; d.units = c.dim; d.in = s->h; d.out = s->x;
-        if (launch_matvec(s->st, PRO_PLAIN, EPI_RESID, d)) return -1;
+        if (mv(s, PRO_PLAIN, EPI_RESID, d)) return -1;
         if (snap(l, DBG_XOUT, s->x, c.dim)) return -1;
     }
     return 0;
@@ -829,7 +850,7 @@ static int enq_gen_step(EhipState *s) {
         MatvecArgs a = head_args(s, s->x);
         a.am_val = s->am_val; a.am_idx = s->am_idx;
         a.am_tokpos = s->tokpos_d; a.am_out = s->gen_tok; a.am_cap = s->ctx;
-        if (launch_matvec(s->st, PRO_NORM, EPI_STORE, a)) { set_err("lm_head launch failed"); return -1; }
+        if (mv(s, PRO_NORM, EPI_STORE, a)) { set_err("lm_head launch failed"); return -1; }
         return 0;
     }
     if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
@@ -1009,7 +1030,7 @@ static int generate_sampled_once(EhipState *s, int tok, int pos, int n, EmberSam
     SampleArgs sa = sample_args(s, p, cap, V);
     // the lm_head's per-workgroup winners serve as the sampler's per-part
     // maxima unless penalties change the logits afterwards
-    const bool parts = p.temperature > 0.0f && !sample_penalized(sa) && s->m->head.dtype != DT_F32;
+    const bool parts = p.temperature > 0.0f && !sample_penalized(sa) && s->m->head.dtype != DT_F32 && !s->ref_order;
     auto enq = [&]() -> int {
         if (parts) {
             if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
@@ -1186,6 +1207,11 @@ static hipGraphExec_t prefill_graph(EhipState *s, int pos0, int mt, bool last, i
 }
 
 extern "C" float *ehip_prefill(EhipState *s, const int *ids, int n, int start) {
+    if (s->ref_order) {   // the reference's prefill computes exactly its forward steps
+        for (int i = 0; i < n; i++)
+            if (!ehip_forward(s, ids[i], start + i)) return nullptr;
+        return s->logits_h;
+    }
     for (int c0 = 0; c0 < n; c0 += s->pf_chunk) {
         const int mt = std::min(s->pf_chunk, n - c0), pass = c0 / s->pf_chunk;
         const bool last = c0 + mt == n;
@@ -1356,6 +1382,10 @@ __global__ __launch_bounds__(WG) void k_stream_read(const uint4 *__restrict__ p,
 #pragma unroll
     for (int u = 0; u < SR_UNROLL; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     if (acc == 0u && threadIdx.x == 0) sink[blockIdx.x & 63] = acc + 1u;
+}
+
+extern "C" void ehip_libm_expf(const float *x, float *y, long n) {
+    for (long i = 0; i < n; i++) y[i] = libm_expf(x[i]);
 }
 
 extern "C" int ehip_measure_read_bw(EhipState *s, uint64_t bytes, int reps, float *gbs) {

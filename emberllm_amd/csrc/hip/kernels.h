@@ -40,6 +40,9 @@ int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
 // EPI_STORE with am_val/am_idx set and no merge: returns the number of
 // per-workgroup winners written (the sampler's per-part maxima), or -1.
 int launch_matvec_parts(hipStream_t st, int pro, const MatvecArgs &a);
+// the same products in the reference's order (one thread per output, block
+// sums added block after block; reforder.hip)
+int launch_matvec_ref(hipStream_t st, int pro, int epi, const MatvecArgs &a);
 
 // ------------------------------------------------------------- attention --
 // GQA attention against the cache.  Prefill: causal attention of n_tok query
@@ -114,6 +117,9 @@ __host__ __device__ inline int attn_prefill_tiles(int ldk) { return ((ldk + 63) 
 // Without xm_cnt the merge is a second kernel; with_merge = false leaves it
 // out (measurement).
 int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_merge = true);
+// decode attention in the reference's order (one workgroup per query head,
+// the softmax and P.V sums in position order; att: [n_heads][ctx] scratch)
+int launch_attn_ref(hipStream_t st, bool f16kv, const AttnArgs &a, float *att);
 // workgroups per kv head: two per CU over all kv heads, or more when a chunk
 // would exceed ATT_DEC_CR rows (0: head_dim not supported)
 int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu);

@@ -19,6 +19,7 @@
 #include <utility>
 
 #include "kernels.h"
+#include "libm_expf.h"
 
 namespace ehip {
 
@@ -176,9 +177,10 @@ __device__ __forceinline__ void samp_slice(int n, int &lo, int &hi) {
     hi = min(n, lo + per);
 }
 
-// e of a logit: the reference's division by the temperature, then expf of the
-// difference to the maximum (sample.c:129-134).
-__device__ __forceinline__ float samp_e(float l, float T, float M) { return expf(l / T - M); }
+// e of a logit: the reference's division by the temperature, then its C
+// library's expf of the difference to the maximum (sample.c:129-134;
+// libm_expf.h)
+__device__ __forceinline__ float samp_e(float l, float T, float M) { return libm_expf(l / T - M); }
 
 // (p desc, index asc): the order of the reference's stable sort
 __device__ __forceinline__ bool samp_before(float pa, int ia, float pb, int ib) {
@@ -568,9 +570,8 @@ __global__ __launch_bounds__(WG) void k_samp_fused(SampleArgs a) {
 // hundred thousand candidates the running sums are ~1e-5 apart, so a
 // last-bit difference in the softmax sum would move a draw now and then.
 // Five steps:
-//   k_sw_e      e = exp(l/T - M) for every token, correctly rounded (the
-//               exponential in double precision, rounded once to float: what
-//               the host's expf returns);
+//   k_sw_e      e = expf(l/T - M) for every token, as the reference's C
+//               library computes it (libm_expf.h);
 //   k_sw_sum    one wave: S = the sum of e in index order, one addition at a
 //               time (sample.c:131-133);
 //   k_sw_tile   p = e / S and a 64-bit key per token, ~bits(p) above the
@@ -589,8 +590,8 @@ __global__ __launch_bounds__(WG) void k_samp_fused(SampleArgs a) {
 // The two sequential sums are the part that cannot be parallelized exactly;
 // each costs about one dependent addition per token.
 
-// e of a logit, correctly rounded
-__device__ __forceinline__ float sw_e(float l, float T, float M) { return (float)exp((double)(l / T - M)); }
+// e of a logit (the same expf as samp_e)
+__device__ __forceinline__ float sw_e(float l, float T, float M) { return libm_expf(l / T - M); }
 
 // The sum of the 64 lanes' v in lane order, added to acc one value at a time;
 // lane q receives the running sum through its own value.

@@ -206,6 +206,11 @@ int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms_per_
  * decode roofline fractions are also quoted against, beside the 8 TB/s
  * datasheet figure. */
 int ehip_measure_read_bw(EhipState *s, uint64_t bytes, int reps, float *gb_per_s);
+/* y[i] = expf(x[i]) for i < n, evaluated on the host with the restatement of
+ * the C library's expf that the reference-order kernels (EHIP_ORDER=reference)
+ * run on the device.  No counterpart in the reference: exported so the
+ * restatement can be checked against the host's libm without a GPU. */
+void ehip_libm_expf(const float *x, float *y, long n);
 
 #ifdef __cplusplus
 }

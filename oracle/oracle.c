@@ -742,3 +742,9 @@ int orc_sample(OrcSampler *s, float *logits, int n) {
     orc_sampler_accept(s, pick);
     return pick;
 }
+
+/* The C library's expf over an array: the exponential the reference's softmax
+ * and SwiGLU call (src/model.c:61, 405), for checking restatements of it. */
+void orc_expf_n(const float *x, float *y, long n) {
+    for (long i = 0; i < n; i++) y[i] = expf(x[i]);
+}

@@ -41,6 +41,7 @@ typedef struct {
 
 uint16_t orc_f32_to_f16(float f);
 float    orc_f16_to_f32(uint16_t h);
+void     orc_expf_n(const float *x, float *y, long n);   /* the C library's expf, as model.c:61, 405 call it */
 void     orc_quantize_q8_0(const float *x, void *out, int n);
 void     orc_quantize_q4_0(const float *x, void *out, int n);
 /* out[d_out] = W[d_out, n_in] . x (activation re-quantized to Q8_0 first) */

@@ -37,6 +37,7 @@ class Sampler(ctypes.Structure):
 _ORC = {
     "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "orc_expf_n": (None, [_FP, _FP, ctypes.c_long]),
     "orc_quantize_q8_0": (None, [_FP, _P, ctypes.c_int]),
     "orc_quantize_q4_0": (None, [_FP, _P, ctypes.c_int]),
     "orc_matmul": (None, [_FP, _FP, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int]),

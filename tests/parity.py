@@ -96,3 +96,17 @@ def check_run(results, case_id):
     assert np.median(mab) <= b["abs_med"] and mab.max() <= b["abs_max"], summary
     assert np.mean(ok) >= b["top1"], summary
     return summary
+
+
+def check_strict(results, case_id):
+    """Assert the target bar itself at every step: max-abs <= 1e-2, rel-L2
+    <= 1e-3, and >= 99% top-1 agreement with no near-tie excuse (the runs of
+    the reference-order mode, which sums in the deterministic build's order)."""
+    assert all(r["finite"] for r in results), f"{case_id}: non-finite logits"
+    rel = np.array([r["rel_l2"] for r in results])
+    mab = np.array([r["max_abs"] for r in results])
+    top1 = float(np.mean([r["agree"] for r in results]))
+    summary = (f"{case_id} (reference order): rel-L2 median {np.median(rel):.2e} max {rel.max():.2e}; "
+               f"max-abs median {np.median(mab):.2e} max {mab.max():.2e}; top-1 {top1:.3f} over {len(results)} steps")
+    assert rel.max() <= REL_L2 and mab.max() <= MAX_ABS and top1 >= 0.99, summary
+    return summary

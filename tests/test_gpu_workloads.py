@@ -26,6 +26,11 @@ The device-held loops must also reproduce the C-API loop exactly: the greedy
 loop's tokens equal the argmax of ember_forward's logits, and the device
 sampler's tokens equal ember_sample's (the host sampler, the reference's
 algorithm) on the same logits.
+
+Each workload also runs in the reference-order mode (EHIP_ORDER=reference:
+the decode kernels of reforder.hip, every fp32 operation the reference's in
+its order, prefill as one step per token), held to the target bar itself at
+every step (tests/parity.py check_strict).
 """
 import ctypes
 import sys
@@ -35,7 +40,7 @@ import pytest
 
 import oracle
 from emberllm_amd import _native, configs, emberllm
-from parity import check_run, compare
+from parity import check_run, check_strict, compare
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
@@ -53,14 +58,14 @@ def target_view(res):
             f"{np.median(mab):.2e} (bar 1e-2), top-1 {top:.3f} (bar 0.99)")
 
 
-def _run(name, prompt, steps, sampled=False):
+def _run(name, prompt, steps, sampled=False, reference_order=False):
     path = configs.model_path(name, threads=16)
     V = configs.ALL[name]["vocab_size"]
     rng = np.random.default_rng(prompt * 7 + steps)
     ids = rng.integers(0, V, prompt)
     ctx = prompt + steps + 2
     lib = _native.lib()
-    say(f"{name} pp{prompt} tg{steps} {'sampled' if sampled else 'greedy'}")
+    say(f"{name} pp{prompt} tg{steps} {'sampled' if sampled else 'greedy'}{' reference order' if reference_order else ''}")
     eng = emberllm.Engine(path, ctx=ctx)
     orc = oracle.Oracle(path, ctx=ctx)
     first = eng.prefill(ids)
@@ -98,6 +103,9 @@ def _run(name, prompt, steps, sampled=False):
     same = np.mean(np.asarray(got) == np.asarray(toks))
     say(f"{name}: device loop reproduces the API loop on {same * 100:.1f}% of {steps} tokens")
     assert same == 1.0, (list(got[:20]), toks[:20])
+    if reference_order:
+        say(check_strict(res, f"{name}-pp{prompt}-tg{steps}"))
+        return
     say(target_view(res))
     # bars: the reference's optimized build against its deterministic build
     # over this same protocol (noise_floor.json, make_golden.py workload)
@@ -122,3 +130,14 @@ def test_qwen3_pp128_tg128(oracle_threads):
 
 def test_qwen3_q4_pp512_tg256(oracle_threads):
     _run("qwen3_06b_q4", 512, 256)
+
+
+WORKLOADS = [("stories110m", 128, 128, False), ("smollm2_135m", 1024, 128, False), ("qwen25_05b", 256, 128, True),
+             ("qwen3_06b", 128, 128, False), ("qwen3_06b_q4", 512, 256, False)]
+
+
+@pytest.mark.parametrize("name,prompt,steps,sampled", WORKLOADS,
+                         ids=[f"{n}-pp{p}-tg{t}{'-sampled' if s else ''}" for n, p, t, s in WORKLOADS])
+def test_workload_reference_order(name, prompt, steps, sampled, oracle_threads, monkeypatch):
+    monkeypatch.setenv("EHIP_ORDER", "reference")
+    _run(name, prompt, steps, sampled=sampled, reference_order=True)

@@ -361,3 +361,32 @@ def test_generator_is_deterministic_and_shaped(tmp_path):
     t = L.ember_model_tensor(m, b"layers.0.w2").contents
     assert t.dtype == _native.DT_Q8_0 and list(t.shape)[:2] == [128, 256] and t.offset % 64 == 0
     L.ember_model_free(m)
+
+
+def test_libm_expf_restatement_equals_the_c_library():
+    """The expf the reference-order kernels use (emberllm_amd/csrc/hip/
+    libm_expf.h, evaluated on the host through ehip_libm_expf) equals the
+    host C library's expf, the function the reference's softmax and SwiGLU
+    call (src/model.c:61, 405), bit for bit: every 61st float bit pattern
+    (about 70 million inputs, both signs, every exponent, NaN and the
+    infinities) plus the edges of the special-case ranges."""
+    import oracle
+    lib = _native.lib()
+    olib = oracle.oracle_lib()
+    bits = np.arange(0, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)
+    edges = np.array([0x42b00000, 0xc2b00000, 0x42b17217, 0x42b17218, 0xc2cff1b4, 0xc2cff1b5, 0x7f800000,
+                      0xff800000, 0x7fc00000, 0x00000001, 0x80000001, 0x3f800000, 0xbf800000], dtype=np.uint32)
+    x = np.concatenate([bits, edges]).view(np.float32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    got = np.empty_like(x)
+    want = np.empty_like(x)
+    lib.ehip_libm_expf(x.ctypes.data_as(fp), got.ctypes.data_as(fp), len(x))
+    olib.orc_expf_n(x.ctypes.data_as(fp), want.ctypes.data_as(fp), len(x))
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    bad = np.flatnonzero(~same)
+    assert bad.size == 0, [(hex(int(x.view(np.uint32)[i])), float(got[i]), float(want[i])) for i in bad[:8]]
+    # against the correctly rounded exponential it differs now and then: the
+    # reason the restatement exists
+    fin = np.isfinite(x) & (np.abs(x) < 80)
+    cr = np.exp(x[fin].astype(np.float64)).astype(np.float32)
+    assert np.mean(cr != want[fin]) > 1e-5   # 7.5e-5 of these bit patterns (6e-4 of uniform [-20, 0])

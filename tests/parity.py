@@ -2,9 +2,11 @@
 
 The target bar is per-step logits within 1e-2 max-abs and 1e-3 relative
 L2 of the reference CPU path, with >= 99% top-1 agreement under teacher
-forcing.  It holds on the small variant models (rel-L2 ~4e-8) and does NOT
-hold end to end on the deep benchmark shapes, where the GPU path differs from
-the reference's deterministic build by ~1e-2 relative L2.
+forcing.  The reference-order mode (EHIP_ORDER=reference) meets it on every
+model and workload with zero difference (check_strict); the default kernels
+meet it on the small variant models (rel-L2 ~4e-8) but NOT end to end on the
+deep benchmark shapes, where they differ from the reference's deterministic
+build by ~1e-2 relative L2.
 
 Why: the reference re-quantizes every matmul input to Q8_0
 (src/kernels.c:210-213), which makes its forward pass discontinuous.  A

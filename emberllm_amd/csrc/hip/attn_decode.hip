@@ -186,7 +186,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     }
     const int pos = a.tokpos[1];
     // rows [0, pos] split into equal chunks over the kv head's workgroups
-    // (two per CU over all kv heads), at least ATT_DEC_RMIN rows each
+    // (one per CU while chunks stay short, then two), at least ATT_DEC_RMIN rows each
     const int R = dec_chunk_rows(pos, nchunk);
     const int nc = (pos + 1 + R - 1) / R;
     if (c >= nc) return;

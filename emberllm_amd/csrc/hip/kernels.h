@@ -139,12 +139,17 @@ constexpr int ATT_DEC_R1MAX = 96;   // positions per chunk up to which a kv head
 // count a little above the CUs a kv head spreads over would put two
 // workgroups on a few CUs, and those set the kernel's end (Qwen3-0.6B shape at
 // positions 1024..1151: 33-36 chunks of 32 rows 7.8 us per layer, 32 chunks of
-// 33-36 rows 6.7 us).  One division, as it follows the position's read.
+// 33-36 rows 6.7 us).  Past that, chunks of fewer than ATT_DEC_RMIN2 rows
+// lose to fewer chunks of ATT_DEC_RMIN2 (positions 3072..3199: 64 chunks of
+// 49-50 rows 11.2 us per layer, 49-50 chunks of 64 rows 10.8 us).  One
+// division, as it follows the position's read.
+constexpr int ATT_DEC_RMIN2 = 64;
 __host__ __device__ inline int dec_chunk_rows(int pos, int max_chunks) {
     const int one = max_chunks / ATT_DEC_WPC > 0 ? max_chunks / ATT_DEC_WPC : 1;
-    const int d = pos + 1 <= ATT_DEC_R1MAX * one ? one : max_chunks;
+    const bool spread = pos + 1 <= ATT_DEC_R1MAX * one;
+    const int d = spread ? one : max_chunks, m = spread ? ATT_DEC_RMIN : ATT_DEC_RMIN2;
     const int r = (pos + d) / d;
-    return r > ATT_DEC_RMIN ? r : ATT_DEC_RMIN;
+    return r > m ? r : m;
 }
 constexpr int XM_CNT_STRIDE = 32;   // ints between arrival counters (one 128-byte line each)
 // out[y * gx + x] = the XCD that workgroup (x, y) of a (gx, gy) grid ran on

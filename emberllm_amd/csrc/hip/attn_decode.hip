@@ -187,7 +187,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     const int pos = a.tokpos[1];
     // rows [0, pos] split into equal chunks over the kv head's workgroups
     // (one per CU while chunks stay short, then two), at least ATT_DEC_RMIN rows each
-    const int R = dec_chunk_rows(pos, nchunk);
+    const int R = dec_chunk_rows(pos, nchunk, F16);
     const int nc = (pos + 1 + R - 1) / R;
     if (c >= nc) return;
     const int t0 = c * R, t1 = min(pos + 1, t0 + R);
@@ -482,14 +482,14 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
 // (chunk maxima are in log2 units).  Thread (s, q) owns float4 quad q of the
 // head row and chunks k = s, s + NS, ...; every partial it needs is loaded in
 // one batch, issued together with the chunk statistics, before any reduction.
-template <int HD>
+template <int HD, bool F16>   // F16: the cache type, which sets the chunk rows
 __global__ __launch_bounds__(WG) void k_attn_merge(AttnArgs a) {
     constexpr int QPR = HD / 4, NS = WG / QPR, KB = 16;
     extern __shared__ __align__(16) float dyn[];   // [max_chunks] float2, then [NS][HD]
     __shared__ float red[NWAVE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
     const int pos = a.tokpos[1];
-    const int R = dec_chunk_rows(pos, a.max_chunks);
+    const int R = dec_chunk_rows(pos, a.max_chunks, F16);
     const int nc = (pos + 1 + R - 1) / R;
     if (nc == 1) return;   // the attention kernel wrote the output
     float2 *sml = reinterpret_cast<float2 *>(dyn);
@@ -592,7 +592,7 @@ static int dec_pick_g(hipStream_t st, const AttnArgs &a, bool with_merge) {
     else return -1;
     if (!with_merge || a.xm_cnt) return 0;
     const size_t lds = 8 * (size_t)a.max_chunks + 4 * (size_t)(WG / (HD / 4)) * HD;
-    hipLaunchKernelGGL((k_attn_merge<HD>), dim3(a.n_heads), dim3(WG), lds, st, a);
+    hipLaunchKernelGGL((k_attn_merge<HD, F16>), dim3(a.n_heads), dim3(WG), lds, st, a);
     return 0;
 }
 

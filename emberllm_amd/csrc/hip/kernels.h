@@ -131,7 +131,7 @@ constexpr int ATT_DEC_NW = 4;       // waves per decode attention workgroup
 constexpr int ATT_DEC_WPC = 2;      // decode attention workgroups per CU
 constexpr int ATT_DEC_CR = 160;     // positions per decode attention workgroup before more are added
 constexpr int ATT_DEC_RMIN = 32;    // positions per decode attention chunk at least (short contexts)
-constexpr int ATT_DEC_R1MAX = 96;   // positions per chunk up to which a kv head uses one workgroup per CU
+constexpr int ATT_DEC_R1MAX = 96;   // positions per chunk up to which a kv head uses one workgroup per CU (fp32 KV)
 // rows per chunk of the decode attention at position pos: (pos + 1) spread
 // over one workgroup per CU (max_chunks / ATT_DEC_WPC of the kv head) while
 // that gives at most ATT_DEC_R1MAX rows, else over all max_chunks; at least
@@ -141,13 +141,16 @@ constexpr int ATT_DEC_R1MAX = 96;   // positions per chunk up to which a kv head
 // positions 1024..1151: 33-36 chunks of 32 rows 7.8 us per layer, 32 chunks of
 // 33-36 rows 6.7 us).  Past that, chunks of fewer than ATT_DEC_RMIN2 rows
 // lose to fewer chunks of ATT_DEC_RMIN2 (positions 3072..3199: 64 chunks of
-// 49-50 rows 11.2 us per layer, 49-50 chunks of 64 rows 10.8 us).  One
-// division, as it follows the position's read.
+// 49-50 rows 11.2 us per layer, 49-50 chunks of 64 rows 10.8 us).  An fp16
+// cache row is half the bytes, and both thresholds double (the SmolLM2-135M
+// shape at positions 4096..4223: 64 chunks of 65-66 rows 11.3 us per layer,
+// 32-33 chunks of 128 rows 9.4 us); a chunk may then exceed ATT_DEC_CR rows,
+// which only sizes the grid.  One division, as it follows the position's read.
 constexpr int ATT_DEC_RMIN2 = 64;
-__host__ __device__ inline int dec_chunk_rows(int pos, int max_chunks) {
-    const int one = max_chunks / ATT_DEC_WPC > 0 ? max_chunks / ATT_DEC_WPC : 1;
-    const bool spread = pos + 1 <= ATT_DEC_R1MAX * one;
-    const int d = spread ? one : max_chunks, m = spread ? ATT_DEC_RMIN : ATT_DEC_RMIN2;
+__host__ __device__ inline int dec_chunk_rows(int pos, int max_chunks, bool f16) {
+    const int one = max_chunks / ATT_DEC_WPC > 0 ? max_chunks / ATT_DEC_WPC : 1, sh = f16 ? 1 : 0;
+    const bool spread = pos + 1 <= (ATT_DEC_R1MAX << sh) * one;
+    const int d = spread ? one : max_chunks, m = spread ? ATT_DEC_RMIN : ATT_DEC_RMIN2 << sh;
     const int r = (pos + d) / d;
     return r > m ? r : m;
 }

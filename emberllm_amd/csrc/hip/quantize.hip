@@ -18,11 +18,13 @@
 //         and clamped to 0..15, element i in the low and element i+16 in the
 //         high nibble of byte i.
 // When a block's largest magnitude is below about 3.7e-37 (Q8_0) or 2.4e-38
-// (Q4_0), 1/d overflows to infinity and x*inv is infinite or NaN.  There the
-// host's conversions (lroundf, and the (int) cast, on x86-64) return the
-// most negative integer, which clamps to -127 (Q8_0) or 0 (Q4_0) whatever
-// the sign; the device's saturating conversion would give +127 or 15 for
-// positive values, so such products take the host's result explicitly.
+// (Q4_0), 1/d overflows to infinity and x*inv is infinite or NaN; a block
+// holding an infinity has d infinite and inverse 0, so its infinite (and NaN)
+// elements give NaN products.  The reference converts with (int)lroundf(p)
+// (Q8_0) and (int)(p + 8.5f) (Q4_0); on x86-64 those give LONG_MIN and
+// INT_MIN for such products, whose int values clamp to code 0 in both
+// encodings whatever the sign.  The device's conversions would saturate
+// instead, so such products take the host's result explicitly.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -73,9 +75,13 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *__restrict__ 
             const float inv = d > 0.0f ? 1.0f / d : 0.0f;
             o[0] = half_bits(d);
             auto code = [inv](float x) {
-                const float p = __fmul_rn(x, inv);
-                const float q = fabsf(p) < 0x1p63f ? fminf(fmaxf(roundf(p), -127.0f), 127.0f) : -127.0f;
-                return (uint32_t)(int)q & 0xffu;
+                // (int)lroundf(p): the rounded value (half away from zero)
+                // reduced to its low 32 bits, and 0 (the low bits of
+                // LONG_MIN) for NaN, infinities and |p| >= 2^63
+                const float r = roundf(__fmul_rn(x, inv));
+                int q = fabsf(r) < 0x1p63f ? (int)(long long)r : 0;
+                q = q > 127 ? 127 : q < -127 ? -127 : q;
+                return (uint32_t)q & 0xffu;
             };
 #pragma unroll
             for (int i = 0; i < 16; i++) o[1 + i] = (uint16_t)(code(v[2 * i]) | (code(v[2 * i + 1]) << 8));

@@ -65,7 +65,9 @@ void ember_quant_q8_row(const float *x, uint8_t *out, int n) {
         const uint16_t dh = ember_float_to_half(d);
         memcpy(out, &dh, 2);
         for (int i = 0; i < EMBER_Q_BLOCK; i++) {
-            long q = lroundf(v[i] * inv);
+            /* the reference's (int)lroundf: NaN and infinite products give
+             * LONG_MIN, whose int conversion is 0 (code 0, not -127) */
+            int q = (int)lroundf(v[i] * inv);
             if (q > 127) q = 127;
             if (q < -127) q = -127;
             out[2 + i] = (uint8_t)(int8_t)q;
@@ -111,7 +113,15 @@ int ember_quantize_file(const char *in_path, const char *out_path, int target) {
     for (int i = 0; i < n; i++) {
         const EmberTensor *t = &tab[i];
         const void *src = ember_model_data(m, t);
-        if (!src) {
+        const int rows = t->shape[0], cols = t->shape[1];
+        const int quantize = t->dtype == EMBER_DT_F32 && t->ndim >= 2 && cols % EMBER_Q_BLOCK == 0;
+        /* the fp32 rows the encoder reads must lie inside the tensor's payload */
+        const int short_payload = quantize && (rows < 0 || cols < 0 ||
+                                               (uint64_t)rows * (uint64_t)cols * 4u > t->nbytes);
+        if (short_payload)
+            fprintf(stderr, "ember: %s: tensor '%.48s' holds %llu bytes, fewer than its [%d, %d] fp32 shape\n",
+                    in_path, t->name, (unsigned long long)t->nbytes, rows, cols);
+        if (!src || short_payload) {
             for (int k = 0; k < i; k++) free(data[k]);
             free(data); free(meta); free(jobs);
             ember_model_free(m);
@@ -122,8 +132,6 @@ int ember_quantize_file(const char *in_path, const char *out_path, int target) {
         if (target == EMBER_DT_Q4_0 &&
             (!strcmp(t->name, "tok_embeddings") || !strcmp(t->name, "lm_head")))
             want = EMBER_DT_Q8_0;
-        const int rows = t->shape[0], cols = t->shape[1];
-        const int quantize = t->dtype == EMBER_DT_F32 && t->ndim >= 2 && cols % EMBER_Q_BLOCK == 0;
         if (!quantize) {   /* passes through unchanged */
             data[i] = ember_xmalloc(t->nbytes, "tensor copy");
             memcpy(data[i], src, t->nbytes);

@@ -184,7 +184,7 @@ void orc_quantize_q8_0(const float *x, void *out, int n) {
         float inv = d > 0.0f ? 1.0f / d : 0.0f;
         o[b].d = orc_f32_to_f16(d);
         for (int i = 0; i < QB; i++) {
-            long q = lroundf(v[i] * inv);
+            int q = (int)lroundf(v[i] * inv);   /* as kernels.c:86: LONG_MIN (NaN, inf) -> 0 */
             o[b].q[i] = (int8_t)(q > 127 ? 127 : (q < -127 ? -127 : q));
         }
     }

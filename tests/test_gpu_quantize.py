@@ -19,6 +19,7 @@ import pytest
 
 import oracle
 from emberllm_amd import _native, configs
+from quant_rows import edge_rows
 
 pytestmark = pytest.mark.gpu
 L = None
@@ -59,36 +60,6 @@ def device_blocks(mats):
     rc = lib().ehip_quantize_rows(jobs, len(mats))
     assert rc == 0, _native.last_error()
     return outs
-
-
-def edge_rows():
-    """Rows of 64 values (two blocks each) that reach every branch."""
-    rng = np.random.default_rng(17)
-    rows = []
-    rows.append(np.zeros(64, np.float32))                                   # amax 0: d 0, inverse 0
-    rows.append(np.array([2.5, -2.5, 1.5, -1.5, 0.5, -0.5, 127, 3.5] * 8, np.float32))   # d 1, exact ties
-    rows.append(np.array([-8, 8, 0.5, -0.5, 7.5, -7.5, 1, 3] * 8, np.float32))   # Q4: first of equal magnitudes
-    rows.append(np.array([8, -8, -0.5, 0.5, -7.5, 7.5, -1, -3] * 8, np.float32))
-    rows.append((rng.standard_normal(64) * 1e-7).astype(np.float32))      # fp16-subnormal scale
-    rows.append((rng.standard_normal(64) * 1e-40).astype(np.float32))     # fp32-subnormal values
-    rows.append((rng.standard_normal(64) * 1e38).astype(np.float32))      # scale past 65504
-    rows.append((rng.standard_normal(64) * 1e7).astype(np.float32))
-    r = rng.standard_normal(64).astype(np.float32)
-    r[5], r[40] = np.inf, -np.inf
-    rows.append(r)
-    r = rng.standard_normal(64).astype(np.float32)
-    r[3], r[33] = np.nan, np.nan
-    rows.append(r)
-    rows.append(np.full(64, -3.0, np.float32))                              # constant block
-    # values at code boundaries: x*inv landing on k + 0.5 after rounding
-    a = np.float32(1.3)
-    d = a / np.float32(127.0)
-    inv = np.float32(1.0) / d
-    r = np.concatenate([[a], (np.arange(63, dtype=np.float32) - 31.5) / inv]).astype(np.float32)
-    rows.append(r)
-    for s in (1e-3, 0.02, 1.0, 50.0):
-        rows.append((rng.standard_normal(64) * s).astype(np.float32))
-    return np.stack(rows)
 
 
 @pytest.mark.parametrize("dtype", [_native.DT_Q8_0, _native.DT_Q4_0], ids=["q8_0", "q4_0"])

@@ -15,6 +15,7 @@ import pytest
 
 import oracle
 from emberllm_amd import _native, configs
+from quant_rows import edge_rows
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -91,6 +92,39 @@ def test_quantizers_match_reference_golden():
         assert np.array_equal(q8, g["q8"][i]) and np.array_equal(q4, g["q4"][i]), i
 
 
+def test_quantizers_match_reference_on_edge_rows():
+    """The host row quantizers and the oracle's against the reference's own
+    ember_quantize_q8_0 / q4_0 (src/kernels.c:73-115, its deterministic
+    build in oracle/_ref) on rows that reach every branch: zero blocks,
+    subnormal and overflowing scales, ties, infinities, NaNs and blocks whose
+    inverse scale overflows (NaN and infinite products, which the reference's
+    (int)lroundf maps to code 0)."""
+    import oracle
+    x = edge_rows()
+    n = x.shape[1]
+    fp = ctypes.POINTER(ctypes.c_float)
+    refl = oracle.reference_lib(debug=True) if os.path.exists(oracle.reference_path(True)) else None
+    orc = oracle.oracle_lib()
+    for bs, host, orcf, reff in ((34, L.ember_quant_q8_row, orc.orc_quantize_q8_0, "ember_quantize_q8_0"),
+                                 (18, L.ember_quant_q4_row, orc.orc_quantize_q4_0, "ember_quantize_q4_0")):
+        for i, row in enumerate(x):
+            row = np.ascontiguousarray(row)
+            got = np.zeros(n // 32 * bs, np.uint8)
+            via_orc = np.zeros_like(got)
+            host(row.ctypes.data_as(fp), got.ctypes.data, n)
+            orcf(row.ctypes.data_as(fp), via_orc.ctypes.data, n)
+            assert np.array_equal(got, via_orc), (bs, i, got, via_orc)
+            if refl is not None:
+                want = np.zeros_like(got)
+                getattr(refl, reff)(row.ctypes.data_as(fp), want.ctypes.data, n)
+                assert np.array_equal(got, want), (bs, i, got, want)
+    # the case the reference maps to 0: codes of a block whose 1/d overflows
+    q8 = np.zeros(68, np.uint8)
+    row = np.ascontiguousarray(x[12])
+    L.ember_quant_q8_row(row.ctypes.data_as(fp), q8.ctypes.data, 64)
+    assert not q8[2:34].any() and not q8[36:68].any()
+
+
 def test_quantize_file_without_gpu_fails_loudly(tmp_path):
     """ember_quantize_file encodes its blocks on the GPU (its parity with the
     reference's requantizer is a GPU test); without one it reports an error
@@ -104,6 +138,29 @@ def test_quantize_file_without_gpu_fails_loudly(tmp_path):
             "sys.exit(_native.lib().ember_quantize_file(%r, %r, 1))\n") % (ROOT, f32.encode(), str(out).encode())
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 1 and "ember: no GPU" in r.stderr, (r.returncode, r.stderr)
+    assert not out.exists()
+
+
+def test_quantize_file_rejects_shape_beyond_payload(tmp_path, capfd):
+    """A 2-D fp32 tensor whose [rows, cols] needs more bytes than its payload
+    holds is rejected before any row is read (the encoder would otherwise
+    read past the tensor, and past the mapping for the last one)."""
+    f32 = configs.model_path("hq_f32", dict(configs.TINY["t_qwen3"], dtype=_native.DT_F32))
+    raw = bytearray(open(f32, "rb").read())
+    tab, n = struct.unpack_from("<Q", raw, 112)[0], struct.unpack_from("<i", raw, 76)[0]
+    for i in range(n):
+        e = tab + 88 * i
+        if raw[e:e + 48].rstrip(b"\0") == b"layers.1.w2":
+            rows = struct.unpack_from("<i", raw, e + 56)[0]
+            struct.pack_into("<i", raw, e + 56, rows * 1000)
+            break
+    else:
+        raise AssertionError("layers.1.w2 not in the table")
+    bad, out = tmp_path / "bad.ember", tmp_path / "q.ember"
+    bad.write_bytes(bytes(raw))
+    assert L.ember_quantize_file(str(bad).encode(), str(out).encode(), _native.DT_Q8_0) == 1
+    err = capfd.readouterr().err
+    assert "layers.1.w2" in err and "fewer than its" in err, err
     assert not out.exists()
 
 

@@ -6,23 +6,27 @@ Workload (the headline configuration): a Qwen3-0.6B-shape model, Q8_0
 vocab 151936, tied embeddings, RoPE theta 1e6), weights drawn N(0, 0.02)
 from the package's seeded generator, norms 1.0, quantized by its bit-exact
 Q8_0 quantizer.  The KV cache (fp32) is filled by a batched prefill of 4096
-seeded random ids; then greedy decode runs at positions 4096.. .
+ids; then greedy-shaped decode runs at positions 4096.. .
 
-A step is one decode token.  `value` is the device-resident greedy loop
-(ehip_generate_greedy: decode graph + on-device argmax, no host round trip)
-over exactly --steps tokens after --warmup untimed ones, timed with HIP
-events on the state's stream between two stream synchronisations.  Also
-reported, never as `value`:
-  api_decode_tok_s      ember_forward per token through the C API, host
-                        logits over PCIe each step (the reference bench's
-                        loop, src/main.c:258-263)
-  decode_tok_s_depth128 the same device loop at depth 128
+A step is one decode token through the C API.  `value` is the reference's
+own benchmark loop (`ember bench`, src/main.c:230-294: the reference's
+main.c compiled unmodified against libember.so, emberllm_amd/_cli/ember):
+per rep a pp<depth> prefill, then --steps calls of ember_forward, each
+returning the step's logits in host memory, tokens (pos*131+7) % V from
+pos = depth; one warmup rep, then the mean of the timed reps' decode rates.
+Without that program (it is built where the reference's sources are) the
+same protocol runs through ctypes.  Also reported, never as `value`:
+  decode_tok_s_device_loop  the device-resident greedy loop
+                        (ehip_generate_greedy: decode graph + on-device argmax,
+                        no host round trip), HIP events on the state's stream
+  api_decode_tok_s      the ember bench protocol through ctypes (ember_forward
+                        per token from Python)
+  decode_tok_s_depth128 ember bench --pp 128 (decode at depth 128)
   decode_tok_s_sampled  the device loop with the full sampler (temperature
                         0.8, top-k 40, top-p 0.9, fixed seed) at the same depth
-  prefill_tok_s_pp128 / _pp4096   ember_prefill at position 0 (mean of 5
-                        after 1 warmup, src/main.c:251-266); the last
-                        pp4096 run leaves the cache filled for the decode
-  ttft_ms_pp128 / _pp4096         the same prefills plus the first token's
+  prefill_tok_s_pp128 / _pp4096   ember bench's prefill rates (mean of the
+                        timed reps, src/main.c:251-266)
+  ttft_ms_pp128 / _pp4096         ember_prefill plus the first token's
                         selection on the host (time to first token)
   load_s                ember_model_load + ember_state_new_ex: the file
                         mapped, weights repacked and uploaded, KV cache and
@@ -111,51 +115,76 @@ def cpu_baseline(path, c, depth, budget_s):
     import oracle
     ncpu = min(16, len(os.sched_getaffinity(0)))
     V = c["vocab_size"]
-    kind, debug_note = "reference", "oracle/_ref/libember_ref.so (reference sources, -O3 -ffast-math -march=x86-64-v3)"
+    # the reference's Makefile builds with -march=native (Makefile:23): its
+    # AVX2 (x86-64-v3) build and, where this host has AVX-512, its x86-64-v4
+    # build are both swept and the faster reported
+    flags = set()
     try:
-        libr = oracle.reference_lib(debug=False)
+        with open("/proc/cpuinfo") as f:
+            flags = set(next((ln.split(":", 1)[1].split() for ln in f if ln.startswith("flags")), []))
+    except OSError:
+        pass
+    has_v4 = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags
+    builds = [False] + ([True] if has_v4 and os.path.exists(oracle.reference_path(False, v4=True)) else [])
+    kind = "reference"
 
-        def make(ctx):
-            return oracle.Reference(path, ctx=ctx, debug=False)
+    def note(v4):
+        return (f"oracle/_ref/{os.path.basename(oracle.reference_path(False, v4))} (the reference's sources with "
+                f"its optimized flags -O3 -ffast-math -funroll-loops, -march={'x86-64-v4' if v4 else 'x86-64-v3'} "
+                f"in place of -march=native)")
+    try:
+        for v4 in builds:
+            oracle.reference_lib(debug=False, v4=v4)
 
-        def set_threads(n):
+        def make(ctx, v4):
+            return oracle.Reference(path, ctx=ctx, debug=False, v4=v4)
+
+        def set_threads(n, v4):
+            libr = oracle.reference_lib(debug=False, v4=v4)
             libr.ember_threads_shutdown()
             libr.ember_threads_init(n)
     except (FileNotFoundError, OSError):
-        kind, debug_note = "port", "oracle/liboracle_fast.so (restatement, optimized flags)"
+        kind, builds = "port", [False]
         libo = oracle.oracle_lib(fast=True)
 
-        def make(ctx):
+        def note(v4):
+            return "oracle/liboracle_fast.so (restatement, optimized flags)"
+
+        def make(ctx, v4):
             return oracle.Oracle(path, ctx=ctx, fast=True)
 
-        def set_threads(n):
+        def set_threads(n, v4):
             libo.orc_threads_shutdown()
             libo.orc_threads_init(n)
     sweep = [t for t in (1, 2, 4, 8, 16) if t <= ncpu]
     if ncpu not in sweep:
         sweep.append(ncpu)
-    per_point = budget_s / len(sweep)
-    eng = make(depth + 64)
-    best = (0.0, 1, 0)
+    per_point = budget_s / (len(sweep) * len(builds))
+    best = (0.0, 1, 0, False)
     t_start = time.time()
-    pos = depth
-    for nt in sweep:
-        set_threads(nt)
-        eng.forward((pos * 131 + 7) % V, pos)       # warmup (first touch of pages)
-        pos += 1
-        n, t0 = 0, time.perf_counter()
-        while n < 2 or (time.perf_counter() - t0 < per_point * 0.6 and n < 96):
-            eng.forward((pos * 131 + 7) % V, pos)
+    tried = []
+    for v4 in builds:
+        eng = make(depth + 64, v4)
+        pos = depth
+        for nt in sweep:
+            set_threads(nt, v4)
+            eng.forward((pos * 131 + 7) % V, pos)       # warmup (first touch of pages)
             pos += 1
-            n += 1
-            if pos >= depth + 60:
-                pos = depth
-        rate = n / (time.perf_counter() - t0)
-        log(f"cpu baseline ({kind}) {nt} threads: {rate:.2f} tok/s over {n} steps")
-        if rate > best[0]:
-            best = (rate, nt, n)
-    eng.close()
-    set_threads(1)
+            n, t0 = 0, time.perf_counter()
+            while n < 2 or (time.perf_counter() - t0 < per_point * 0.6 and n < 96):
+                eng.forward((pos * 131 + 7) % V, pos)
+                pos += 1
+                n += 1
+                if pos >= depth + 60:
+                    pos = depth
+            rate = n / (time.perf_counter() - t0)
+            tried.append(f"{'v4' if v4 else 'v3'}/{nt}t {rate:.1f}")
+            log(f"cpu baseline ({kind}, {'x86-64-v4' if v4 else 'x86-64-v3'}) {nt} threads: "
+                f"{rate:.2f} tok/s over {n} steps")
+            if rate > best[0]:
+                best = (rate, nt, n, v4)
+        eng.close()
+        set_threads(1, v4)
     cpu = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -164,8 +193,54 @@ def cpu_baseline(path, c, depth, budget_s):
         pass
     return {"value": round(best[0], 3), "unit": "tok/s", "cores": best[1], "kind": kind,
             "sample": (f"{best[2]} greedy-shaped decode steps (token stream (pos*131+7)%V) at positions "
-                       f"{depth}.. of the same model via {debug_note}; best of threads {sweep} "
-                       f"({time.time() - t_start:.0f} s total) on '{cpu}', {ncpu} cores available")}
+                       f"{depth}.. of the same model via {note(best[3])}; best of threads {sweep} and builds "
+                       f"[{', '.join(tried)} tok/s] ({time.time() - t_start:.0f} s total) on '{cpu}', "
+                       f"{ncpu} cores available")}
+
+
+GPU_CLI = os.path.join(ROOT, "emberllm_amd", "_cli", "ember")
+
+
+def cli_bench(path, pp, tg, reps, kv16):
+    """`ember bench` (src/main.c:230-294) over libember.so: returns its
+    prefill and decode rates (mean and sd over the timed reps), or None
+    when the program is absent."""
+    import re
+    import subprocess
+    if not os.path.exists(GPU_CLI):
+        return None
+    cmd = [GPU_CLI, "bench", path, "--pp", str(pp), "--tg", str(tg), "--reps", str(reps)]
+    if kv16:
+        cmd += ["--kv-type", "f16"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"{' '.join(cmd)} failed ({r.returncode}): {r.stderr[-2000:]}")
+    out = {}
+    for what, key in (("prefill", "pp"), ("decode", "tg")):
+        m = re.search(rf"{what}\s+\({key}(\d+)\):\s+([0-9.]+) tok/s\s+\(\+/- ([0-9.]+)\)", r.stdout)
+        if not m:
+            raise RuntimeError(f"unexpected ember bench output: {r.stdout}")
+        out[what] = (float(m.group(2)), float(m.group(3)))
+    log(f"ember bench --pp {pp} --tg {tg} --reps {reps}{' --kv-type f16' if kv16 else ''}: "
+        f"prefill {out['prefill'][0]:.1f} tok/s, decode {out['decode'][0]:.1f} +/- {out['decode'][1]:.1f} tok/s")
+    return out
+
+
+def ctypes_bench(eng, pp, tg, reps):
+    """The same protocol through ctypes (ember_prefill, then ember_forward
+    per token with host logits): mean decode rate of the timed reps."""
+    lib, V = eng.lib, eng.vocab
+    ids = np.array([(i * 131 + 7) % V for i in range(pp)], np.int32)
+    pids = ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+    rates = []
+    for r in range(1 + reps):
+        lib.ember_prefill(eng.m, eng.st, pids, pp, 0)
+        t = time.perf_counter()
+        for pos in range(pp, pp + tg):
+            lib.ember_forward(eng.m, eng.st, (pos * 131 + 7) % V, pos)
+        if r:
+            rates.append(tg / (time.perf_counter() - t))
+    return float(np.mean(rates)), float(np.std(rates, ddof=1))
 
 
 def quantize_bench(model):
@@ -225,6 +300,7 @@ def main():
     ap.add_argument("--model", default="qwen3_06b")
     ap.add_argument("--depth", type=int, default=4096)
     ap.add_argument("--kv", choices=("f32", "f16"), default="f32")
+    ap.add_argument("--reps", type=int, default=5, help="timed reps of the ember bench protocol (src/main.c:232)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill and kernel timings")
@@ -286,6 +362,10 @@ def main():
     t0 = time.time()
     path = configs.model_path(args.model, threads=16)
     log(f"model {path} ready in {time.time() - t0:.1f} s")
+    # ---- the headline: ember bench over libember.so (its own process) -----
+    cli = None
+    if not (args.prefill_only or args.sampled_only):
+        cli = cli_bench(path, depth, K, args.reps, args.kv == "f16")
     ctx = depth + max(K, W) + 2
     t = time.perf_counter()
     # ember_model_load + ember_state_new_ex: the file mapped, every weight
@@ -308,33 +388,29 @@ def main():
         return
 
     # ---- prefill --------------------------------------------------------
-    def prefill_rate(n, reps=5, warm=1):
-        """The reference bench's prefill protocol (src/main.c:251-266): one
-        untimed run, then the mean of `reps` timed ones; returns (mean, sd,
-        last logits)."""
+    def prefill_ttft(n, reps=5, warm=1):
+        """ember_prefill of n ids at position 0 plus the first token's
+        selection on the host, mean of `reps` after `warm`; returns the last
+        logits."""
         ids = rng.integers(0, V, n).astype(np.int32)
-        rates, firsts = [], []
+        firsts = []
         for r in range(warm + reps):
             t = time.perf_counter()
             lg = eng.prefill(ids)
-            dt = time.perf_counter() - t
-            int(np.argmax(lg))   # the first generated token: time to first token
+            int(np.argmax(lg))   # the first generated token
             if r >= warm:
-                rates.append(n / dt)
                 firsts.append(time.perf_counter() - t)
         out[f"ttft_ms_pp{n}"] = float(np.mean(firsts)) * 1e3
-        return float(np.mean(rates)), float(np.std(rates, ddof=1) if len(rates) > 1 else 0.0), lg
+        return lg
 
     if not args.decode_only:
-        out["prefill_tok_s_pp128"], out["prefill_tok_s_pp128_sd"], _ = prefill_rate(128)
-        log(f"prefill pp128 {out['prefill_tok_s_pp128']:.1f} tok/s, "
-            f"time to first token {out['ttft_ms_pp128']:.2f} ms")
-    # fill the cache to `depth` (also timed: pp<depth>, mean of 5 after 1 warmup)
-    key = f"prefill_tok_s_pp{depth}"
-    out[key], out[key + "_sd"], lg = prefill_rate(depth, reps=1 if args.decode_only else 5,
-                                                  warm=0 if args.decode_only else 1)
-    log(f"prefill pp{depth} {out[key]:.1f} tok/s, time to first token {out[f'ttft_ms_pp{depth}']:.2f} ms")
+        prefill_ttft(128)
+        log(f"time to first token pp128 {out['ttft_ms_pp128']:.2f} ms")
+    lg = prefill_ttft(depth, reps=1 if args.decode_only else 5, warm=0 if args.decode_only else 1)
+    log(f"time to first token pp{depth} {out[f'ttft_ms_pp{depth}']:.2f} ms")
     tok0 = int(np.argmax(lg))
+    if cli:
+        out[f"prefill_tok_s_pp{depth}"], out[f"prefill_tok_s_pp{depth}_sd"] = cli["prefill"]
 
     def sampled_rate():
         smp = _native.EmberSampler()
@@ -354,22 +430,23 @@ def main():
     # ---- decode at depth: device-resident greedy loop --------------------
     eng.generate_greedy(tok0, depth, W)             # warmup (graph capture happens before the
                                                     # timed region of every call)
-    wall = time.perf_counter()
-    toks, ms = eng.generate_greedy(tok0, depth, K)  # synchronises before and after
-    wall = time.perf_counter() - wall
-    tok_s = K / (ms / 1e3)
-    ms_step = ms / K
-    mean_bytes = float(np.mean([step_bytes(c, depth + i, e_kv) for i in range(K)]))
-    log(f"decode @{depth}: {tok_s:.1f} tok/s ({ms_step * 1e3:.1f} us/step, wall {K / wall:.1f} tok/s), "
-        f"{mean_bytes / 1e6:.1f} MB/step -> {tok_s * mean_bytes / HBM_PEAK:.3f} of HBM roofline")
+    _, ms = eng.generate_greedy(tok0, depth, K)     # synchronises before and after
+    out["decode_tok_s_device_loop"] = K / (ms / 1e3)
+    out["decode_us_per_step_device_loop"] = ms / K * 1e3
+    log(f"decode @{depth}, device greedy loop: {out['decode_tok_s_device_loop']:.1f} tok/s "
+        f"({ms / K * 1e3:.1f} us/step)")
 
-    # ---- the same decode through the C API (host logits every step) -------
-    pos, t = depth, time.perf_counter()
-    for i in range(K):
-        eng.forward((pos * 131 + 7) % V, pos)
-        pos += 1
-    out["api_decode_tok_s"] = K / (time.perf_counter() - t)
-    log(f"api decode @{depth}: {out['api_decode_tok_s']:.1f} tok/s (ember_forward, PCIe logits)")
+    # ---- the ember bench protocol through ctypes ----------------------------
+    out["api_decode_tok_s"], out["api_decode_tok_s_sd"] = ctypes_bench(eng, depth, K, args.reps)
+    log(f"ember bench protocol via ctypes @{depth}: {out['api_decode_tok_s']:.1f} tok/s")
+    if cli:
+        tok_s, tok_sd, harness = cli["decode"][0], cli["decode"][1], "ember bench (src/main.c) over libember.so"
+    else:
+        tok_s, tok_sd, harness = out["api_decode_tok_s"], out["api_decode_tok_s_sd"], "ember bench protocol via ctypes"
+    ms_step = 1e3 / tok_s
+    mean_bytes = float(np.mean([step_bytes(c, depth + i, e_kv) for i in range(K)]))
+    log(f"decode @{depth} ({harness}): {tok_s:.1f} tok/s ({ms_step * 1e3:.1f} us/step), "
+        f"{mean_bytes / 1e6:.1f} MB/step -> {tok_s * mean_bytes / HBM_PEAK:.3f} of HBM roofline")
 
     roof = None
     if not args.decode_only:
@@ -402,32 +479,37 @@ def main():
                           f"at position {depth}, {ab} algorithmic bytes per launch, mean of {reps_k} "
                           f"launches walking the {c['n_layers']} layers' caches"}
 
-        # ---- depth 128 ------------------------------------------------------
-        eng.generate_greedy(tok0, 128, W)
-        _, ms128 = eng.generate_greedy(tok0, 128, K)
-        out["decode_tok_s_depth128"] = K / (ms128 / 1e3)
-        log(f"decode @128: {out['decode_tok_s_depth128']:.1f} tok/s")
-
         # ---- sampled decode at depth (T 0.8, top-k 40, top-p 0.9) ---------
         out["decode_tok_s_sampled"] = sampled_rate()
     eng.close()
+
+    if not args.decode_only and depth != 128:
+        # ---- depth 128: ember bench --pp 128 --------------------------------
+        c128 = cli_bench(path, 128, K, args.reps, args.kv == "f16")
+        if c128:
+            out["prefill_tok_s_pp128"], out["prefill_tok_s_pp128_sd"] = c128["prefill"]
+            out["decode_tok_s_depth128"], out["decode_tok_s_depth128_sd"] = c128["decode"]
 
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(path, c, depth, args.cpu_seconds)
 
+    reps = args.reps
     line = {
-        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": K if cli else W,
         "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 dot / f32 accumulate (Q8_0 weights and activations), f32 KV" if e_kv == 4 else
                  "int8 dot / f32 accumulate (Q8_0 weights and activations), f16 KV",
         "data": "synthetic: seeded N(0,0.02) weights quantized to Q8_0, seeded uniform random prompt ids",
-        "config": {"workload": f"{args.model}-shape greedy decode of {K} tokens at depth {depth} after a "
+        "config": {"workload": f"{args.model}-shape decode of {K} tokens at depth {depth} after a "
                                f"{depth}-token batched prefill; {args.kv} KV cache",
-                   "depth": depth, "kv": args.kv, "parallelism": "single GPU, single stream"},
+                   "depth": depth, "kv": args.kv, "parallelism": "single GPU, single stream",
+                   "harness": f"{harness}: {reps} timed reps (after 1 warmup rep) of a pp{depth} prefill "
+                              f"then {K} ember_forward calls with host logits; value = mean of the reps' rates",
+                   "value_sd": round(tok_sd, 2)},
         "hbm_roofline_frac_step": round(tok_s * mean_bytes / HBM_PEAK, 4),
         "bytes_per_step": int(mean_bytes),
-        "wall_tok_s": round(K / wall, 2),
     }
     line.update({k: (round(v, 2) if isinstance(v, float) else v) for k, v in out.items()})
     line["roofline"] = roof

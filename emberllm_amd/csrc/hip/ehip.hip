@@ -396,7 +396,9 @@ struct EhipState {
     int ctx, f16kv, esize, graph_mode;
     hipStream_t st;
     void *kc, *vc;
-    int *tokpos_d, *tokpos_h;
+    int *tokpos_d, *tokpos_h;   // {token, position, steps generated, API step ticket}
+    int *done_h;                // pinned: the ticket of the last completed API step
+    int ticket;
     float *x, *qkv, *o, *h, *logits_d, *logits_h;
     float *part;
     float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
@@ -494,6 +496,7 @@ extern "C" void ehip_state_destroy(EhipState *s) {
     if (s->smp_hist) (void)hipFree(s->smp_hist);
     for (void *p : s->allocs) (void)hipFree(p);
     if (s->tokpos_h) (void)hipHostFree(s->tokpos_h);
+    if (s->done_h) (void)hipHostFree(s->done_h);
     if (s->logits_h) (void)hipHostFree(s->logits_h);
     if (s->ev0) (void)hipEventDestroy(s->ev0);
     if (s->ev1) (void)hipEventDestroy(s->ev1);
@@ -677,6 +680,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     if (hipHostMalloc(&s->tokpos_h, 16, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(&s->done_h, 64, hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(&s->logits_h, 4 * ((size_t)c.vocab_size + 4), hipHostMallocDefault) != hipSuccess ||
         hipEventCreate(&s->ev0) != hipSuccess || hipEventCreate(&s->ev1) != hipSuccess) {
         set_err("pinned host allocation failed");
@@ -684,6 +688,8 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
         return nullptr;
     }
     memset(s->logits_h, 0, 4 * ((size_t)c.vocab_size + 4));
+    memset(s->tokpos_h, 0, 16);
+    *s->done_h = 0;
     return s;
 }
 
@@ -790,12 +796,52 @@ static int enq_decode(EhipState *s) {
     return enq_head(s, s->x);
 }
 
+// The API step's completion: its ticket (tokpos[3], copied in with the token)
+// stored into pinned host memory by one lane after the head, with a
+// system-scope release, so the host sees it once the logits are in host
+// memory.  The host polls that word instead of waking from
+// hipStreamSynchronize (about 5 us sooner per step).
+__global__ void k_step_done(const int *tokpos, int *done_h) {
+    if (threadIdx.x == 0) __hip_atomic_store(done_h, tokpos[3], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// One API decode step: token, position and ticket in (one 16-byte copy), the
+// layers, the head, the logits out, the ticket back.  The quantized heads
+// store the logits (and the error flag behind them) straight into the pinned
+// host buffer as they are produced, so the PCIe writes overlap the head's
+// weight stream (a copy after the head added about 12 us per step); the F32
+// and reference-order heads are followed by a copy.
 static int enq_step(EhipState *s) {
     const int V = s->m->cfg.vocab_size;
-    HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 8, hipMemcpyHostToDevice, s->st), -1);
-    if (enq_decode(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
-    HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * ((size_t)V + 1), hipMemcpyDeviceToHost, s->st), -1);
+    HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
+    if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
+    const bool direct = !s->ref_order && s->m->head.dtype != DT_F32;
+    MatvecArgs a = head_args(s, s->x);
+    if (direct) a.out_host = s->logits_h;
+    if (mv(s, PRO_NORM, EPI_STORE, a)) { set_err("lm_head launch failed"); return -1; }
+    if (!direct)
+        HCHK(hipMemcpyAsync(s->logits_h, s->logits_d, 4 * ((size_t)V + 1), hipMemcpyDeviceToHost, s->st), -1);
+    hipLaunchKernelGGL(k_step_done, dim3(1), dim3(64), 0, s->st, (const int *)s->tokpos_d, s->done_h);
+    HCHK(hipGetLastError(), -1);
     return 0;
+}
+
+// Wait for the API step holding `ticket`: poll the pinned word its last
+// kernel writes, querying the stream now and then so that a failed launch
+// ends the wait with an error.
+static int wait_step(EhipState *s, int ticket) {
+    for (unsigned long k = 1;; k++) {
+        if (__atomic_load_n(s->done_h, __ATOMIC_ACQUIRE) == ticket) return 0;
+        if ((k & 1023) == 0) {
+            const hipError_t q = hipStreamQuery(s->st);
+            if (q == hipErrorNotReady) continue;
+            if (q != hipSuccess) { set_err("decode step: %s", hipGetErrorString(q)); return -1; }
+            if (__atomic_load_n(s->done_h, __ATOMIC_ACQUIRE) == ticket) return 0;
+            set_err("decode step: the stream finished without the step's completion word");
+            return -1;
+        }
+        __builtin_ia32_pause();
+    }
 }
 
 static int run_step(EhipState *s) {
@@ -820,9 +866,11 @@ static int run_step(EhipState *s) {
 extern "C" float *ehip_forward(EhipState *s, int tok, int pos) {
     s->tokpos_h[0] = tok;
     s->tokpos_h[1] = pos;
+    s->tokpos_h[2] = 0;
     for (int attempt = 0; attempt < 2; attempt++) {
+        const int ticket = s->tokpos_h[3] = ++s->ticket;
         if (run_step(s)) return nullptr;
-        HCHK(hipStreamSynchronize(s->st), nullptr);
+        if (wait_step(s, ticket)) return nullptr;
         int flag;
         memcpy(&flag, s->logits_h + s->m->cfg.vocab_size, 4);
         if (!flag) return s->logits_h;

@@ -34,6 +34,11 @@ struct MatvecArgs {
     // and am_out[n] = token (when n < am_cap).
     float *am_val; int *am_idx;
     int *am_tokpos; int *am_out; int am_cap;
+    // EPI_STORE only, optional: the outputs also stored straight into this
+    // pinned host buffer (the API's logits), and the word after the last
+    // output (out[units], the step's error flag) copied behind them, so the
+    // PCIe writes overlap the product's weight stream instead of following it
+    float *out_host;
 };
 constexpr int MATVEC_MAX_GRID = 2048;
 int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);

@@ -224,6 +224,10 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
         }
     }
 
+    // the error-flag word behind the outputs, for the host's copy
+    if (EPI == EPI_STORE && a.out_host && blockIdx.x == 0 && tid == 0)
+        reinterpret_cast<int *>(a.out_host)[a.units] = reinterpret_cast<const int *>(a.out)[a.units];
+
     // ---- 4. row groups: prefetch the next, compute the current ------------
     float best_v = -INFINITY;
     int best_i = INT_MAX;
@@ -292,6 +296,7 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
             if (EPI == EPI_STORE) {
                 const float o = a.bias ? mine[0] + pre : mine[0];
                 a.out[u] = o;
+                if (a.out_host) a.out_host[u] = o;
                 am_take(best_v, best_i, o, u);
             } else if (EPI == EPI_RESID) {
                 a.out[u] = pre + mine[0];
@@ -431,6 +436,7 @@ int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a) {
     const int K = a.W.cols;
     if (K % QB != 0 || K <= 0 || a.units <= 0) return -1;
     if (a.am_val && (epi != EPI_STORE || a.W.dtype == DT_F32)) return -1;
+    if (a.out_host && (epi != EPI_STORE || a.W.dtype == DT_F32)) return -1;
     int grid = -1;
     if (pro == PRO_NORM && epi == EPI_STORE) grid = pick_dt<PRO_NORM, EPI_STORE>(st, a);
     else if (pro == PRO_EMBED_NORM && epi == EPI_STORE) grid = pick_dt<PRO_EMBED_NORM, EPI_STORE>(st, a);

@@ -113,14 +113,18 @@ def oracle_lib(fast=False):
     return _cache[key]
 
 
-def reference_path(debug=True):
-    return os.path.join(HERE, "_ref", "libember_ref_debug.so" if debug else "libember_ref.so")
+def reference_path(debug=True, v4=False):
+    """debug: the `make debug` flags; else the optimized flags, built for
+    x86-64-v3 (AVX2) or, with v4, x86-64-v4 (AVX-512)."""
+    if debug:
+        return os.path.join(HERE, "_ref", "libember_ref_debug.so")
+    return os.path.join(HERE, "_ref", "libember_ref_v4.so" if v4 else "libember_ref.so")
 
 
-def reference_lib(debug=True):
-    key = "ref_debug" if debug else "ref"
+def reference_lib(debug=True, v4=False):
+    key = "ref_debug" if debug else ("ref_v4" if v4 else "ref")
     if key not in _cache:
-        _cache[key] = _load(reference_path(debug), _REF)
+        _cache[key] = _load(reference_path(debug, v4), _REF)
     return _cache[key]
 
 
@@ -200,8 +204,8 @@ class Oracle:
 class Reference:
     """One model + state of the compiled reference library."""
 
-    def __init__(self, path, ctx=0, kv_fp16=False, debug=True):
-        self.L = reference_lib(debug)
+    def __init__(self, path, ctx=0, kv_fp16=False, debug=True, v4=False):
+        self.L = reference_lib(debug, v4)
         self.m = self.L.ember_model_load(path.encode())
         if not self.m:
             raise RuntimeError(f"reference cannot open {path}")

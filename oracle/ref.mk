@@ -6,6 +6,9 @@
 #   _ref/libember_ref_debug.so  flags of `make debug` (Makefile:57-59)
 #   _ref/libember_ref.so        flags of the optimized build (Makefile:23),
 #                               -march=x86-64-v3 in place of -march=native
+#   _ref/libember_ref_v4.so     the same with -march=x86-64-v4 (AVX-512), for
+#                               hosts that have it (the build host's
+#                               -march=native need not match the GPU host)
 #   _ref/ember_cli              the reference's command-line program, every
 #                               source file, `make debug` flags (the CPU side
 #                               the product library's build of the same
@@ -21,7 +24,7 @@ SRC := $(filter-out $(REF)/src/main.c,$(wildcard $(REF)/src/*.c))
 COMMON = -std=c11 -D_DEFAULT_SOURCE -fPIC -shared -pthread -Wl,-Bsymbolic -w
 
 .PHONY: all
-all: _ref/libember_ref_debug.so _ref/libember_ref.so _ref/ember_cli _ref/ember_cli_o3
+all: _ref/libember_ref_debug.so _ref/libember_ref.so _ref/libember_ref_v4.so _ref/ember_cli _ref/ember_cli_o3
 
 _ref:
 	mkdir -p _ref
@@ -31,6 +34,9 @@ _ref/libember_ref_debug.so: $(SRC) | _ref
 
 _ref/libember_ref.so: $(SRC) | _ref
 	$(CC) $(COMMON) -O3 -ffast-math -march=x86-64-v3 -funroll-loops -o $@ $(SRC) -lm
+
+_ref/libember_ref_v4.so: $(SRC) | _ref
+	$(CC) $(COMMON) -O3 -ffast-math -march=x86-64-v4 -funroll-loops -o $@ $(SRC) -lm
 
 _ref/ember_cli: $(wildcard $(REF)/src/*.c) | _ref
 	$(CC) -std=c11 -D_DEFAULT_SOURCE -pthread -w -O2 -fno-fast-math -ffp-contract=off -o $@ $(wildcard $(REF)/src/*.c) -lm

@@ -21,11 +21,12 @@ Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings (and
 with an fp16 cache, and forced to the exact-order kernels), of 128 / 256 /
 200 tokens on the Qwen3 / Qwen2.5 / SmolLM2 shapes (default and exact-order
 attention), of the small variant models with the attention forced onto
-matrix cores; and a
-2-layer Qwen3-width model prefilling 2,300 tokens (one 2048-token pass with
-128-token MFMA tiles, then a 252-token pass at position 2048), also compared
-end to end with the oracle (logits, at the reference builds' own noise floor
-for that prefill, and every layer's KV rows).
+matrix cores; the second 2048-token pass of the Qwen3-0.6B shape's
+4096-token prefill; and a 2-layer Qwen3-width model prefilling 4,200 tokens
+(two 2048-token passes with 128-token MFMA tiles, then a 104-token pass at
+position 4096), also compared end to end with the oracle (logits, at the
+reference builds' own noise floor for that prefill, and every layer's KV
+rows).
 """
 import sys
 
@@ -97,8 +98,19 @@ def test_decode_kernels_two_kernel_merge(monkeypatch):
     assert ok, text
 
 
-def test_decode_kernels_fp16_cache():
-    ok, text = _decode_kernels("qwen3_06b", 1024, kv16=True)
+F16_DEPTHS = [("qwen3_06b", 1024), ("qwen3_06b", 4096), ("qwen3_06b", 6000), ("smollm2_135m", 4096)]
+
+
+@pytest.mark.parametrize("name,depth", F16_DEPTHS, ids=[f"{n}@{d}" for n, d in F16_DEPTHS])
+def test_decode_kernels_fp16_cache(name, depth):
+    """The fp16-cache attention, whose rows-per-chunk thresholds are twice the
+    fp32 ones (half the bytes per row): at the Qwen3-0.6B shape, depth 1024
+    gives the same 32 chunks of 33 rows as fp32, depth 4096 32 chunks of 129
+    rows (fp32: 64 of 65), depth 6000 32 chunks of 188 rows, more than a
+    workgroup's 160-row sizing (fp32: 64 of 94); the SmolLM2-135M shape at
+    4096 runs the 1-D grid whose kv heads share their XCD's slots, with
+    128-row chunks."""
+    ok, text = _decode_kernels(name, depth, kv16=True)
     assert ok, text
 
 
@@ -150,6 +162,16 @@ def test_prefill_kernels_512(name, kv16):
     assert ok, text
 
 
+def test_prefill_kernels_4096_second_pass():
+    """The headline's own 4096-token prefill, pass 1: 2048 tokens at position
+    2048 over a 4,096-row cache, on 128-token MFMA GEMM tiles and the
+    split-operand matrix-core attention over up to 4,096 keys (its K/V tile
+    images written by k_pf_kvsplit for the whole cache), at the Qwen3-0.6B
+    shape, first and last layer."""
+    ok, text = _prefill_kernels("qwen3_06b", 4096, [(0, 1), (27, 1)])
+    assert ok, text
+
+
 SHORT = [("qwen3_06b", 128, ""), ("qwen3_06b_q4", 128, ""), ("qwen25_05b", 256, ""), ("smollm2_135m", 200, ""),
          ("stories110m", 128, ""), ("qwen25_05b", 256, "exact"), ("smollm2_135m", 200, "exact")]
 
@@ -195,30 +217,33 @@ def test_prefill_kernels_matrix_cores_small(name, n, monkeypatch):
 
 
 @pytest.mark.parametrize("name", ["w_qwen3", "w_qwen3_q4"])
-def test_prefill_two_passes(name, oracle_threads):
-    """2,300 tokens: pass 0 (2048 tokens, 128-token-tile MFMA GEMMs, the
-    unsplit P.V kernel) and pass 1 (252 tokens at position 2048 over a
-    2,300-row cache), each layer's kernels checked; then the logits and every
-    layer's KV rows against the oracle's own prefill."""
-    ok, text = _prefill_kernels(name, 2300, [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_prefill_three_passes(name, oracle_threads):
+    """4,200 tokens: pass 0 (2048 tokens, 128-token-tile MFMA GEMMs), pass 1
+    (2048 tokens at position 2048 over a 4,096-row cache, as the headline's
+    4096-token prefill) and pass 2 (104 tokens at position 4096 over a
+    4,200-row cache, the short-prompt GEMM), each layer's kernels checked;
+    then the logits and every layer's KV rows, all 4,200 of them, against the
+    oracle's own prefill of the same ids."""
+    n = 4200
+    ok, text = _prefill_kernels(name, n, [(0, 0), (1, 0), (0, 1), (1, 1), (0, 2), (1, 2)])
     assert ok, text
     path = configs.model_path(name, threads=16)
     mf = kc.ModelFile(path)
-    ids = np.random.default_rng(2300).integers(0, mf.V, 2300)
-    say(f"{name}: 2,300-token prefill against the oracle")
-    eng = emberllm.Engine(path, ctx=2308)
-    orc = oracle.Oracle(path, ctx=2308)
+    ids = np.random.default_rng(n).integers(0, mf.V, n)
+    say(f"{name}: {n}-token prefill against the oracle")
+    eng = emberllm.Engine(path, ctx=n + 8)
+    orc = oracle.Oracle(path, ctx=n + 8)
     assert eng.prefill_pass_tokens() == 2048
     c = compare(eng.prefill(ids), orc.prefill(ids))
     # end to end, activation codes an ulp decides cascade (tests/parity.py):
     # held to the reference's own optimized-vs-deterministic deviation on this
-    # very prefill (noise_floor.json "<name>-p2300", 1.5e-2 relative L2)
-    say(f"{name} logits: " + check_run([c], f"{name}-p2300"))
+    # very prefill (noise_floor.json "<name>-p4200")
+    say(f"{name} logits: " + check_run([c], f"{name}-p{n}"))
     per_layer = orc.ctx * mf.kvd * 4
     for layer in range(mf.L):
         for which in (0, 1):
-            g = kc.cache_rows(eng.kv_read(which, layer, 2300), mf, False)
-            o = kc.cache_rows(orc.kv(which)[layer * per_layer:(layer + 1) * per_layer], mf, False)[:2300]
+            g = kc.cache_rows(eng.kv_read(which, layer, n), mf, False)
+            o = kc.cache_rows(orc.kv(which)[layer * per_layer:(layer + 1) * per_layer], mf, False)[:n]
             rows = np.linalg.norm(g - o, axis=1) / np.linalg.norm(o, axis=1)
             say(f"{name} layer {layer} {'KV'[which]} rows: median rel {np.median(rows):.1e}, max {rows.max():.1e}")
             if layer == 0:

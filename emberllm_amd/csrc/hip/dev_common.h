@@ -23,6 +23,7 @@ constexpr int WG = 256;     // threads per workgroup (4 wave64)
 // and another reads can stay in scratch memory; arrays of this type are kept
 // in registers.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int NWAVE = WG / 64;
 
 struct DMat {

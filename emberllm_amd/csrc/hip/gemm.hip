@@ -22,7 +22,6 @@ namespace ehip {
 // The row is staged in LDS with each 32-element block padded to QP floats,
 // so that the quantizing lanes' 16-byte reads of consecutive blocks spread
 // over the banks.  Element i lives at xs[lds_at(i)].
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int QP = 36;
 __device__ __forceinline__ int lds_at(int i) { return i + (i / QB) * (QP - QB); }
 

@@ -411,7 +411,9 @@ static int pick_nch(hipStream_t st, const MatvecArgs &a, size_t lds) {
     if (per_lane <= 2) return pick_upw<DT, PRO, EPI, 2>(st, a, lds);
     if (per_lane <= 3) return pick_upw<DT, PRO, EPI, 3>(st, a, lds);
     if (per_lane <= 5) return pick_upw<DT, PRO, EPI, 5>(st, a, lds);
-    if (DT == DT_Q8 && per_lane <= 8) return pick_upw<DT, PRO, EPI, 8>(st, a, lds);
+    if constexpr (DT == DT_Q8) {
+        if (per_lane <= 8) return pick_upw<DT, PRO, EPI, 8>(st, a, lds);
+    }
     return -1;
 }
 

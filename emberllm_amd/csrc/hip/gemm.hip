@@ -11,8 +11,14 @@
 // v_mfma_i32_32x32x32_i8 per 32-weight quant block, so each block's integer
 // dot product is exact and separately available; the fp32 epilogue of every
 // block applies the reference's order sum += ((float)isum * dw) * dx
-// (vecdot_q8 / vecdot_q4, kernels.c:151-183).  Roofline: the epilogue's four
-// VALU operations per output element and block bound it, not the MFMA rate.
+// (vecdot_q8 / vecdot_q4, kernels.c:151-183), or for products over at least
+// GEMM_SPLIT_MIN_K inputs (FUSED) sum = fma((float)isum, dw * dx, sum): one
+// rounding and one VALU operation fewer per output and block.  Those
+// products already split their block sums over pipelines elsewhere (the
+// short-prompt and decode products), so the models they belong to run at the
+// reference builds' own noise floor; the others keep the reference's order.
+// Roofline: the epilogue's VALU operations per output element and block
+// bound it, not the MFMA rate.
 // k_gemm (F32 weights): a 64 x 64 tile per workgroup, 4 x 4 micro-tiles per
 // thread, dot_f32 order.
 #include "kernels.h"
@@ -245,7 +251,7 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
-template <int DT, int EPI, int TT, int KB>
+template <int DT, int EPI, int TT, int KB, bool FUSED>
 __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
     constexpr int GM_KB = KB;
     constexpr int GM_T = TT, NY = TT / 64;            // tokens per tile, MFMA tiles per wave along tokens
@@ -266,8 +272,11 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
     constexpr int WLD = GM_U * WROW / 16 / WG, XLD = GM_T * XROW / 16 / WG;
     constexpr int NDW = GM_KB * GM_U / WG, NDX = (GM_KB * GM_T + WG - 1) / WG;   // scales per thread
     static_assert(GM_KB * GM_U % WG == 0, "weight scales per thread");
+    // Staging registers hold the loaded values untouched: a use of any of
+    // them here (such as converting a scale) would make the compiler wait for
+    // every load issued before it, exposing a memory round trip per stage.
     i32x4 wr[WLD], xr[XLD];   // native vectors: HIP's int4 struct kept these in scratch
-    float dwr[NDW], dxr[NDX]; int xsr[NDX];
+    uint16_t dwr[NDW]; float dxr[NDX]; int xsr[NDX];
     auto load = [&](int st) __attribute__((always_inline)) {
         const int b0 = st * GM_KB;
 #pragma unroll
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < NDW; i++) {
             const int f = tid + i * WG, kb = f / GM_U, r = f % GM_U;
-            dwr[i] = h2f(a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + min(b0 + kb, nb - 1)]);
+            dwr[i] = a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + min(b0 + kb, nb - 1)];
         }
 #pragma unroll
         for (int i = 0; i < NDX; i++) {
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < NDW; i++) {
             const int f = tid + i * WG;
-            dws[buf][f / GM_U][f % GM_U] = dwr[i];
+            dws[buf][f / GM_U][f % GM_U] = h2f(dwr[i]);
         }
 #pragma unroll
         for (int i = 0; i < NDX; i++) {
@@ -360,7 +369,8 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
                     for (int r = 0; r < 16; r++) {
                         const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
                         const float dw = dws[buf][kb][wu + 32 * x + mrow(r, h)];
-                        acc[x][y][r] += ((float)isum * dw) * dx;
+                        if (FUSED) acc[x][y][r] = fmaf((float)isum, dw * dx, acc[x][y][r]);
+                        else acc[x][y][r] += ((float)isum * dw) * dx;
                     }
                 }
         }
@@ -409,6 +419,8 @@ constexpr int GS_T = 32, GS_KB = 4;
 // blocks, and adds their sums in pipeline order at the end.  The waves'
 // serial walk over K (each block's product feeds the next block's sum) is
 // then a SPLIT-th as long, and SPLIT times as many waves share each SIMD.
+// The split products also apply each block as one fma (as k_gemm_mfma's
+// FUSED form): sum = fma((float)isum, dw * dx, sum).
 // FULL: every pipeline's block range is a whole number of stages (nb a
 // multiple of 4 * SPLIT), so no load needs clamping and no stage is partial:
 // the loads walk precomputed pointers and the epilogue has no tail test.
@@ -580,7 +592,8 @@ void k_gemm_small(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
-                acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+                if (SPLIT > 1) acc[r] = fmaf((float)isum, dw[kb][r] * dx[kb], acc[r]);
+                else acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
             }
         }
     };
@@ -1089,13 +1102,18 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         // 128-token tiles are as fast or faster)
         const bool t64 = (long)gu * ((a.n + 127) / 128) < 512;
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
-#define GMF(DT, TT)                                                                                     \
-        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2>), g, dim3(WG), 0, st, a); \
-        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2>), g, dim3(WG), 0, st, a); \
+#define GMK(DT, TT, FU)                                                                                 \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU>), g, dim3(WG), 0, st, a); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2, FU>), g, dim3(WG), 0, st, a); \
         else return -1;                                                                                 \
         return 0;
+#define GMF(DT, TT) if (fused) { GMK(DT, TT, true) } else { GMK(DT, TT, false) }
+        // products over at least GEMM_SPLIT_MIN_K inputs take the fused block
+        // scaling (see k_gemm_mfma)
+        const bool fused = a.W.cols >= GEMM_SPLIT_MIN_K;
         if (a.W.dtype == DT_Q8) { if (t64) { GMF(DT_Q8, 64) } else { GMF(DT_Q8, 128) } }
         if (t64) { GMF(DT_Q4, 64) } else { GMF(DT_Q4, 128) }
+#undef GMK
 #undef GMF
     }
     dim3 grid((a.units + TM - 1) / TM, (a.n + TN - 1) / TN);

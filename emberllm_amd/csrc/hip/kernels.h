@@ -112,7 +112,8 @@ size_t attn_kvimg_bytes(int hd, bool f16kv, int ctx, int n_kv);
 // (and the output's quantization) in one kernel
 constexpr int PF_FUSE_KEYS = 256;
 // products over at least GEMM_SPLIT_MIN_K inputs may split their block sums
-// over pipelines (prefill GEMM); shorter ones keep one sequential sum
+// over pipelines and fuse each block's scaling into one fma (prefill GEMM);
+// shorter ones keep one sequential sum in the reference's order
 constexpr int GEMM_SPLIT_MIN_K = 1024;
 inline int attn_prefill_ldk(int pos_base, int n_tok) { return (pos_base + n_tok + 3) & ~3; }
 // tile-maximum slots per prefill score row (64-key tiles, padded to 4)

@@ -304,6 +304,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill and kernel timings")
+    ap.add_argument("--no-api", action="store_true",
+                    help="profiling aid: skip the ember_forward protocol (ember bench and its ctypes form); "
+                         "the line's value is then the device loop's")
+    ap.add_argument("--no-cli", action="store_true",
+                    help="profiling aid: skip the ember bench program (its own process); the protocol runs "
+                         "through ctypes only")
     ap.add_argument("--sampled-only", action="store_true",
                     help="profiling aid: fill the cache to --depth, run only the device sampling loop "
                          "(T 0.8, top-k 40, top-p 0.9) and print its rate; no JSON line")
@@ -364,7 +370,7 @@ def main():
     log(f"model {path} ready in {time.time() - t0:.1f} s")
     # ---- the headline: ember bench over libember.so (its own process) -----
     cli = None
-    if not (args.prefill_only or args.sampled_only):
+    if not (args.prefill_only or args.sampled_only or args.no_cli or args.no_api):
         cli = cli_bench(path, depth, K, args.reps, args.kv == "f16")
     ctx = depth + max(K, W) + 2
     t = time.perf_counter()
@@ -437,12 +443,15 @@ def main():
         f"({ms / K * 1e3:.1f} us/step)")
 
     # ---- the ember bench protocol through ctypes ----------------------------
-    out["api_decode_tok_s"], out["api_decode_tok_s_sd"] = ctypes_bench(eng, depth, K, args.reps)
-    log(f"ember bench protocol via ctypes @{depth}: {out['api_decode_tok_s']:.1f} tok/s")
+    if not args.no_api:
+        out["api_decode_tok_s"], out["api_decode_tok_s_sd"] = ctypes_bench(eng, depth, K, args.reps)
+        log(f"ember bench protocol via ctypes @{depth}: {out['api_decode_tok_s']:.1f} tok/s")
     if cli:
         tok_s, tok_sd, harness = cli["decode"][0], cli["decode"][1], "ember bench (src/main.c) over libember.so"
-    else:
+    elif not args.no_api:
         tok_s, tok_sd, harness = out["api_decode_tok_s"], out["api_decode_tok_s_sd"], "ember bench protocol via ctypes"
+    else:
+        tok_s, tok_sd, harness = out["decode_tok_s_device_loop"], 0.0, "device greedy loop (--no-api)"
     ms_step = 1e3 / tok_s
     mean_bytes = float(np.mean([step_bytes(c, depth + i, e_kv) for i in range(K)]))
     log(f"decode @{depth} ({harness}): {tok_s:.1f} tok/s ({ms_step * 1e3:.1f} us/step), "
@@ -483,7 +492,7 @@ def main():
         out["decode_tok_s_sampled"] = sampled_rate()
     eng.close()
 
-    if not args.decode_only and depth != 128:
+    if not args.decode_only and not args.no_cli and depth != 128:
         # ---- depth 128: ember bench --pp 128 --------------------------------
         c128 = cli_bench(path, 128, K, args.reps, args.kv == "f16")
         if c128:
@@ -505,8 +514,9 @@ def main():
         "config": {"workload": f"{args.model}-shape decode of {K} tokens at depth {depth} after a "
                                f"{depth}-token batched prefill; {args.kv} KV cache",
                    "depth": depth, "kv": args.kv, "parallelism": "single GPU, single stream",
-                   "harness": f"{harness}: {reps} timed reps (after 1 warmup rep) of a pp{depth} prefill "
-                              f"then {K} ember_forward calls with host logits; value = mean of the reps' rates",
+                   "harness": (f"{harness}: {reps} timed reps (after 1 warmup rep) of a pp{depth} prefill "
+                               f"then {K} ember_forward calls with host logits; value = mean of the reps' rates")
+                              if not args.no_api else f"{harness}: {K} steps after {W} warmup steps",
                    "value_sd": round(tok_sd, 2)},
         "hbm_roofline_frac_step": round(tok_s * mean_bytes / HBM_PEAK, 4),
         "bytes_per_step": int(mean_bytes),

@@ -354,7 +354,7 @@ extern "C" EhipModel *ehip_model_upload(const EhipConfig *cfg, const EhipLayer *
 }
 
 // ---------------------------------------------------------------- state ----
-constexpr int PF_CHUNK = 2048;  // prefill tokens per pass through the layers (at most)
+constexpr int PF_CHUNK = 4096;  // prefill tokens per pass through the layers (at most)
 constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores per pass (at most)
 // Prefill attention in the reference's summation order (the exact-order
 // kernels) or on matrix cores (a running softmax over fp16 products of split

@@ -21,12 +21,12 @@ Qwen3-0.6B Q4_0 @512; prefill of 512 tokens on both Qwen3 encodings (and
 with an fp16 cache, and forced to the exact-order kernels), of 128 / 256 /
 200 tokens on the Qwen3 / Qwen2.5 / SmolLM2 shapes (default and exact-order
 attention), of the small variant models with the attention forced onto
-matrix cores; the second 2048-token pass of the Qwen3-0.6B shape's
-4096-token prefill; and a 2-layer Qwen3-width model prefilling 4,200 tokens
-(two 2048-token passes with 128-token MFMA tiles, then a 104-token pass at
-position 4096), also compared end to end with the oracle (logits, at the
-reference builds' own noise floor for that prefill, and every layer's KV
-rows).
+matrix cores; the Qwen3-0.6B shape's 4096-token prefill (one pass); and a
+2-layer Qwen3-width model prefilling 4,200 tokens (a 4096-token pass with
+128-token MFMA tiles, then a 104-token pass at position 4096; or two calls
+of 2,100 tokens, the second at start 2,100), also compared end to end with
+the oracle (logits, at the reference builds' own noise floor for that
+prefill, and every layer's KV rows).
 """
 import sys
 
@@ -114,24 +114,32 @@ def test_decode_kernels_fp16_cache(name, depth):
     assert ok, text
 
 
-def _prefill_kernels(name, n_prompt, captures, kv16=False, attention_only=False):
-    """Prefill n_prompt tokens once per (layer, pass) in `captures`, checking
-    that pass's kernels of that layer (or only its KV stores and attention:
-    the product checks do not cover F32 weights)."""
+def _prefill_kernels(name, n_prompt, captures, kv16=False, attention_only=False, split=0):
+    """Prefill n_prompt tokens once per (layer, pass[, call]) in `captures`,
+    checking that pass's kernels of that layer (or only its KV stores and
+    attention: the product checks do not cover F32 weights).  With `split`
+    the prompt goes in as two ember_prefill calls, tokens [0, split) and then
+    [split, n_prompt) at start = split; `call` picks the call captured."""
     path = configs.model_path(name, threads=16)
     mf = kc.ModelFile(path)
     rng = np.random.default_rng(n_prompt)
     ids = rng.integers(0, mf.V, n_prompt)
     eng = emberllm.Engine(path, ctx=n_prompt + 8, kv_fp16=kv16)
+    calls = [(0, split), (split, n_prompt)] if split else [(0, n_prompt)]
     lines, ok = [], True
-    for layer, pas in captures:
-        say(f"prefill kernels {name} n={n_prompt} layer {layer} pass {pas}")
-        eng.debug_capture_prefill(layer, pas)
-        eng.prefill(ids)
-        slots, pos0 = [], 0
-        for s in range(6):
-            rows, pos0 = eng.debug_read_prefill(s)
-            slots.append(rows)
+    for cap in captures:
+        layer, pas, ci = (cap + (0,))[:3]
+        say(f"prefill kernels {name} n={n_prompt} layer {layer} pass {pas} call {ci}")
+        for k, (a0, a1) in enumerate(calls):
+            if k == ci:
+                eng.debug_capture_prefill(layer, pas)
+            eng.prefill(ids[a0:a1], start=a0)
+            if k == ci:
+                slots, pos0 = [], 0
+                for s in range(6):
+                    rows, pos0 = eng.debug_read_prefill(s)
+                    slots.append(rows)
+                eng.debug_capture_prefill(-1, 0)
         n = slots[0].shape[0]
         k, v = layer_cache(eng, mf, layer, pos0 + n)
         rep = kc.Report(f"{name} prefill {n_prompt} pass {pas} (tokens {pos0}..{pos0 + n - 1}) kv16={kv16}")
@@ -162,13 +170,13 @@ def test_prefill_kernels_512(name, kv16):
     assert ok, text
 
 
-def test_prefill_kernels_4096_second_pass():
-    """The headline's own 4096-token prefill, pass 1: 2048 tokens at position
-    2048 over a 4,096-row cache, on 128-token MFMA GEMM tiles and the
-    split-operand matrix-core attention over up to 4,096 keys (its K/V tile
-    images written by k_pf_kvsplit for the whole cache), at the Qwen3-0.6B
-    shape, first and last layer."""
-    ok, text = _prefill_kernels("qwen3_06b", 4096, [(0, 1), (27, 1)])
+def test_prefill_kernels_4096():
+    """The headline's own 4096-token prefill, one pass over a 4,096-row cache:
+    128-token MFMA GEMM tiles with the fused block scaling, the 32 x 32 tiles
+    of wo and w2, and the split-operand matrix-core attention over 4,096 keys
+    (its K/V tile images written by k_pf_kvsplit), at the Qwen3-0.6B shape,
+    first and last layer."""
+    ok, text = _prefill_kernels("qwen3_06b", 4096, [(0, 0), (27, 0)])
     assert ok, text
 
 
@@ -216,25 +224,34 @@ def test_prefill_kernels_matrix_cores_small(name, n, monkeypatch):
     assert ok, text
 
 
-@pytest.mark.parametrize("name", ["w_qwen3", "w_qwen3_q4"])
-def test_prefill_three_passes(name, oracle_threads):
-    """4,200 tokens: pass 0 (2048 tokens, 128-token-tile MFMA GEMMs), pass 1
-    (2048 tokens at position 2048 over a 4,096-row cache, as the headline's
-    4096-token prefill) and pass 2 (104 tokens at position 4096 over a
-    4,200-row cache, the short-prompt GEMM), each layer's kernels checked;
-    then the logits and every layer's KV rows, all 4,200 of them, against the
-    oracle's own prefill of the same ids."""
+@pytest.mark.parametrize("name,split", [("w_qwen3", 0), ("w_qwen3_q4", 0), ("w_qwen3", 2100)],
+                         ids=["w_qwen3", "w_qwen3_q4", "w_qwen3-continued"])
+def test_prefill_long_passes(name, split, oracle_threads):
+    """4,200 tokens in one call: pass 0 (4096 tokens, 128-token-tile MFMA
+    GEMMs with the fused block scaling) and pass 1 (104 tokens at position
+    4096 over a 4,200-row cache, the short-prompt GEMM); or in two calls
+    (split): 2,100 tokens, then 2,100 more at start 2,100 over the first
+    call's cache rows (a long pass whose keys reach back before it).  Each
+    pass's kernels of both layers are checked; then the final logits and
+    every layer's KV rows, all 4,200 of them, against the oracle's own
+    prefill of the whole prompt in one call."""
     n = 4200
-    ok, text = _prefill_kernels(name, n, [(0, 0), (1, 0), (0, 1), (1, 1), (0, 2), (1, 2)])
+    caps = [(0, 0, 0), (1, 0, 0), (0, 0, 1), (1, 0, 1)] if split else [(0, 0), (1, 0), (0, 1), (1, 1)]
+    ok, text = _prefill_kernels(name, n, caps, split=split)
     assert ok, text
     path = configs.model_path(name, threads=16)
     mf = kc.ModelFile(path)
     ids = np.random.default_rng(n).integers(0, mf.V, n)
-    say(f"{name}: {n}-token prefill against the oracle")
+    say(f"{name}: {n}-token prefill{f' in two calls at {split}' if split else ''} against the oracle")
     eng = emberllm.Engine(path, ctx=n + 8)
     orc = oracle.Oracle(path, ctx=n + 8)
-    assert eng.prefill_pass_tokens() == 2048
-    c = compare(eng.prefill(ids), orc.prefill(ids))
+    assert eng.prefill_pass_tokens() == 4096
+    if split:
+        eng.prefill(ids[:split])
+        lg = eng.prefill(ids[split:], start=split)
+    else:
+        lg = eng.prefill(ids)
+    c = compare(lg, orc.prefill(ids))
     # end to end, activation codes an ulp decides cascade (tests/parity.py):
     # held to the reference's own optimized-vs-deterministic deviation on this
     # very prefill (noise_floor.json "<name>-p4200")

@@ -961,18 +961,25 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
 // scales nor lo planes: its values are fp16 already.
 //
 // k_pf_kvsplit converts the pass's keys once per layer: per (kv head, 64-key
-// tile) it writes the tile's LDS image (below) to HBM, so every row tile of
-// k_pf_flash16 stages a tile with plain 16-byte copies instead of converting
-// it again (at pp4096 each K/V row was otherwise converted by up to 32
-// workgroups).  The image, per tile:
-//   K planes [plane][row][dim] (pitch HD + 8 halves), key 32t + 8a + 4b + r
-//   at row 32t + 16b + 4a + r (fl_krow), so score product kk = 2t + b reads
-//   16 consecutive rows and lane quarter q receives keys 32t + 8q + 4b + r:
+// tile) it writes the tile's image (below) to HBM, and every row tile of
+// k_pf_flash16 copies it into LDS as it lies, with direct-to-LDS loads
+// (global_load_lds_dwordx4: a wave moves 1 KB of contiguous bytes without
+// passing them through registers), instead of converting the tile again (at
+// pp4096 each K/V row was otherwise converted by up to 32 workgroups).  The
+// image, per tile, unpadded: 16-byte pieces are XOR-swizzled within their row
+// by the row index, so the 16 rows a matrix-core operand read touches hit
+// distinct banks:
+//   K planes [plane][row][dim], key 32t + 8a + 4b + r at row
+//   32t + 16b + 4a + r (fl_krow), so score product kk = 2t + b reads 16
+//   consecutive rows and lane quarter q receives keys 32t + 8q + 4b + r:
 //   eight consecutive keys per lane and 32-key half tile;
-//   V^T planes [plane][dim][key] (pitch 72 halves): the P.V product over keys
+//   the per-key exponents of K and V (fp32 cache), int kex[64], vex[64];
+//   V^T planes [plane][dim][key] (rows of 64 keys): the P.V product over keys
 //   32t + 8q .. +7 (lane quarter q, element 4b + r) reads them as one 16-byte
-//   row piece, and the lane's own probabilities are its B operand;
-//   the per-key exponents of K and V (fp32 cache).
+//   row piece, and the lane's own probabilities are its B operand.
+// k_pf_flash16 stages the first two parts (K and exponents) and the V part
+// separately, each while the other is in use, so a tile's loads overlap the
+// previous tile's products.
 // Conversion: wave w takes key pairs 8w .. 8w + 7, lane l key pair
 // 8w + (l & 7) and dim quads (l >> 3) + 8c; a row's maximum is a reduction
 // over the eight lanes of its pair.  Keys past the pass's last repeat it.
@@ -996,34 +1003,24 @@ __device__ __forceinline__ uint32_t fl_pack(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// geometry of one (kv head, tile) image, in bytes.  The LDS layout pads the
-// plane rows (bank spread); the HBM image is the same data without the
-// padding, moved in 16-byte pieces: piece p of the HBM image lands at LDS
-// byte lds_at(p).
+// geometry of one (kv head, tile) image, in bytes; the LDS copy is the same
+// bytes at the same offsets (K and exponents in one array, V in another)
 template <int HD, bool F16> struct FlImg {
     static constexpr int NP = F16 ? 1 : 2;                 // planes: hi, and lo for an fp32 cache
-    static constexpr int KPH = HD + 8;                     // K plane pitch (halves): 16 rows' 16-byte reads on distinct banks
-    static constexpr int VPH = FL_BK + 8;                  // V^T plane pitch (halves)
-    static constexpr int KOFF = 0;
-    static constexpr int VOFF = KOFF + NP * FL_BK * KPH * 2;
-    static constexpr int EOFF = VOFF + NP * HD * VPH * 2;  // int kex[64], vex[64] (fp32 cache)
-    static constexpr int BYTES = EOFF + (F16 ? 0 : 2 * FL_BK * 4);     // LDS bytes
-    static constexpr int KP = NP * FL_BK * HD / 8;         // HBM pieces: K planes
-    static constexpr int VP = NP * HD * FL_BK / 8;         //             V^T planes
-    static constexpr int PIECES = KP + VP + (F16 ? 0 : 2 * FL_BK / 4);
-    static constexpr int HBYTES = 16 * PIECES;             // HBM bytes per image
-    static_assert(VOFF % 16 == 0 && EOFF % 16 == 0 && BYTES % 16 == 0, "16-byte pieces");
-    static __device__ __forceinline__ int lds_at(int p) {
-        if (p < KP) {   // K plane p / (64 HD/8), row (p / (HD/8)) % 64, piece p % (HD/8)
-            constexpr int RP = HD / 8;
-            return KOFF + 2 * KPH * (p / RP) + 16 * (p % RP);
-        }
-        if (p < KP + VP) {   // V^T plane, row, piece of 8 keys
-            const int v = p - KP;
-            return VOFF + 2 * VPH * (v / 8) + 16 * (v % 8);
-        }
-        return EOFF + 16 * (p - KP - VP);
-    }
+    static constexpr int KRB = 2 * HD;                     // K plane row bytes
+    static constexpr int KRP = HD / 8;                     // 16-byte pieces per K row
+    static constexpr int KBYTES = NP * FL_BK * KRB;        // K planes
+    static constexpr int EBYTES = F16 ? 0 : 2 * FL_BK * 4; // int kex[64], vex[64] (fp32 cache)
+    static constexpr int KE = KBYTES + EBYTES;             // first staging part
+    static constexpr int VBYTES = NP * HD * FL_BK * 2;     // V^T planes, 128-byte rows
+    static constexpr int HBYTES = KE + VBYTES;             // bytes per image
+    static constexpr int SLAB = 1024;                      // one wave's direct-to-LDS load
+    static constexpr int KE_SLABS = (KE + SLAB - 1) / SLAB, V_SLABS = VBYTES / SLAB;
+    static_assert(KE % 16 == 0 && VBYTES % SLAB == 0 && (KRP & (KRP - 1)) == 0, "image geometry");
+    // K row r (plane-major: plane * 64 + row), piece p
+    static __device__ __forceinline__ int k_at(int r, int p) { return r * KRB + 16 * (p ^ (r & (KRP - 1))); }
+    // V^T row d (plane-major: plane * HD + dim), piece p (keys 8p .. 8p + 7)
+    static __device__ __forceinline__ int v_at(int d, int p) { return d * 128 + 16 * (p ^ (d & 7)); }
 };
 
 size_t attn_kvimg_bytes(int hd, bool f16kv, int ctx, int n_kv) {
@@ -1040,11 +1037,9 @@ template <int HD, bool F16>
 __global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
     using I = FlImg<HD, F16>;
     constexpr int NC = HD / 32;         // dim quads per lane and key
-    constexpr int KPH = I::KPH, VPH = I::VPH;
-    __shared__ __align__(16) uint8_t img[I::BYTES];
-    _Float16 *ksm = reinterpret_cast<_Float16 *>(img + I::KOFF);
-    _Float16 *vsm = reinterpret_cast<_Float16 *>(img + I::VOFF);
-    int *kex = reinterpret_cast<int *>(img + I::EOFF), *vex = kex + FL_BK;
+    __shared__ __align__(16) uint8_t img[I::HBYTES];   // the image as it goes to HBM
+    uint8_t *vimg = img + I::KE;
+    int *kex = reinterpret_cast<int *>(img + I::KBYTES), *vex = kex + FL_BK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = blockIdx.x, kt = blockIdx.y;
     const int klast = a.pos_base + a.n_tok - 1;
@@ -1061,19 +1056,25 @@ __global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
                 kr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.kc) + off);
                 vr[j][c] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.vc) + off);
             }
+        // dim quad dq = dq0 + 8c is half (dq & 1) of piece dq >> 1 of its K row;
+        // keys 2kp, 2kp + 1 are word kp & 3 of piece kp >> 2 of a V^T row
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int c = 0; c < NC; c++)
-                *reinterpret_cast<uint2 *>(&ksm[fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c)]) = kr[j][c];
+            for (int c = 0; c < NC; c++) {
+                const int dq = dq0 + 8 * c;
+                *reinterpret_cast<uint2 *>(img + I::k_at(fl_krow(2 * kp + j), dq >> 1) + 8 * (dq & 1)) = kr[j][c];
+            }
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const int d0 = 4 * (dq0 + 8 * c);
-            uint32_t *vp = reinterpret_cast<uint32_t *>(&vsm[d0 * VPH + 2 * kp]);
-            vp[0] = (vr[0][c].x & 0xffffu) | (vr[1][c].x << 16);
-            vp[VPH / 2] = (vr[0][c].x >> 16) | (vr[1][c].x & 0xffff0000u);
-            vp[VPH] = (vr[0][c].y & 0xffffu) | (vr[1][c].y << 16);
-            vp[3 * VPH / 2] = (vr[0][c].y >> 16) | (vr[1][c].y & 0xffff0000u);
+            const int d0 = 4 * (dq0 + 8 * c), w = 4 * (kp & 3);
+            const uint32_t r4[4] = { (vr[0][c].x & 0xffffu) | (vr[1][c].x << 16),
+                                     (vr[0][c].x >> 16) | (vr[1][c].x & 0xffff0000u),
+                                     (vr[0][c].y & 0xffffu) | (vr[1][c].y << 16),
+                                     (vr[0][c].y >> 16) | (vr[1][c].y & 0xffff0000u) };
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                *reinterpret_cast<uint32_t *>(vimg + I::v_at(d0 + e, kp >> 2) + w) = r4[e];
         }
     } else {
         f32x4 kr[2][NC], vr[2][NC];
@@ -1114,9 +1115,11 @@ __global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
                     hi[e] = (_Float16)x;
                     lo[e] = (_Float16)(x - (float)hi[e]);
                 }
-                const int at = fl_krow(2 * kp + j) * KPH + 4 * (dq0 + 8 * c);
-                *reinterpret_cast<uint2 *>(&ksm[at]) = make_uint2(fl_pack(hi[0], hi[1]), fl_pack(hi[2], hi[3]));
-                *reinterpret_cast<uint2 *>(&ksm[FL_BK * KPH + at]) = make_uint2(fl_pack(lo[0], lo[1]), fl_pack(lo[2], lo[3]));
+                const int dq = dq0 + 8 * c, rk = fl_krow(2 * kp + j);
+                *reinterpret_cast<uint2 *>(img + I::k_at(rk, dq >> 1) + 8 * (dq & 1)) =
+                    make_uint2(fl_pack(hi[0], hi[1]), fl_pack(hi[2], hi[3]));
+                *reinterpret_cast<uint2 *>(img + I::k_at(FL_BK + rk, dq >> 1) + 8 * (dq & 1)) =
+                    make_uint2(fl_pack(lo[0], lo[1]), fl_pack(lo[2], lo[3]));
             }
 #pragma unroll
         for (int c = 0; c < NC; c++)
@@ -1126,33 +1129,57 @@ __global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
                 const float x1 = __builtin_amdgcn_ldexpf(vr[1][c][e], ev[1]);
                 const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
                 const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
-                const int at = (4 * (dq0 + 8 * c) + e) * VPH + 2 * kp;
-                *reinterpret_cast<uint32_t *>(&vsm[at]) = fl_pack(h0, h1);
-                *reinterpret_cast<uint32_t *>(&vsm[HD * VPH + at]) = fl_pack(l0, l1);
+                const int d = 4 * (dq0 + 8 * c) + e, w = 4 * (kp & 3);
+                *reinterpret_cast<uint32_t *>(vimg + I::v_at(d, kp >> 2) + w) = fl_pack(h0, h1);
+                *reinterpret_cast<uint32_t *>(vimg + I::v_at(HD + d, kp >> 2) + w) = fl_pack(l0, l1);
             }
     }
     __syncthreads();
-    // the image to HBM without the rows' padding
+    // the image to HBM as it lies
     u32x4 *dst = reinterpret_cast<u32x4 *>(a.kvimg + ((size_t)g * a.kvimg_tiles + kt) * I::HBYTES);
-    for (int p = tid; p < I::PIECES; p += WG) dst[p] = *reinterpret_cast<const u32x4 *>(img + I::lds_at(p));
+    for (int p = tid; p < I::HBYTES / 16; p += WG) dst[p] = *reinterpret_cast<const u32x4 *>(img + 16 * p);
 }
 
-// 64 rows per workgroup, two workgroups per CU: one's staging overlaps the
-// other's products (128 rows per workgroup, one per CU, measured slower)
+// s_waitcnt immediate that waits until at most n vector memory operations of
+// the wave are outstanding (expcnt and lgkmcnt left alone)
+constexpr int fl_vmcnt(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+// Workgroup barrier for the staging loop: this wave's LDS reads are done,
+// then s_barrier, with no fence (a workgroup fence would wait for every
+// vector memory operation, the next part's loads included; the loop waits for
+// the loads it needs with explicit vmcnt counts).  The empty asm statements
+// keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void fl_sync() {
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+// one 16-byte piece per lane from src into LDS at the wave-uniform base dst,
+// lane l's piece at dst + 16 l (global_load_lds_dwordx4)
+__device__ __forceinline__ void fl_load_lds(const uint8_t *src, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+}
+
+// 64 rows per workgroup, two workgroups per CU: one's barriers overlap the
+// other's products (128 rows per workgroup, one per CU, measured slower).
+// Per key tile, with its K part and exponents (kimg) and its V part (vimg)
+// staged separately by direct-to-LDS loads:
+//   scores from kimg, the exponents read; barrier; the next tile's K part
+//   issued into kimg; softmax; wait for this tile's V part; barrier; P.V from
+//   vimg; wait for the next K part; barrier; the next tile's V part issued.
+// Each part's loads land while the other part's products run.
 template <int HD, bool F16>
 __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     using I = FlImg<HD, F16>;
-    constexpr int NP = I::NP;
     constexpr int NQ = HD / 32;         // 32-dim steps of a score product
     constexpr int ND = HD / 16;         // 16-dim output products
-    constexpr int KPH = I::KPH, VPH = I::VPH;
-    constexpr int NT = WG, BR = FL_BR;                   // threads, rows per workgroup
-    constexpr int NPC = (I::PIECES + NT - 1) / NT;       // image pieces per thread
-    static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64, "tile shape");
-    __shared__ __align__(16) uint8_t img[I::BYTES];
-    const _Float16 *ksm = reinterpret_cast<const _Float16 *>(img + I::KOFF);
-    const _Float16 *vsm = reinterpret_cast<const _Float16 *>(img + I::VOFF);
-    const int *kex = reinterpret_cast<const int *>(img + I::EOFF), *vex = kex + FL_BK;
+    constexpr int BR = FL_BR;                            // rows per workgroup
+    constexpr int KE_N = (I::KE_SLABS + NWAVE - 1) / NWAVE, KE_MIN = I::KE_SLABS / NWAVE;   // K-part slabs per wave
+    constexpr int V_N = I::V_SLABS / NWAVE;
+    static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64 && I::V_SLABS % NWAVE == 0, "tile shape");
+    __shared__ __align__(16) uint8_t kimg[I::KE_SLABS * I::SLAB];   // K planes, exponents, slab padding
+    __shared__ __align__(16) uint8_t vimg[I::VBYTES];
+    const int *kex = reinterpret_cast<const int *>(kimg + I::KBYTES), *vex = kex + FL_BK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = lane & 15, q = lane >> 4;
     const int g = blockIdx.x;
@@ -1194,22 +1221,36 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     f32x4 o[ND];
 #pragma unroll
     for (int d = 0; d < ND; d++) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.kvimg + (size_t)g * a.kvimg_tiles * I::HBYTES);
+    // wave w moves slabs w, w + 4, ... of a part; the K part's last slab is
+    // partly past the image, and its lanes there re-read the last piece into
+    // kimg's padding
+    const uint8_t *gimg = a.kvimg + (size_t)g * a.kvimg_tiles * I::HBYTES;
+    auto stage_ke = [&](int kt) {
+        const uint8_t *src = gimg + (size_t)kt * I::HBYTES;
+#pragma unroll
+        for (int u = 0; u < KE_N; u++) {
+            const int sl = wave + NWAVE * u;
+            if (u < KE_MIN || sl < I::KE_SLABS)
+                fl_load_lds(src + min(sl * I::SLAB + 16 * lane, I::KE - 16), kimg + sl * I::SLAB);
+        }
+    };
+    auto stage_v = [&](int kt) {
+        const uint8_t *src = gimg + (size_t)kt * I::HBYTES + I::KE;
+#pragma unroll
+        for (int u = 0; u < V_N; u++) {
+            const int sl = wave + NWAVE * u;
+            fl_load_lds(src + sl * I::SLAB + 16 * lane, vimg + sl * I::SLAB);
+        }
+    };
+    stage_ke(0);
+    stage_v(0);
+    __builtin_amdgcn_s_waitcnt(fl_vmcnt(0));
+    __syncthreads();
 
     const int nkt = kend / FL_BK + 1;
     for (int kt = 0; kt < nkt; kt++) {
         const int k0 = kt * FL_BK;
-        {   // the tile's image: loads first, then the LDS stores
-            u32x4 pc[NPC];
-#pragma unroll
-            for (int u = 0; u < NPC; u++) pc[u] = src[min(tid + u * NT, I::PIECES - 1)];
-            src += I::PIECES;
-            __syncthreads();   // the previous tile has been read
-#pragma unroll
-            for (int u = 0; u < NPC; u++)
-                if (tid + u * NT < I::PIECES) *reinterpret_cast<u32x4 *>(img + I::lds_at(tid + u * NT)) = pc[u];
-            __syncthreads();
-        }
+        const bool more = kt + 1 < nkt;
 
         // ---- S'^T: sc[2t + b][r] = S'[row i][key k0 + 32t + 8q + 4b + r]
         f32x4 sc[4];
@@ -1220,8 +1261,8 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
             f16x8 kh[4], kl[4];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                kh[kk] = *reinterpret_cast<const f16x8 *>(&ksm[(16 * kk + i) * KPH + 32 * s + 8 * q]);
-                if constexpr (!F16) kl[kk] = *reinterpret_cast<const f16x8 *>(&ksm[(FL_BK + 16 * kk + i) * KPH + 32 * s + 8 * q]);
+                kh[kk] = *reinterpret_cast<const f16x8 *>(kimg + I::k_at(16 * kk + i, 4 * s + q));
+                if constexpr (!F16) kl[kk] = *reinterpret_cast<const f16x8 *>(kimg + I::k_at(FL_BK + 16 * kk + i, 4 * s + q));
             }
             if constexpr (!F16) {
 #pragma unroll
@@ -1248,6 +1289,10 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
                     vx[t][4 * u] = va.x; vx[t][4 * u + 1] = va.y; vx[t][4 * u + 2] = va.z; vx[t][4 * u + 3] = va.w;
                 }
             }
+        if (more) {   // every wave is past its kimg reads: the next tile's K part may land
+            fl_sync();
+            stage_ke(kt + 1);
+        }
         // running softmax of the row (log2 units); keys past the row's position are masked
         float mx = -INFINITY;
         int el = 1 << 20;   // the smallest V-row exponent among the row's visible keys of the tile
@@ -1284,14 +1329,19 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
                 ph[t][jj] = (_Float16)x;
                 pl[t][jj] = (_Float16)(x - (float)ph[t][jj]);
             }
+        if (kt > 0) {   // this tile's V part, issued before the next tile's K part
+            if (more) __builtin_amdgcn_s_waitcnt(fl_vmcnt(KE_MIN));
+            else __builtin_amdgcn_s_waitcnt(fl_vmcnt(0));
+            fl_sync();
+        }
         // ---- O''^T += V'^T . P''^T over keys 32t + 8q + jj
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             f16x8 vh[ND], vl[ND];
 #pragma unroll
             for (int d = 0; d < ND; d++) {
-                vh[d] = *reinterpret_cast<const f16x8 *>(&vsm[(16 * d + i) * VPH + 32 * t + 8 * q]);
-                if constexpr (!F16) vl[d] = *reinterpret_cast<const f16x8 *>(&vsm[(HD + 16 * d + i) * VPH + 32 * t + 8 * q]);
+                vh[d] = *reinterpret_cast<const f16x8 *>(vimg + I::v_at(16 * d + i, 4 * t + q));
+                if constexpr (!F16) vl[d] = *reinterpret_cast<const f16x8 *>(vimg + I::v_at(HD + 16 * d + i, 4 * t + q));
             }
             if constexpr (!F16) {
 #pragma unroll
@@ -1301,6 +1351,11 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
             for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[d], pl[t], o[d], 0, 0, 0);
 #pragma unroll
             for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[d], ph[t], o[d], 0, 0, 0);
+        }
+        if (more) {   // the next K part has landed and every wave is past its vimg reads
+            __builtin_amdgcn_s_waitcnt(fl_vmcnt(0));
+            fl_sync();
+            stage_v(kt + 1);
         }
     }
     // o[d][r] = 2^(14 + ecur) O^T[dim 16d + 4q + r][row i]

@@ -1140,6 +1140,8 @@ __global__ __launch_bounds__(WG) void k_pf_kvsplit(AttnArgs a) {
     for (int p = tid; p < I::HBYTES / 16; p += WG) dst[p] = *reinterpret_cast<const u32x4 *>(img + 16 * p);
 }
 
+template <bool B> struct FlMask { static constexpr bool value = B; };
+
 // s_waitcnt immediate that waits until at most n vector memory operations of
 // the wave are outstanding (expcnt and lgkmcnt left alone)
 constexpr int fl_vmcnt(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
@@ -1189,6 +1191,7 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     const int b = R / G, h = R % G;
     const int pos = a.pos_base + b;                       // keys [0, pos] are visible to the row
     const int kend = a.pos_base + (min(r0 + BR, nrows) - 1) / G;   // the workgroup's last visible key
+    const int kfirst = a.pos_base + r0 / G;   // keys [0, kfirst] are visible to every row of the workgroup
 
     // the Q row: lane quarter q holds dims 32s + 8q .. + 7 of step s
     f16x8 qh[NQ], ql[NQ];
@@ -1293,20 +1296,30 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
             fl_sync();
             stage_ke(kt + 1);
         }
-        // running softmax of the row (log2 units); keys past the row's position are masked
+        // running softmax of the row (log2 units); keys past the row's position
+        // are masked (only in tiles that reach past the workgroup's first row)
         float mx = -INFINITY;
         int el = 1 << 20;   // the smallest V-row exponent among the row's visible keys of the tile
+        auto scores = [&](auto masked) {
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++)
+            for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = kk >> 1, jj = 4 * (kk & 1) + r;
-                const bool vis = k0 + 32 * t + 8 * q + jj <= pos;
-                const float v = vis ? __builtin_amdgcn_ldexpf(sc[kk][r], -(eq + kx[t][jj])) * sscale : -INFINITY;
-                sc[kk][r] = v;
-                mx = fmaxf(mx, v);
-                if (vis) el = min(el, vx[t][jj]);
-            }
+                for (int r = 0; r < 4; r++) {
+                    const int t = kk >> 1, jj = 4 * (kk & 1) + r;
+                    float v = __builtin_amdgcn_ldexpf(sc[kk][r], -(eq + kx[t][jj])) * sscale;
+                    if constexpr (decltype(masked)::value) {
+                        const bool vis = k0 + 32 * t + 8 * q + jj <= pos;
+                        v = vis ? v : -INFINITY;
+                        if (vis) el = min(el, vx[t][jj]);
+                    } else {
+                        el = min(el, vx[t][jj]);
+                    }
+                    sc[kk][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+        };
+        if (k0 + FL_BK - 1 <= kfirst) scores(FlMask<false>{});
+        else scores(FlMask<true>{});
         const float mn = fmaxf(m, fl_quarter_max(mx));   // finite: key 0 is in the first tile
         const float alpha = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first tile (m = -inf)
         m = mn;

@@ -1101,8 +1101,15 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         // 64-token tiles while 128-token tiles give fewer than two
         // workgroups per CU (the epilogue's dependent chains want the waves:
         // Qwen3-0.6B-shape pp1024 6.64 -> 6.23 ms; from 512 workgroups on the
-        // 128-token tiles are as fast or faster)
-        const bool t64 = (long)gu * ((a.n + 127) / 128) < 512;
+        // 128-token tiles are as fast or faster), and when they fill whole
+        // rounds of the GPU's workgroup slots where 128-token tiles would not:
+        // a 256-CU part holds 3 of those per CU (166 VGPRs) and 4 of these
+        // (110), so a 4096-token q|k|v product (1,024 or 2,048 workgroups)
+        // runs two full rounds of 64-token tiles instead of one and a third
+        // (pp4096 19.95 -> 19.55 ms)
+        const long g128 = (long)gu * ((a.n + 127) / 128), gt64 = (long)gu * ((a.n + 63) / 64);
+        auto fill = [](long g, long slots) { return (double)g / (double)(((g + slots - 1) / slots) * slots); };
+        const bool t64 = g128 < 512 || fill(gt64, 4 * 256) > fill(g128, 3 * 256) + 0.1;
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
 #define GMK(DT, TT, FU)                                                                                 \
         if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU>), g, dim3(WG), 0, st, a); \

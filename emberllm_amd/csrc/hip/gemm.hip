@@ -246,26 +246,35 @@ __global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
 // Output (i, j) of an MFMA tile sits in lane j + 32*((i/4)%2), accumulator
 // (i%4) + 4*(i/8); A fragments hold W[u][16h .. 16h+15] of one block, B
 // fragments X[t][16h .. 16h+15], h = lane / 32.
+// SP = 2 (fused block scaling, Q8_0, 64-token tiles): two such pipelines of
+// 256 threads side by side in one workgroup, pipeline p over the p-th half of
+// the blocks, their sums added in pipeline order at the end (through LDS):
+// twice the waves per SIMD for grids of at most two workgroups per CU.
 constexpr int GM_U = 128;
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
-template <int DT, int EPI, int TT, int KB, bool FUSED>
-__global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
+template <int DT, int EPI, int TT, int KB, bool FUSED, int SP>
+__global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
     constexpr int GM_KB = KB;
     constexpr int GM_T = TT, NY = TT / 64;            // tokens per tile, MFMA tiles per wave along tokens
     constexpr int WB = DT == DT_Q8 ? 32 : 16;          // weight bytes per row and block
     constexpr int WROW = GM_KB * WB, XROW = GM_KB * 32; // stage bytes per row
     static_assert(TT == 64 || TT == 128, "token tile of 64 or 128");
-    __shared__ __align__(16) uint8_t ws[2][GM_U * WROW];
-    __shared__ __align__(16) int8_t xsm[2][GM_T * XROW];
-    __shared__ float dws[2][GM_KB][GM_U], dxs[2][GM_KB][GM_T];
-    __shared__ int sxs[2][GM_KB][GM_T];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert(SP == 1 || (SP == 2 && FUSED && TT == 64 && DT == DT_Q8), "split pipelines: fused Q8_0, 64-token tiles");
+    __shared__ __align__(16) uint8_t wsp[SP][2][GM_U * WROW];
+    __shared__ __align__(16) int8_t xsp[SP][2][GM_T * XROW];
+    __shared__ float dwp[SP][2][GM_KB][GM_U], dxp[SP][2][GM_KB][GM_T];
+    __shared__ int sxp[SP][2][GM_KB][GM_T];
+    const int tid = SP == 1 ? (int)threadIdx.x : (int)threadIdx.x % WG, pl = SP == 1 ? 0 : (int)threadIdx.x / WG;
+    const int lane = tid & 63, wave = tid >> 6;
+    auto &ws = wsp[pl]; auto &xsm = xsp[pl]; auto &dws = dwp[pl]; auto &dxs = dxp[pl]; auto &sxs = sxp[pl];
     const int j = lane & 31, h = lane >> 5;
     const int u0 = blockIdx.x * GM_U, t0 = blockIdx.y * GM_T;
-    const int K = a.W.cols, nb = K / QB, nst = (nb + GM_KB - 1) / GM_KB;
+    // pipeline pl: blocks [bp0, bp0 + nbp); pipeline 0 has the most stages
+    const int K = a.W.cols, nb = K / QB, nbh = SP == 1 ? nb : ((nb + 1) / 2 + GM_KB - 1) / GM_KB * GM_KB;
+    const int bp0 = pl * nbh, nbp = min(nb, bp0 + nbh) - bp0, nst = (nbh + GM_KB - 1) / GM_KB;
     const int wu = (wave & 1) * 64, wt = (wave >> 1) * (TT / 2);   // this wave's 64 x TT/2 corner
 
     // global -> registers for one stage: weights (WROW bytes per row), codes, scales
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
     i32x4 wr[WLD], xr[XLD];   // native vectors: HIP's int4 struct kept these in scratch
     uint16_t dwr[NDW]; float dxr[NDX]; int xsr[NDX];
     auto load = [&](int st) __attribute__((always_inline)) {
-        const int b0 = st * GM_KB;
+        const int b0 = bp0 + st * GM_KB;
 #pragma unroll
         for (int i = 0; i < WLD; i++) {
             const int f = tid + i * WG, row = f / (WROW / 16), c = (f % (WROW / 16)) * 16;
@@ -341,7 +350,7 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
         if (st + 1 < nst) load(st + 1);
 #pragma unroll
         for (int kb = 0; kb < GM_KB; kb++) {
-            if (st * GM_KB + kb >= nb) break;
+            if (st * GM_KB + kb >= nbp) break;
             i32x4 af[2], bf[NY];
 #pragma unroll
             for (int x = 0; x < 2; x++) {      // weight rows wu + 32x + j, k-half h
@@ -379,6 +388,26 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(GemmArgs a) {
             store(buf ^ 1);
             __syncthreads();
         }
+    }
+    if constexpr (SP == 2) {   // pipeline 1's sums through the (now free) weight stages
+        static_assert(2 * NY * 16 * WG * 4 <= (int)sizeof(wsp), "exchange fits the stages");
+        float *xch = reinterpret_cast<float *>(&wsp[0][0][0]);
+        if (pl == 1) {
+#pragma unroll
+            for (int x = 0; x < 2; x++)
+#pragma unroll
+                for (int y = 0; y < NY; y++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) xch[((x * NY + y) * 16 + r) * WG + tid] = acc[x][y][r];
+        }
+        __syncthreads();
+        if (pl == 1) return;
+#pragma unroll
+        for (int x = 0; x < 2; x++)
+#pragma unroll
+            for (int y = 0; y < NY; y++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[x][y][r] += xch[((x * NY + y) * 16 + r) * WG + tid];
     }
 #pragma unroll
     for (int x = 0; x < 2; x++)
@@ -1111,15 +1140,19 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         auto fill = [](long g, long slots) { return (double)g / (double)(((g + slots - 1) / slots) * slots); };
         const bool t64 = g128 < 512 || fill(gt64, 4 * 256) > fill(g128, 3 * 256) + 0.1;
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
-#define GMK(DT, TT, FU)                                                                                 \
-        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU>), g, dim3(WG), 0, st, a); \
-        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2, FU>), g, dim3(WG), 0, st, a); \
+        // products over at least GEMM_SPLIT_MIN_K inputs take the fused block
+        // scaling (see k_gemm_mfma), and Q8_0 64-token grids of at most two
+        // workgroups per CU split K over two pipelines (Qwen3-0.6B shape:
+        // pp512 3.93 -> 3.78 ms, pp1024 5.85 -> 5.78, pp4096 18.81 -> 18.72)
+        const bool fused = a.W.cols >= GEMM_SPLIT_MIN_K;
+        const bool sp2 = fused && t64 && gt64 <= 2 * 256;
+#define GMK(DT, TT, FU, SP)                                                                             \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); \
         else return -1;                                                                                 \
         return 0;
-#define GMF(DT, TT) if (fused) { GMK(DT, TT, true) } else { GMK(DT, TT, false) }
-        // products over at least GEMM_SPLIT_MIN_K inputs take the fused block
-        // scaling (see k_gemm_mfma)
-        const bool fused = a.W.cols >= GEMM_SPLIT_MIN_K;
+#define GMF(DT, TT) if (fused) { GMK(DT, TT, true, 1) } else { GMK(DT, TT, false, 1) }
+        if (a.W.dtype == DT_Q8 && sp2) { GMK(DT_Q8, 64, true, 2) }
         if (a.W.dtype == DT_Q8) { if (t64) { GMF(DT_Q8, 64) } else { GMF(DT_Q8, 128) } }
         if (t64) { GMF(DT_Q4, 64) } else { GMF(DT_Q4, 128) }
 #undef GMK

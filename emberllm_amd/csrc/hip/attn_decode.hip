@@ -129,10 +129,12 @@ template <int HD, bool F16> struct DecLay {
 // XMODE: 0 = chunk partials for k_attn_merge; 1 = in-kernel merge on the
 // 2-D grid (n_kv a multiple of 8: chunk c of kv head g is workgroup
 // g + n_kv c, max_chunks = 8 xm_slots / n_kv); 2 = in-kernel merge on the
-// 1-D grid of 8 * xm_slots.
+// 1-D grid of 8 * xm_slots; 3 = mode 1 with the wo product folded in (every
+// workgroup of kv head g, on g's XCD, waits for the merged o_g and computes
+// its wo_rows rows of the group's wo partial: see AttnArgs::wo).
 template <int HD, int GM, bool F16, int NL, int NW, int XMODE>
 __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
-    constexpr bool XM = XMODE != 0;
+    constexpr bool XM = XMODE != 0, FW = XMODE == 3;
     using L = DecLay<HD, F16>;
     constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL;
     constexpr int NT = NW * 64, RPB = NW * RPL;   // threads, rows per workgroup load
@@ -164,315 +166,88 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     }
     const int G = a.n_heads / a.n_kv;
     const int xcc_want = XM ? a.xm_xcc[g] : 0;
-    const int j = lane % LPR, rw = lane / LPR;
-    const bool pj = j < P;
-    const int jc = pj ? j : P - 1;   // clamped piece index for loads
-    const int qd = a.n_heads * HD;
-    const size_t hoff = (size_t)g * HD;
-    // ---- 1. loads: the token's q heads / k / v pieces and the QK-norm
-    // weights first (they do not depend on the position, so their round trip
-    // overlaps the one that reads it), then the position-dependent RoPE row
-    // and the first K/V batch ------------------------------------------------
-    float qv[GM][PE], kn[PE], vn[PE], qw[PE], kw[PE];
-    float2 cs[PE];
-#pragma unroll
-    for (int h = 0; h < GM; h++)
-        load_floats<PE>(qv[h], a.q + ((size_t)g * G + min(h, G - 1)) * HD + jc * PE);
-    load_floats<PE>(kn, a.q + qd + hoff + jc * PE);
-    load_floats<PE>(vn, a.q + qd + a.kv_dim + hoff + jc * PE);
-    if (a.q_norm) {
-        load_floats<PE>(qw, a.q_norm + jc * PE);
-        load_floats<PE>(kw, a.k_norm + jc * PE);
+    // FW: this thread's 16 wo codes (row fw_r of the workgroup's wo_rows,
+    // 16-byte chunk fw_j of the group's G * HD columns) and their block
+    // scale, loaded before anything else (they depend on nothing)
+    constexpr int CPR = GM * HD / 16;   // chunks per wo row (G == GM)
+    const int fw_r = tid / CPR, fw_j = tid % CPR;
+    const int fw_row = c * a.wo_rows + fw_r;
+    int4 fw_q = make_int4(0, 0, 0, 0);
+    uint16_t fw_d = 0;
+    if constexpr (FW) {
+        const int rc = min(c * a.wo_rows + min(fw_r, a.wo_rows - 1), a.wo.rows - 1);
+        const int col0 = g * G * HD;
+        fw_q = *reinterpret_cast<const int4 *>(a.wo.q + (size_t)rc * a.wo.cols + col0 + 16 * fw_j);
+        fw_d = a.wo.d[(size_t)rc * (a.wo.cols / QB) + col0 / QB + fw_j / 2];
     }
-    const int pos = a.tokpos[1];
-    // rows [0, pos] split into equal chunks over the kv head's workgroups
-    // (one per CU while chunks stay short, then two), at least ATT_DEC_RMIN rows each
-    const int R = dec_chunk_rows(pos, nchunk, F16);
-    const int nc = (pos + 1 + R - 1) / R;
-    if (c >= nc) return;
-    const int t0 = c * R, t1 = min(pos + 1, t0 + R);
-    const bool neox = a.rope_style == ROPE_NEOX;
-
-    {
-        const float2 *rp = a.rope + (size_t)pos * (HD / 2);
-        const int i0 = neox ? (jc % (P / 2)) * PE : jc * (PE / 2);
-#pragma unroll
-        for (int e = 0; e < PE; e += 2) {
-            const float4 f = *reinterpret_cast<const float4 *>(rp + i0 + min(e, neox ? PE - 2 : PE / 2 - 2));
-            cs[e] = make_float2(f.x, f.y);
-            cs[e + 1] = make_float2(f.z, f.w);
-        }
-    }
-    uint4 kr[NL], vr[NL];
-    auto load_batch = [&](int tb) {   // K rows first, then V rows
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int t = min(tb + i * RPB + wave * RPL + rw, t1 - 1);
-            const size_t off = (size_t)t * a.kv_dim + hoff + (size_t)jc * PE;
-            kr[i] = F16 ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.kc) + off)
-                        : *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.kc) + off);
-        }
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int t = min(tb + i * RPB + wave * RPL + rw, t1 - 1);
-            const size_t off = (size_t)t * a.kv_dim + hoff + (size_t)jc * PE;
-            vr[i] = F16 ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.vc) + off)
-                        : *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.vc) + off);
+    // FW: o_g is complete in this XCD's L2: raise the group's flag
+    auto raise = [&]() {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            if (xcc_id() != xcc_want) __hip_atomic_fetch_or(a.xm_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.wo_flag + g * XM_CNT_STRIDE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     };
-    load_batch(t0);
 
-    // ---- 2. QK-norm (model.c:386-389, after bias, before RoPE) and RoPE
-    // (model.c:66-80) of the group's q heads and of k, in registers --------
-    auto head_norm = [&](float (&v)[PE], const float (&w)[PE]) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int e = 0; e < PE; e++) ss += v[e] * v[e];
-        ss = group_sum<LPR>(pj ? ss : 0.0f);
-        const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-        for (int e = 0; e < PE; e++) v[e] = v[e] * scale * w[e];
-    };
-    const int partner = lane - j + (jc + P / 2) % P;
-    const bool low = j < P / 2;
-    auto rope = [&](float (&v)[PE]) {
-        if (neox) {   // pairs (i, i + hd/2): the partner piece is P/2 lanes away
-#pragma unroll
-            for (int e = 0; e < PE; e++) {
-                const float pv = __shfl(v[e], partner);
-                v[e] = low ? v[e] * cs[e].x - pv * cs[e].y : pv * cs[e].y + v[e] * cs[e].x;
-            }
-        } else {      // pairs (2i, 2i + 1) inside the piece
-#pragma unroll
-            for (int e = 0; e < PE; e += 2) {
-                const float v0 = v[e], v1 = v[e + 1];
-                const float2 r = cs[e / 2];
-                v[e] = v0 * r.x - v1 * r.y;
-                v[e + 1] = v0 * r.y + v1 * r.x;
-            }
-        }
-    };
-    if (a.q_norm) {
-#pragma unroll
-        for (int h = 0; h < GM; h++) head_norm(qv[h], qw);
-        head_norm(kn, kw);
-    }
-#pragma unroll
-    for (int h = 0; h < GM; h++) rope(qv[h]);
-    rope(kn);
-    if (F16) {   // the cache holds fp16 (model.c:39-48): attend to the rounded values
-#pragma unroll
-        for (int e = 0; e < PE; e++) { kn[e] = h2f(f2h(kn[e])); vn[e] = h2f(f2h(vn[e])); }
-    }
-    if (c == nc - 1 && wave == 0 && rw == 0 && pj) {   // the chunk holding `pos` stores its row
-        const size_t off = (size_t)pos * a.kv_dim + hoff + (size_t)j * PE;
-        if constexpr (F16) {
-            uint32_t pk[PE / 2], pv[PE / 2];
-#pragma unroll
-            for (int e = 0; e < PE / 2; e++) {
-                pk[e] = (uint32_t)f2h(kn[2 * e]) | ((uint32_t)f2h(kn[2 * e + 1]) << 16);
-                pv[e] = (uint32_t)f2h(vn[2 * e]) | ((uint32_t)f2h(vn[2 * e + 1]) << 16);
-            }
-            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.kc) + off) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.vc) + off) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
-        } else {
-            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(a.kc) + off) = make_float4(kn[0], kn[1], kn[2], kn[3]);
-            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(a.vc) + off) = make_float4(vn[0], vn[1], vn[2], vn[3]);
-        }
+    if constexpr (FW) {
+        auto attend = [&]() {
+#include "attn_decode_body.inc"
+        };
+        attend();
+    } else {
+#include "attn_decode_body.inc"
+        return;
     }
 
-    // ---- 3. batches of BR rows: the next batch's loads are issued before the
-    // current batch's scores; a running (max, sum, output) per wave.  Scores
-    // are in log2 units (scaled by log2(e)/sqrt(hd)), so a probability is one
-    // v_exp_f32. ------------------------------------------------------------
-    const float sscale = a.inv_sqrt * LOG2E;
-    float m[GM], l[GM], o[GM][PE];
-#pragma unroll
-    for (int h = 0; h < GM; h++) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < PE; e++) o[h][e] = 0.0f;
-    }
-    for (int tb = t0; tb < t1; tb += BR) {
-        uint4 kc[NL], vc[NL];
-#pragma unroll
-        for (int i = 0; i < NL; i++) { kc[i] = kr[i]; vc[i] = vr[i]; }
-        if (tb + BR < t1) load_batch(tb + BR);
-        float sc[NL][GM];
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int t = tb + i * RPB + wave * RPL + rw;
-            float kf[PE];
-            if (t == pos) {
-#pragma unroll
-                for (int e = 0; e < PE; e++) kf[e] = kn[e];
-            } else {
-                piece_to_float<F16>(kc[i], kf);
-            }
-#pragma unroll
-            for (int h = 0; h < GM; h++) {
-                float sv = qv[h][0] * kf[0];
-#pragma unroll
-                for (int e = 1; e < PE; e++) sv = fmaf(qv[h][e], kf[e], sv);
-                sc[i][h] = group_sum<LPR>(pj ? sv : 0.0f) * sscale;
-            }
-        }
-        float mn[GM];
-#pragma unroll
-        for (int h = 0; h < GM; h++) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < NL; i++)
-                if (tb + i * RPB + wave * RPL + rw < t1) mx = fmaxf(mx, sc[i][h]);
-            mn[h] = fmaxf(m[h], stride_max<LPR>(mx));
-            const float r = m[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[h] - mn[h]);
-            l[h] *= r;
-#pragma unroll
-            for (int e = 0; e < PE; e++) o[h][e] *= r;
-            m[h] = mn[h];
-        }
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int t = tb + i * RPB + wave * RPL + rw;
-            if (t >= t1) continue;
-            float vf[PE];
-            if (t == pos) {
-#pragma unroll
-                for (int e = 0; e < PE; e++) vf[e] = vn[e];
-            } else {
-                piece_to_float<F16>(vc[i], vf);
-            }
-#pragma unroll
-            for (int h = 0; h < GM; h++) {
-                const float p = __builtin_amdgcn_exp2f(sc[i][h] - m[h]);
-                l[h] += p;
-#pragma unroll
-                for (int e = 0; e < PE; e++) o[h][e] = fmaf(p, vf[e], o[h][e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < GM; h++) {
-        l[h] = stride_sum<LPR>(l[h]);
-#pragma unroll
-        for (int e = 0; e < PE; e++) o[h][e] = stride_sum<LPR>(o[h][e]);
-        if (rw == 0 && pj && h < G)
-#pragma unroll
-            for (int e = 0; e < PE; e++) sm_o[wave][h][j * PE + e] = o[h][e];
-        if (lane == 0 && h < G) { sm_m[wave][h] = m[h]; sm_l[wave][h] = l[h]; }
-    }
-    __syncthreads();
-
-    // ---- 4. combine the waves; publish or write ----------------------------
-    // Partials: o at part[head][chunk][HD], (m, l) at part_ml[head][chunk][2],
-    // m in log2 units.
-    const size_t head0 = (size_t)g * G;   // first query head of the group
-    float *part_ml = a.part + (size_t)a.n_heads * a.max_chunks * HD;
-    for (int i = tid; i < G * HD; i += NT) {
-        const int h = i / HD, d = i % HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_m[w][h]);
-        float O = 0.0f, S = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float mw = sm_m[w][h];
-            const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            O = fmaf(f, sm_o[w][h][d], O);
-            S = fmaf(f, sm_l[w][h], S);
-        }
-        if (nc == 1) {
-            a.out[(head0 + h) * HD + d] = O * (1.0f / S);
-        } else {
-            const size_t slot = (head0 + h) * a.max_chunks + c;
-            a.part[slot * HD + d] = O;
-            if (d == 0) { part_ml[2 * slot] = M; part_ml[2 * slot + 1] = S; }
-        }
-    }
-    if (!XM || nc == 1) return;
-
-    // ---- 5. the last chunk of this kv head to finish merges through L2 ------
-    // Every workgroup of kv head g runs on XCD a.xm_xcc[g]: its partial
-    // stores are complete in that L2 after the wait, the counter lives in the
-    // same L2 (workgroup-scope atomics are performed there), and the last
-    // arriver's loads of the partials hit it (its L1 has never held them).
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // ---- 6. (FW) the group's wo partial ------------------------------------
+    // Wait for the flag (a bounded wait: on time-out the error flag sends the
+    // host to the two-kernel schedule), then quantize o_g as k_matvec's
+    // PRO_PLAIN prologue does (the same codes and fp16-rounded scales) and
+    // take this workgroup's rows in k_matvec's block order per lane:
+    // ((float)isum * dw) * dx, summed over the row's lanes.
+    __shared__ int sm_go;
+    __shared__ __align__(16) int sm_qx[GM * HD / 4];
+    __shared__ float sm_dx[GM * HD / QB];
     if (tid == 0) {
         if (xcc_id() != xcc_want) __hip_atomic_fetch_or(a.xm_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int old = __hip_atomic_fetch_add(a.xm_cnt + g * XM_CNT_STRIDE, 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_WORKGROUP);
-        sm_last = old == nc - 1;
-    }
-    __syncthreads();
-    if (!sm_last) return;
-    // o = sum_k o_k 2^(m_k - M) / sum_k l_k 2^(m_k - M),  M = max_k m_k;
-    // thread (s, h, q) owns float4 q of head h and chunks s, s + NSL, ...
-    // (one wave per (s, h) when GM * QPR = 64, so its chunk loop is uniform),
-    // merged online in rounds of KB chunks whose loads are all in flight
-    const int u = tid % (GM * QPR), hh = u / QPR, q = u % QPR, sl = tid / (GM * QPR);
-    const bool act = sl < NSL && hh < G;
-    const float2 *pml = reinterpret_cast<const float2 *>(part_ml) + (head0 + min(hh, G - 1)) * a.max_chunks;
-    const float *po = a.part + (head0 + min(hh, G - 1)) * a.max_chunks * HD + 4 * q;
-    float mr = -INFINITY, sr = 0.0f;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (act) {
-        constexpr int KB = 16;   // one round for up to 16 * NSL chunks (64 with two query heads of 128)
-        for (int k0 = sl; k0 < nc; k0 += KB * NSL) {
-            float2 ml[KB];
-            float4 ov[KB];
-#pragma unroll
-            for (int b = 0; b < KB; b++) {
-                const int k = k0 + b * NSL;
-                if (k < nc) {
-                    ml[b] = pml[k];
-                    ov[b] = *reinterpret_cast<const float4 *>(po + (size_t)k * HD);
-                } else {
-                    ml[b] = make_float2(-INFINITY, 0.0f);
-                    ov[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                }
+        int ok = 1;
+        for (int n = 0; __hip_atomic_load(a.wo_flag + g * XM_CNT_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0; n++) {
+            if (n >= a.wo_spin) {
+                ok = 0;
+                __hip_atomic_fetch_or(a.xm_err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
             }
-            float mn = mr;
-#pragma unroll
-            for (int b = 0; b < KB; b++) mn = fmaxf(mn, ml[b].x);
-            const float r = mr == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr - mn);
-            sr *= r; acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
-            mr = mn;
-#pragma unroll
-            for (int b = 0; b < KB; b++) {
-                const float f = ml[b].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[b].x - mr);
-                sr = fmaf(ml[b].y, f, sr);
-                acc.x = fmaf(f, ov[b].x, acc.x); acc.y = fmaf(f, ov[b].y, acc.y);
-                acc.z = fmaf(f, ov[b].z, acc.z); acc.w = fmaf(f, ov[b].w, acc.w);
-            }
+            __builtin_amdgcn_s_sleep(1);
         }
-        if (q == 0) sm_xm[sl][hh] = mr;
+        sm_go = ok;
     }
     __syncthreads();
-    if (act) {
-        float MM = sm_xm[0][hh];
-#pragma unroll
-        for (int s2 = 1; s2 < NSL; s2++) MM = fmaxf(MM, sm_xm[s2][hh]);
-        const float r = mr == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr - MM);
-        acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
-        sm_acc[tid] = acc;
-        if (q == 0) sm_xl[sl][hh] = sr * r;
+    if (!sm_go) return;
+    if (tid < GM * HD / 4) {
+        const float4 x = *reinterpret_cast<const float4 *>(a.out + (size_t)g * G * HD + 4 * tid);
+        float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+        m = max8(m);
+        const float d = m / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = (int)fminf(fmaxf(roundf(x.x * id), -127.0f), 127.0f);
+        const int q1 = (int)fminf(fmaxf(roundf(x.y * id), -127.0f), 127.0f);
+        const int q2 = (int)fminf(fmaxf(roundf(x.z * id), -127.0f), 127.0f);
+        const int q3 = (int)fminf(fmaxf(roundf(x.w * id), -127.0f), 127.0f);
+        sm_qx[tid] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+        if ((tid & 7) == 0) sm_dx[tid >> 3] = h2f(f2h(d));
     }
     __syncthreads();
-    if (sl == 0 && hh < G) {
-        float4 O = sm_acc[u];
-        float S = sm_xl[0][hh];
-#pragma unroll
-        for (int s2 = 1; s2 < NSL; s2++) {
-            const float4 v = sm_acc[s2 * GM * QPR + u];
-            O.x += v.x; O.y += v.y; O.z += v.z; O.w += v.w;
-            S += sm_xl[s2][hh];
-        }
-        const float r = 1.0f / S;
-        *reinterpret_cast<float4 *>(a.out + (head0 + hh) * HD + 4 * q) = make_float4(O.x * r, O.y * r, O.z * r, O.w * r);
-    }
-    if (tid == 0) __hip_atomic_store(a.xm_cnt + g * XM_CNT_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int4 xq = *reinterpret_cast<const int4 *>(&sm_qx[4 * fw_j]);
+    int isum = sdot4(fw_q.x, xq.x, 0);
+    isum = sdot4(fw_q.y, xq.y, isum);
+    isum = sdot4(fw_q.z, xq.z, isum);
+    isum = sdot4(fw_q.w, xq.w, isum);
+    // lanes 2k, 2k + 1 hold the two halves of block k
+    isum += __builtin_amdgcn_mov_dpp(isum, 0xb1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+    float v = (fw_j & 1) ? 0.0f : ((float)isum * h2f(fw_d)) * sm_dx[fw_j >> 1];
+    v = group_sum<CPR>(v);
+    if (fw_j == 0 && fw_r < a.wo_rows && fw_row < a.wo.rows) a.wo_part[(size_t)g * a.wo.rows + fw_row] = v;
 }
 
 // Split-K merge, one workgroup per query head, when the chunks of a kv head
@@ -575,6 +350,9 @@ template <int HD, bool F16, int GM>
 static void dec_launch(hipStream_t st, const AttnArgs &a, dim3 grid) {
     constexpr int NL = ATT_DEC_NL, NW = ATT_DEC_NW;
     if (!a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 0>), grid, dim3(NW * 64), 0, st, a);
+    else if (grid.y > 1 && a.wo_part) {
+        if constexpr (HD != 48 && GM * HD >= 128) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 3>), grid, dim3(NW * 64), 0, st, a);
+    }
     else if (grid.y > 1) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 1>), grid, dim3(NW * 64), 0, st, a);
     else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 2>), grid, dim3(NW * 64), 0, st, a);
 }
@@ -608,6 +386,13 @@ int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_
         if ((long)per_head * ATT_DEC_CR < a.ctx) return -1;
     } else if ((long)a.max_chunks * ATT_DEC_CR < a.ctx) {
         return -1;
+    }
+    if (a.wo_part) {   // the folded wo product: the 2-D merge grid, whole groups of 8-64 chunks per row
+        const int G = a.n_heads / a.n_kv, cpr = G * a.hd / 16;
+        if (!a.xm_cnt || a.n_kv % 8 || !a.wo_flag || a.wo.dtype != DT_Q8 || !a.wo.q || !a.wo.d) return -1;
+        if ((G & (G - 1)) || (a.hd != 64 && a.hd != 128) || cpr < 8 || cpr > 64) return -1;
+        if (a.wo.cols != a.n_heads * a.hd || a.wo.rows <= 0 || a.wo_spin < 0) return -1;
+        if (a.wo_rows <= 0 || (long)a.wo_rows * a.max_chunks < a.wo.rows || a.wo_rows * cpr > ATT_DEC_NW * 64) return -1;
     }
     switch (a.hd) {
         case 48: return f16kv ? dec_pick_g<48, true>(st, a, with_merge) : dec_pick_g<48, false>(st, a, with_merge);

@@ -400,6 +400,19 @@ struct EhipState {
     int *done_h;                // pinned: the ticket of the last completed API step
     int ticket;
     float *x, *qkv, *o, *h, *logits_d, *logits_h;
+    // the decode attention with the wo product folded in (attn_decode.hip,
+    // merge mode 3): the kv groups' wo partials [n_kv][dim], their flags
+    // [n_layers][n_kv][XM_CNT_STRIDE] (zero between launches), and a second
+    // residual buffer: the w1|w3 matvec writes x + the partials there, so
+    // the layers' residual alternates between x and x2
+    float *x2, *wo_part;
+    int *wo_flag;
+    bool fw_cur;   // whether the decode launches enqueued last fold the wo product in
+    // polls of a kv group's wo flag before the folded product gives up
+    // (ATT_DEC_FW_SPIN; EHIP_FW_TEST_SPIN=n sets it, a test hook: 0 makes
+    // every workgroup that finds the flag still down time out, so the
+    // fallback can be exercised while the kernels run as usual)
+    int fw_spin;
     float *part;
     float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
     int mc_dec;     // chunks per kv head, two-kernel merge
@@ -543,11 +556,13 @@ static int xm_probe(EhipState *s) {
     return 0;
 }
 
-// After a launch that found a workgroup on an unexpected XCD the counters may
-// hold stale arrivals: clear them with the flag.
+// After a launch that found a workgroup on an unexpected XCD (or whose folded
+// wo product timed out) the counters and flags may hold stale values: clear
+// them with the error flag.
 static int xm_reset(EhipState *s) {
     const EhipConfig &c = s->m->cfg;
     HCHK(hipMemsetAsync(s->xm_cnt, 0, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, s->st), -1);
+    HCHK(hipMemsetAsync(s->wo_flag, 0, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, s->st), -1);
     HCHK(hipMemsetAsync(s->xm_err, 0, 4, s->st), -1);
     HCHK(hipStreamSynchronize(s->st), -1);
     return 0;
@@ -573,6 +588,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     EhipState *s = new EhipState();  // value-initialised: every pointer starts null
     s->m = m; s->ctx = ctx; s->f16kv = kv_fp16 ? 1 : 0; s->esize = kv_fp16 ? 2 : 4;
     s->graph_mode = env_int("EHIP_GRAPH", 1);
+    s->fw_spin = env_int("EHIP_FW_TEST_SPIN", ATT_DEC_FW_SPIN);
     if (hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking) != hipSuccess) {
         set_err("hipStreamCreate failed");
         delete s;
@@ -640,7 +656,10 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->smp_cidx = (int *)salloc(s, 4 * SAMPLE_GRID * SAMPLE_TOPK_MAX)) &&
               (s->smp_we = (float *)salloc(s, 4 * (size_t)c.vocab_size)) &&
               (s->smp_wcum = (float *)salloc(s, 4 * (size_t)c.vocab_size)) &&
-              (s->smp_wk = (unsigned long long *)salloc(s, 8 * 2 * (size_t)sample_wide_pad(c.vocab_size)));
+              (s->smp_wk = (unsigned long long *)salloc(s, 8 * 2 * (size_t)sample_wide_pad(c.vocab_size))) &&
+              (s->x2 = (float *)salloc(s, 4 * (size_t)c.dim)) &&
+              (s->wo_part = (float *)salloc(s, 4 * (size_t)c.n_kv_heads * c.dim)) &&
+              (s->wo_flag = (int *)salloc(s, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, true));
     if (ok && m->any_f32) ok = (s->xf = (float *)salloc(s, 4 * pfc * wide)) != nullptr;
     if (ok && s->ref_order) ok = (s->att_ref = (float *)salloc(s, 4 * (size_t)c.n_heads * ctx)) != nullptr;
     if (ok && s->pf_mode != PF_EXACT && attn_kvimg_bytes(hd, s->f16kv, ctx, c.n_kv_heads) > 0) {
@@ -714,7 +733,27 @@ static int mv(EhipState *s, int pro, int epi, const MatvecArgs &a) {
     return s->ref_order ? launch_matvec_ref(s->st, pro, epi, a) : launch_matvec(s->st, pro, epi, a);
 }
 
-static int enq_attn_decode(EhipState *s, int l, bool with_merge = true) {
+// Whether the decode step folds the wo product into the attention (merge
+// mode 3): the in-kernel merge on the 2-D grid (kv heads a multiple of 8),
+// query heads per kv head a power of two with G * head_dim of 128..1024, and
+// Q8_0 wo (Q8_0 or Q4_0 w1|w3) in every layer.  EHIP_FUSE_WO=0 turns it off.
+static bool fw_usable(EhipState *s) {
+    const EhipModel *m = s->m;
+    const EhipConfig &c = m->cfg;
+    if (!s->xm_on || s->ref_order || !env_int("EHIP_FUSE_WO", 1)) return false;
+    const int G = c.n_heads / c.n_kv_heads, cpr = G * c.head_dim / 16;
+    if (c.n_kv_heads % 8 || (G & (G - 1)) || (c.head_dim != 64 && c.head_dim != 128) || cpr < 8 || cpr > 64) return false;
+    if (c.n_kv_heads > MATVEC_MAX_PARTS) return false;
+    const int mc = 8 * s->xm_slots / c.n_kv_heads;
+    if ((c.dim + mc - 1) / mc * cpr > ATT_DEC_NW * 64) return false;
+    for (int l = 0; l < c.n_layers; l++) {
+        const DevLayer &y = m->layers[l];
+        if (y.wo.dtype != DT_Q8 || (y.w13.dtype != DT_Q8 && y.w13.dtype != DT_Q4)) return false;
+    }
+    return true;
+}
+
+static int enq_attn_decode(EhipState *s, int l, bool with_merge = true, bool fw = false) {
     AttnArgs a = attn_args(s, l);
     a.q = s->qkv; a.q_stride = 0; a.tokpos = s->tokpos_d; a.pos_base = 0; a.n_tok = 1;
     if (s->ref_order) {
@@ -729,6 +768,14 @@ static int enq_attn_decode(EhipState *s, int l, bool with_merge = true) {
         a.xm_cnt = s->xm_cnt + (size_t)l * s->m->cfg.n_kv_heads * XM_CNT_STRIDE;
         a.xm_xcc = s->xm_xcc;
         a.xm_err = s->xm_err;
+        if (fw) {
+            const EhipConfig &c = s->m->cfg;
+            a.wo = s->m->layers[l].wo;
+            a.wo_part = s->wo_part;
+            a.wo_flag = s->wo_flag + (size_t)l * c.n_kv_heads * XM_CNT_STRIDE;
+            a.wo_rows = (c.dim + a.max_chunks - 1) / a.max_chunks;
+            a.wo_spin = s->fw_spin;
+        }
     }
     a.out = s->o;
     return launch_attn_decode(s->st, s->f16kv, a, with_merge);
@@ -746,13 +793,23 @@ static int enq_head(EhipState *s, const float *xin) {
     return mv(s, PRO_NORM, EPI_STORE, head_args(s, xin));
 }
 
-static int enq_w13(EhipState *s, int l) {
+// w1|w3 + SwiGLU of layer l on the residual xin; with xnext (the folded wo
+// product) the input is xin + the kv groups' wo partials, written to xnext
+static int enq_w13(EhipState *s, int l, const float *xin, float *xnext = nullptr) {
     const EhipModel *m = s->m;
     const DevLayer &y = m->layers[l];
     MatvecArgs a{};
     a.W = y.w13; a.units = m->cfg.hidden_dim; a.pair_off = m->cfg.hidden_dim;
-    a.in = s->x; a.norm_w = y.ffn_norm; a.eps = m->cfg.norm_eps; a.out = s->h;
-    return mv(s, PRO_NORM, EPI_SWIGLU, a);
+    a.in = xin; a.norm_w = y.ffn_norm; a.eps = m->cfg.norm_eps; a.out = s->h;
+    if (!xnext) return mv(s, PRO_NORM, EPI_SWIGLU, a);
+    a.parts = s->wo_part; a.n_parts = m->cfg.n_kv_heads; a.x_out = xnext;
+    a.flag_reset = s->wo_flag + (size_t)l * m->cfg.n_kv_heads * XM_CNT_STRIDE;
+    return mv(s, PRO_NORM_PARTS, EPI_SWIGLU, a);
+}
+
+// the residual after the last layer of the enqueued decode launches
+static float *x_final(EhipState *s) {
+    return s->fw_cur && (s->m->cfg.n_layers & 1) ? s->x2 : s->x;
 }
 
 // The layer launches of one decode step (the tokpos copy is the caller's).
@@ -766,34 +823,43 @@ static int enq_layers(EhipState *s) {
         HCHK(hipMemcpyAsync(s->dbg[slot], src, 4 * (size_t)n, hipMemcpyDeviceToDevice, s->st), -1);
         return 0;
     };
+    // with the folded wo product the residual alternates: layer l reads
+    // xs[l & 1], its w1|w3 matvec writes x + the attention's wo partials to
+    // xs[(l + 1) & 1], which the w2 matvec then updates in place
+    const bool fw = s->fw_cur = fw_usable(s);
+    float *xs[2] = { s->x, fw ? s->x2 : s->x };
     for (int l = 0; l < c.n_layers; l++) {
         const DevLayer &y = m->layers[l];
+        float *xin = xs[l & 1], *xnext = xs[(l + 1) & 1];
         MatvecArgs a{};
-        a.W = y.qkv; a.units = qd + 2 * kvd; a.in = s->x; a.norm_w = y.attn_norm; a.eps = c.norm_eps;
-        a.tokpos = s->tokpos_d; a.emb = m->emb; a.x_out = s->x; a.out = s->qkv; a.bias = y.bias_qkv;
-        if (l > 0 && snap(l, DBG_XIN, s->x, c.dim)) return -1;
+        a.W = y.qkv; a.units = qd + 2 * kvd; a.in = xin; a.norm_w = y.attn_norm; a.eps = c.norm_eps;
+        a.tokpos = s->tokpos_d; a.emb = m->emb; a.x_out = xin; a.out = s->qkv; a.bias = y.bias_qkv;
+        if (l > 0 && snap(l, DBG_XIN, xin, c.dim)) return -1;
         if (mv(s, l == 0 ? PRO_EMBED_NORM : PRO_NORM, EPI_STORE, a)) return -1;
-        if (l == 0 && snap(l, DBG_XIN, s->x, c.dim)) return -1;   // the embedding row it gathered
+        if (l == 0 && snap(l, DBG_XIN, xin, c.dim)) return -1;   // the embedding row it gathered
         if (snap(l, DBG_QKV, s->qkv, qd + 2 * kvd)) return -1;
-        if (enq_attn_decode(s, l)) return -1;
+        if (enq_attn_decode(s, l, true, fw)) return -1;
         if (snap(l, DBG_O, s->o, qd)) return -1;
-        MatvecArgs b{};
-        b.W = y.wo; b.units = c.dim; b.in = s->o; b.out = s->x;
-        if (mv(s, PRO_PLAIN, EPI_RESID, b)) return -1;
-        if (snap(l, DBG_XMID, s->x, c.dim)) return -1;
-        if (enq_w13(s, l)) return -1;
+        if (!fw) {
+            MatvecArgs b{};
+            b.W = y.wo; b.units = c.dim; b.in = s->o; b.out = xin;
+            if (mv(s, PRO_PLAIN, EPI_RESID, b)) return -1;
+            if (snap(l, DBG_XMID, xin, c.dim)) return -1;
+        }
+        if (enq_w13(s, l, xin, fw ? xnext : nullptr)) return -1;
+        if (fw && snap(l, DBG_XMID, xnext, c.dim)) return -1;
         if (snap(l, DBG_H, s->h, c.hidden_dim)) return -1;
         MatvecArgs d{};
-        d.W = y.w2; d.units = c.dim; d.in = s->h; d.out = s->x;
+        d.W = y.w2; d.units = c.dim; d.in = s->h; d.out = xnext;
         if (mv(s, PRO_PLAIN, EPI_RESID, d)) return -1;
-        if (snap(l, DBG_XOUT, s->x, c.dim)) return -1;
+        if (snap(l, DBG_XOUT, xnext, c.dim)) return -1;
     }
     return 0;
 }
 
 static int enq_decode(EhipState *s) {
     if (enq_layers(s)) return -1;
-    return enq_head(s, s->x);
+    return enq_head(s, x_final(s));
 }
 
 // The API step's completion: its ticket (tokpos[3], copied in with the token)
@@ -816,7 +882,7 @@ static int enq_step(EhipState *s) {
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 16, hipMemcpyHostToDevice, s->st), -1);
     if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
     const bool direct = !s->ref_order && s->m->head.dtype != DT_F32;
-    MatvecArgs a = head_args(s, s->x);
+    MatvecArgs a = head_args(s, x_final(s));
     if (direct) a.out_host = s->logits_h;
     if (mv(s, PRO_NORM, EPI_STORE, a)) { set_err("lm_head launch failed"); return -1; }
     if (!direct)
@@ -895,7 +961,7 @@ static int xm_flag(EhipState *s) {
 static int enq_gen_step(EhipState *s) {
     if (s->m->head.dtype != DT_F32) {   // argmax fused into the lm_head matvec
         if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
-        MatvecArgs a = head_args(s, s->x);
+        MatvecArgs a = head_args(s, x_final(s));
         a.am_val = s->am_val; a.am_idx = s->am_idx;
         a.am_tokpos = s->tokpos_d; a.am_out = s->gen_tok; a.am_cap = s->ctx;
         if (mv(s, PRO_NORM, EPI_STORE, a)) { set_err("lm_head launch failed"); return -1; }
@@ -1082,7 +1148,7 @@ static int generate_sampled_once(EhipState *s, int tok, int pos, int n, EmberSam
     auto enq = [&]() -> int {
         if (parts) {
             if (enq_layers(s)) { set_err("a decode kernel could not be launched for this shape"); return -1; }
-            MatvecArgs h = head_args(s, s->x);
+            MatvecArgs h = head_args(s, x_final(s));
             h.am_val = s->am_val; h.am_idx = s->am_idx;
             sa.nparts = launch_matvec_parts(s->st, PRO_NORM, h);
             if (sa.nparts <= 0) { set_err("lm_head launch failed"); return -1; }
@@ -1303,7 +1369,7 @@ extern "C" int ehip_kv_write(EhipState *s, int which, int layer, int n_pos, cons
 extern "C" int ehip_debug_buffer(EhipState *s, int which, void *host, uint64_t bytes) {
     const EhipConfig &c = s->m->cfg;
     const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
-    const void *src[5] = { s->x, s->qkv, s->o, s->h, s->logits_d };
+    const void *src[5] = { x_final(s), s->qkv, s->o, s->h, s->logits_d };
     const uint64_t len[5] = { 4ull * c.dim, 4ull * (qd + 2 * kvd), 4ull * qd, 4ull * c.hidden_dim,
                               4ull * c.vocab_size };
     if (which < 0 || which > 4 || bytes > len[which]) { set_err("debug_buffer: bad request"); return -1; }
@@ -1387,7 +1453,7 @@ extern "C" int ehip_debug_read_prefill(EhipState *s, int slot, void *host, uint6
 extern "C" int ehip_prefill_pass_tokens(const EhipState *s) { return s->pf_chunk; }
 
 extern "C" int ehip_decode_fusion(const EhipState *s) {
-    return s->xm_on ? 1 : 0;
+    return (s->xm_on ? 1 : 0) | (fw_usable(const_cast<EhipState *>(s)) ? 2 : 0);
 }
 
 extern "C" int ehip_set_graph_mode(EhipState *s, int mode) {
@@ -1476,7 +1542,7 @@ extern "C" int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, flo
         const int l = i++ % L;
         if (kernel == 0) return enq_attn_decode(s, l, false);
         if (kernel == 1) return enq_head(s, s->x);
-        if (kernel == 2) return enq_w13(s, l);
+        if (kernel == 2) return enq_w13(s, l, s->x);
         return -1;
     };
     if (one()) { set_err("time_kernel: unknown kernel %d", kernel); return -1; }  // warm-up

@@ -10,10 +10,14 @@ namespace ehip {
 //             PRO_PLAIN       Q8_0-quantize in
 //             PRO_EMBED_NORM  in = embedding row of the device token, written
 //                             to x_out, then as PRO_NORM
+//             PRO_NORM_PARTS  in + (parts[0] + ... + parts[n_parts - 1]) (the
+//                             kv groups' wo partials of the decode attention),
+//                             written to x_out, then as PRO_NORM; workgroup 0
+//                             clears flag_reset[p * XM_CNT_STRIDE], p < n_parts
 //   epilogue  EPI_STORE   out[r] = W[r].x' (+ bias[r])
 //             EPI_RESID   out[r] += W[r].x'
 //             EPI_SWIGLU  out[u] = silu(W[u].x') * W[u+pair_off].x'
-enum { PRO_NORM = 0, PRO_PLAIN = 1, PRO_EMBED_NORM = 2 };
+enum { PRO_NORM = 0, PRO_PLAIN = 1, PRO_EMBED_NORM = 2, PRO_NORM_PARTS = 3 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 
 struct MatvecArgs {
@@ -24,7 +28,11 @@ struct MatvecArgs {
     const float *norm_w;  // [W.cols]
     float eps;
     const int *tokpos;    // device {tok, pos}
-    DMat emb;             // embedding table (PRO_EMBED_NORM)
+    union {   // (one storage: no prologue uses both)
+        DMat emb;         // embedding table (PRO_EMBED_NORM)
+        // PRO_NORM_PARTS: n_parts vectors of W.cols floats, n_parts <= MATVEC_MAX_PARTS
+        struct { const float *parts; int n_parts; int *flag_reset; };
+    };
     float *x_out;
     float *out;
     const float *bias;
@@ -41,6 +49,7 @@ struct MatvecArgs {
     float *out_host;
 };
 constexpr int MATVEC_MAX_GRID = 2048;
+constexpr int MATVEC_MAX_PARTS = 8;
 int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a);
 // EPI_STORE with am_val/am_idx set and no merge: returns the number of
 // per-workgroup winners written (the sampler's per-part maxima), or -1.
@@ -83,20 +92,42 @@ struct AttnArgs {
     // (n_kv, max_chunks = 8 xm_slots / n_kv), which is what runs.
     int xm_slots;
     float *out;            // [n_tok][n_heads*hd]
-    // prefill scratch: scores [n_heads][n_tok][ldk] (ldk >= pos_base + n_tok,
-    // a multiple of 4); the maximum of each 64-key tile of a row,
-    // [n_heads][n_tok][attn_prefill_tiles(ldk)]; per row the maximum and
-    // 1/sum of the exponentials [n_heads][n_tok]
-    float *scores, *tmax, *rowmax, *rowinv;
-    int ldk;
-    // prefill, optional: the output's Q8_0 codes, fp16-rounded block scales
-    // and code sums ([n_tok][n_heads*hd / 32]), as the quantization kernel
-    // would make them from `out`; written when the launch reports it
-    int8_t *qx; float *qdx; int *qxs;
-    // prefill on matrix cores (head_dim 64 / 128): the pass's K/V converted
-    // once into per-(kv head, 64-key tile) images, kvimg_tiles tiles per head
-    // (attn_kvimg_bytes)
-    uint8_t *kvimg; int kvimg_tiles;
+    // The prefill fields and the decode-only folded wo product share their
+    // storage (no launch uses both), which keeps the struct's size and layout
+    // those of the prefill fields alone: a larger argument struct measured
+    // 1-1.3% slower decode steps.
+    union {
+        struct {
+            // prefill scratch: scores [n_heads][n_tok][ldk] (ldk >= pos_base +
+            // n_tok, a multiple of 4); the maximum of each 64-key tile of a
+            // row, [n_heads][n_tok][attn_prefill_tiles(ldk)]; per row the
+            // maximum and 1/sum of the exponentials [n_heads][n_tok]
+            float *scores, *tmax, *rowmax, *rowinv;
+            int ldk;
+            // prefill, optional: the output's Q8_0 codes, fp16-rounded block
+            // scales and code sums ([n_tok][n_heads*hd / 32]), as the
+            // quantization kernel would make them from `out`; written when the
+            // launch reports it
+            int8_t *qx; float *qdx; int *qxs;
+            // prefill on matrix cores (head_dim 64 / 128): the pass's K/V
+            // converted once into per-(kv head, 64-key tile) images,
+            // kvimg_tiles tiles per head (attn_kvimg_bytes)
+            uint8_t *kvimg; int kvimg_tiles;
+        };
+        struct {
+            // decode with xm_cnt on the 2-D grid, optional: the wo product
+            // folded in (Q8_0 wo, every kv group's G * hd columns in whole
+            // 32-weight blocks).  Once kv head g's output is merged into
+            // `out`, its workgroup c computes rows [c wo_rows, (c + 1)
+            // wo_rows) of W_o[:, the group's columns] . o_g into
+            // wo_part[g][row], with o_g Q8_0-quantized as the decode matvec
+            // quantizes its input.  wo_flag[g * XM_CNT_STRIDE] is raised when
+            // o_g is complete and must be zero at launch (the next w1|w3
+            // matvec clears it).  wo_spin bounds the polls of that flag
+            // (ATT_DEC_FW_SPIN; a time-out raises the error flag).
+            DMat wo; float *wo_part; int *wo_flag; int wo_rows, wo_spin;
+        };
+    };
 };
 // prefill: q rows already normed and rotated, k/v already in the cache.
 // *quantized (if non-null) says whether the launch also wrote a.qx/qdx/qxs.
@@ -133,6 +164,7 @@ int attn_decode_chunks(int ctx, int n_kv, int hd, int n_cu);
 // when a chunk of the XCD with the most kv heads would exceed ATT_DEC_CR rows
 int attn_decode_slots(int ctx, int n_kv, int n_cu);
 constexpr int ATT_DEC_NL = 5;       // K and V pieces per thread per batch in the decode attention
+constexpr int ATT_DEC_FW_SPIN = 1 << 18;   // polls of the folded wo's flag before the error flag is raised
 constexpr int ATT_DEC_NW = 4;       // waves per decode attention workgroup
 constexpr int ATT_DEC_WPC = 2;      // decode attention workgroups per CU
 constexpr int ATT_DEC_CR = 160;     // positions per decode attention workgroup before more are added

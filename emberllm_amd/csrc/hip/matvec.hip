@@ -142,6 +142,20 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) xv[i] = in4[min(tid + WG * i, nslot - 1)];
     }
+    // PRO_NORM_PARTS: the partial vectors, loaded with the input (every load
+    // unconditional: parts past n_parts re-read the last one and are dropped)
+    constexpr int NPV = PRO == PRO_NORM_PARTS ? MATVEC_MAX_PARTS : 1;
+    float4 pv[PRO == PRO_NORM_PARTS ? XPT : 1][NPV];
+    if constexpr (PRO == PRO_NORM_PARTS) {
+        const float4 *p4 = reinterpret_cast<const float4 *>(a.parts);
+#pragma unroll
+        for (int i = 0; i < XPT; i++)
+#pragma unroll
+            for (int p = 0; p < NPV; p++)
+                pv[i][p] = p4[(size_t)min(p, a.n_parts - 1) * nslot + min(tid + WG * i, nslot - 1)];
+        if (blockIdx.x == 0 && tid < a.n_parts)
+            __hip_atomic_store(a.flag_reset + tid * XM_CNT_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (PRO != PRO_PLAIN) {
         const float4 *w4 = reinterpret_cast<const float4 *>(a.norm_w);
 #pragma unroll
@@ -152,6 +166,16 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
     cur.load(a, u0, lane, nch, nb);
 
     // ---- 2. RMSNorm and Q8_0 quantization of the activation, in registers --
+    if constexpr (PRO == PRO_NORM_PARTS) {   // x + (p_0 + p_1 + ...), parts in order
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            float4 t = pv[i][0];
+#pragma unroll
+            for (int p = 1; p < NPV; p++)
+                if (p < a.n_parts) { t.x += pv[i][p].x; t.y += pv[i][p].y; t.z += pv[i][p].z; t.w += pv[i][p].w; }
+            xv[i].x += t.x; xv[i].y += t.y; xv[i].z += t.z; xv[i].w += t.w;
+        }
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
@@ -164,7 +188,7 @@ __global__ __launch_bounds__(WG) void k_matvec(MatvecArgs a) {
         if (!live) xv[i] = make_float4(0, 0, 0, 0);
         if (PRO != PRO_PLAIN) ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
     }
-    if (PRO == PRO_EMBED_NORM && blockIdx.x == 0) {
+    if ((PRO == PRO_EMBED_NORM || PRO == PRO_NORM_PARTS) && blockIdx.x == 0) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int s = tid + WG * i;
@@ -424,6 +448,7 @@ static int pick_dt(hipStream_t st, const MatvecArgs &a) {
         case DT_Q8: return pick_nch<DT_Q8, PRO, EPI>(st, a, (size_t)K + (size_t)(K / QB) * 8);
         case DT_Q4: return pick_nch<DT_Q4, PRO, EPI>(st, a, (size_t)K + (size_t)(K / QB) * 8);
         case DT_F32: {
+            if constexpr (PRO == PRO_NORM_PARTS) return -1;
             if ((size_t)K * 4 > 64 * 1024) return -1;
             long grid = ((long)a.units + NWAVE - 1) / NWAVE;
             if (grid > MATVEC_MAX_GRID) grid = MATVEC_MAX_GRID;
@@ -444,6 +469,11 @@ int launch_matvec(hipStream_t st, int pro, int epi, const MatvecArgs &a) {
     else if (pro == PRO_EMBED_NORM && epi == EPI_STORE) grid = pick_dt<PRO_EMBED_NORM, EPI_STORE>(st, a);
     else if (pro == PRO_NORM && epi == EPI_SWIGLU) grid = pick_dt<PRO_NORM, EPI_SWIGLU>(st, a);
     else if (pro == PRO_PLAIN && epi == EPI_RESID) grid = pick_dt<PRO_PLAIN, EPI_RESID>(st, a);
+    else if (pro == PRO_NORM_PARTS && epi == EPI_SWIGLU) {
+        if (!a.parts || !a.x_out || !a.flag_reset || a.n_parts < 1 || a.n_parts > MATVEC_MAX_PARTS) return -1;
+        if (a.W.dtype != DT_Q8 && a.W.dtype != DT_Q4) return -1;
+        grid = pick_dt<PRO_NORM_PARTS, EPI_SWIGLU>(st, a);
+    }
     if (grid <= 0) return -1;
     if (a.am_val) return launch_argmax_merge(st, a.am_val, a.am_idx, grid, a.units, a.am_tokpos, a.am_out, a.am_cap);
     return 0;

@@ -102,8 +102,8 @@ class Engine:
         self.lib.ehip_set_graph_mode(self.dev, 1 if on else 0)
 
     def decode_fusion(self):
-        """Bit 0: the attention kernel merges its chunks itself
-        (ehip_decode_fusion)."""
+        """Bit 0: the attention kernel merges its chunks itself; bit 1: it
+        also computes the wo product (ehip_decode_fusion)."""
         return self.lib.ehip_decode_fusion(self.dev)
 
     def time_decode(self, pos0, steps):

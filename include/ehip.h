@@ -185,7 +185,10 @@ int ehip_prefill_pass_tokens(const EhipState *s);
 int ehip_set_graph_mode(EhipState *s, int mode);
 /* How the state's decode step is scheduled: bit 0 = the attention kernel
  * merges its chunks itself (no merge kernel), which needs every workgroup of
- * a kv head on one XCD; the state checks that at creation. */
+ * a kv head on one XCD; the state checks that at creation.  Bit 1 = the
+ * attention kernel also computes the wo product (no wo matvec launch).  A
+ * step whose kernels find a workgroup on another XCD, or whose wo product
+ * times out, clears both bits for the rest of the state's life. */
 int ehip_decode_fusion(const EhipState *s);
 /* Time `steps` decode steps at positions pos0.. with HIP events recorded on
  * the state's stream; writes the average step time in ms.  Tokens follow the

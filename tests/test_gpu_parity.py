@@ -68,15 +68,19 @@ def test_benchmark_shapes(case, oracle_threads):
     say(check_run(teacher_forced(case), case["id"]))
 
 
-@pytest.mark.parametrize("schedule", ["in-kernel-merge", "two-kernel"])
+@pytest.mark.parametrize("schedule", ["folded-wo", "in-kernel-merge", "two-kernel"])
 def test_decode_schedules(schedule, oracle_threads, monkeypatch):
     """The Qwen3-0.6B shape (8 kv heads: one per XCD of the MI355X) under each
     decode schedule the state can choose: the attention kernel merging its
-    chunks through the XCD's L2 (the default there) and the chunk kernel +
-    merge kernel (EHIP_XMERGE=0).  Both must match the oracle, including past
-    one chunk per workgroup (prompt 300, decode to depth 332)."""
+    chunks through the XCD's L2 and computing its kv group's share of the wo
+    product (the default there), the same merge with wo as its own matvec
+    (EHIP_FUSE_WO=0), and the chunk kernel + merge kernel (EHIP_XMERGE=0).
+    All must match the oracle, including past one chunk per workgroup
+    (prompt 300, decode to depth 332)."""
     if schedule == "two-kernel":
         monkeypatch.setenv("EHIP_XMERGE", "0")
+    elif schedule == "in-kernel-merge":
+        monkeypatch.setenv("EHIP_FUSE_WO", "0")
     name = "qwen3_06b"
     path = configs.model_path(name, threads=16)
     V = configs.ALL[name]["vocab_size"]
@@ -85,7 +89,7 @@ def test_decode_schedules(schedule, oracle_threads, monkeypatch):
     say(f"qwen3_06b schedule={schedule} p300 d32")
     eng = emberllm.Engine(path, ctx=400)
     fusion = eng.decode_fusion()
-    want = {"in-kernel-merge": 1, "two-kernel": 0}[schedule]
+    want = {"folded-wo": 3, "in-kernel-merge": 1, "two-kernel": 0}[schedule]
     assert fusion == want, f"state chose fusion {fusion}, expected {want} on this device"
     orc = oracle.Oracle(path, ctx=400)
     res = [compare(eng.prefill(ids), orc.prefill(ids))]
@@ -376,4 +380,40 @@ def test_xcd_check_falls_back_to_the_merge_kernel(name, monkeypatch):
             got, _ = eng.generate_greedy(tok0, len(ids), 9)
         np.testing.assert_array_equal(got, want_toks)
         assert eng.decode_fusion() == 0, "the state must keep the two-kernel schedule after the check fired"
+        eng.close()
+
+
+def test_folded_wo_timeout_falls_back(monkeypatch):
+    """The folded wo product waits for its kv group's merged output with a
+    bounded poll of a flag; on time-out the workgroup raises the error flag
+    instead of writing its rows.  EHIP_FW_TEST_SPIN=0 makes every workgroup
+    that finds the flag still down time out at once (the kernels otherwise
+    run as usual), so the state must switch to the two-kernel schedule for
+    good and re-run the work, returning exactly what a state created with
+    that schedule returns, through ember_forward and the device loop."""
+    name = "qwen3_06b"
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    ids = np.arange(100) * 89 % V
+    say("folded wo product: forced time-out")
+    monkeypatch.setenv("EHIP_XMERGE", "0")
+    ref = emberllm.Engine(path, ctx=160)
+    assert ref.decode_fusion() == 0
+    tok0 = int(np.argmax(ref.prefill(ids)))
+    want_fwd = ref.forward(tok0, len(ids))
+    want_toks, _ = ref.generate_greedy(tok0, len(ids), 9)
+    ref.close()
+    monkeypatch.delenv("EHIP_XMERGE")
+    monkeypatch.setenv("EHIP_FW_TEST_SPIN", "0")
+    for path_kind in ("forward", "device loop"):
+        eng = emberllm.Engine(path, ctx=160)
+        if eng.decode_fusion() != 3:
+            eng.close()
+            pytest.skip("the state does not fold the wo product on this device")
+        eng.prefill(ids)
+        if path_kind == "forward":
+            np.testing.assert_array_equal(eng.forward(tok0, len(ids)), want_fwd)
+        got, _ = eng.generate_greedy(tok0, len(ids), 9)
+        np.testing.assert_array_equal(got, want_toks)
+        assert eng.decode_fusion() == 0, "the state must keep the two-kernel schedule after the time-out"
         eng.close()

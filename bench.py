@@ -32,9 +32,11 @@ same protocol runs through ctypes.  Also reported, never as `value`:
                         mapped, weights repacked and uploaded, KV cache and
                         scratch allocated
   roofline              the dominant kernel (split-K attention of one layer
-                        at depth 4096): algorithmic bytes per launch over
-                        its average duration (HIP events, isolated launches
-                        on the state's stream)
+                        at depth 4096, in the form the decode step runs:
+                        with its in-kernel merge and folded wo product where
+                        the state uses them): algorithmic bytes per launch
+                        over its average duration (HIP events, isolated
+                        launches on the state's stream)
   cpu_baseline          the reference's own C code, compiled from its
                         sources into oracle/_ref/ (or, absent that, the
                         oracle's port), decoding at the same depth on the
@@ -90,6 +92,14 @@ def attn_launch_bytes(c, pos, e_kv):
     kvd = c["n_kv_heads"] * c["head_dim"]
     qd = c["n_heads"] * c["head_dim"]
     return 2 * (pos + 1) * kvd * e_kv + 2 * kvd * e_kv + 4 * (qd + 2 * kvd) + 4 * qd
+
+
+def wo_fold_bytes(c):
+    """Algorithmic bytes the folded wo product adds to an attention launch:
+    the Q8_0 wo weights read (34 bytes per 32) and the kv groups' partial
+    vectors written."""
+    qd = c["n_heads"] * c["head_dim"]
+    return c["dim"] * (qd // 32) * 34 + 4 * c["n_kv_heads"] * c["dim"]
 
 
 def profiled_traffic(kernel, model, depth, kv):
@@ -461,12 +471,15 @@ def main():
     if not args.decode_only:
         # ---- dominant kernel: attention of one layer at this depth ---------
         reps_k = 200
+        fusion = eng.decode_fusion()
         ms_att = eng.time_kernel(0, depth, reps_k)
-        ab = attn_launch_bytes(c, depth, e_kv)
+        ab = attn_launch_bytes(c, depth, e_kv) + (wo_fold_bytes(c) if fusion & 2 else 0)
         ms_head = eng.time_kernel(1, depth, reps_k)
         hb = c["vocab_size"] * (c["dim"] // 32) * 34 + 4 * c["vocab_size"]
         ms_w13 = eng.time_kernel(2, depth, reps_k)
         wb = 2 * c["hidden_dim"] * (c["dim"] // 32) * 34 + 4 * c["hidden_dim"]
+        if fusion & 2:   # its prologue reads the wo partials and writes the residual
+            wb += 4 * (c["n_kv_heads"] + 1) * c["dim"]
         out["kernels"] = {
             "attention_layer": {"us": ms_att * 1e3, "GB_s": ab / (ms_att / 1e3) / 1e9, "bytes": ab},
             "lm_head": {"us": ms_head * 1e3, "GB_s": hb / (ms_head / 1e3) / 1e9, "bytes": hb},
@@ -484,7 +497,8 @@ def main():
                 "frac": round(achieved / (HBM_PEAK / 1e9), 4),
                 "traffic": profiled_traffic("ehip::k_attn_dec", args.model, depth, args.kv),
                 "kernel": f"k_attn_dec (split-K GQA attention over one layer's KV cache"
-                          f"{', chunk partials merged in-kernel by the last workgroup of each kv head' if eng.decode_fusion() & 1 else ''}) "
+                          f"{', chunk partials merged in-kernel by the last workgroup of each kv head' if fusion & 1 else ''}"
+                          f"{', then the wo partials of the kv groups (Q8_0 wo weights read)' if fusion & 2 else ''}) "
                           f"at position {depth}, {ab} algorithmic bytes per launch, mean of {reps_k} "
                           f"launches walking the {c['n_layers']} layers' caches"}
 

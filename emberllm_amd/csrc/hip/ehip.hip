@@ -1536,13 +1536,23 @@ extern "C" int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, flo
     HCHK(hipMemcpyAsync(s->tokpos_d, s->tokpos_h, 8, hipMemcpyHostToDevice, s->st), -1);
     // successive launches walk through the layers, so each reads weights or
     // cache rows of its own, as in a decode step (the lm_head is one matrix)
+    // The kernels run in the form the decode step uses: with the wo product
+    // folded into the attention, the attention raises each kv group's flag
+    // and the w1|w3 prologue adds the partials and clears the flags, so the
+    // attention's launches clear every layer's flags before each pass over
+    // the layers (a fill of a few KB per n_layers launches, timed with them).
     const int L = s->m->cfg.n_layers;
+    const bool fw = fw_usable(s);
+    const size_t nflag = (size_t)L * s->m->cfg.n_kv_heads * XM_CNT_STRIDE;
     int i = 0;
     auto one = [&]() -> int {
         const int l = i++ % L;
-        if (kernel == 0) return enq_attn_decode(s, l, false);
+        if (kernel == 0) {
+            if (fw && l == 0) HCHK(hipMemsetAsync(s->wo_flag, 0, 4 * nflag, s->st), -1);
+            return enq_attn_decode(s, l, false, fw);
+        }
         if (kernel == 1) return enq_head(s, s->x);
-        if (kernel == 2) return enq_w13(s, l, s->x);
+        if (kernel == 2) return enq_w13(s, l, s->x, fw ? s->x2 : nullptr);
         return -1;
     };
     if (one()) { set_err("time_kernel: unknown kernel %d", kernel); return -1; }  // warm-up
@@ -1554,5 +1564,9 @@ extern "C" int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, flo
     float t = 0.0f;
     HCHK(hipEventElapsedTime(&t, s->ev0, s->ev1), -1);
     *ms = t / reps;
+    if (fw && kernel == 0) {   // the flags the last launches raised
+        HCHK(hipMemsetAsync(s->wo_flag, 0, 4 * nflag, s->st), -1);
+        HCHK(hipStreamSynchronize(s->st), -1);
+    }
     return 0;
 }

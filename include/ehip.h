@@ -197,8 +197,9 @@ int ehip_time_decode(EhipState *s, int pos0, int steps, float *ms_per_step);
 /* Time `reps` back-to-back launches of one decode-step kernel on the
  * state's stream with HIP events, at position pos; writes average ms.
  * kernel: 0 = the split-K attention kernel (with its in-kernel chunk merge
- * when ehip_decode_fusion reports one; the separate merge kernel is not
- * timed), 1 = lm_head matvec, 2 = fused w1|w3 matvec.  Launches of kernels 0
+ * and folded wo product when ehip_decode_fusion reports them; the separate
+ * merge kernel is not timed), 1 = lm_head matvec, 2 = fused w1|w3 matvec
+ * (adding the wo partials when they are folded).  Launches of kernels 0
  * and 2 walk through the layers, so each streams its own cache rows or
  * weights from HBM as in a decode step. */
 int ehip_time_kernel(EhipState *s, int kernel, int pos, int reps, float *ms_per_launch);

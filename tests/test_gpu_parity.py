@@ -95,6 +95,8 @@ def test_decode_schedules(schedule, oracle_threads, monkeypatch):
     res = [compare(eng.prefill(ids), orc.prefill(ids))]
     for i, t in enumerate(toks):
         res.append(compare(eng.forward(int(t), 300 + i), orc.forward(int(t), 300 + i)))
+    # a schedule whose error flag fired would have re-run its steps on the two-kernel one
+    assert eng.decode_fusion() == want, f"the state left fusion {want} during the run"
     eng.close()
     orc.close()
     # bars of the same shape's teacher-forced case (the reference builds' noise floor)

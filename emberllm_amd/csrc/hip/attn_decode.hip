@@ -131,10 +131,13 @@ template <int HD, bool F16> struct DecLay {
 // g + n_kv c, max_chunks = 8 xm_slots / n_kv); 2 = in-kernel merge on the
 // 1-D grid of 8 * xm_slots; 3 = mode 1 with the wo product folded in (every
 // workgroup of kv head g, on g's XCD, waits for the merged o_g and computes
-// its wo_rows rows of the group's wo partial: see AttnArgs::wo).
+// its wo_rows rows of the group's wo partial: see AttnArgs::wo); 4 = mode 2
+// with the wo product folded in the same way, each kv head's rows shared
+// over its own chunk count, G * HD / 16 of the CPR lanes per row in use and
+// (CPR >= 32) two rounds of rows per workgroup.
 template <int HD, int GM, bool F16, int NL, int NW, int XMODE>
 __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
-    constexpr bool XM = XMODE != 0, FW = XMODE == 3;
+    constexpr bool XM = XMODE != 0, FW = XMODE >= 3, FW1 = XMODE == 4;
     using L = DecLay<HD, F16>;
     constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL;
     constexpr int NT = NW * 64, RPB = NW * RPL;   // threads, rows per workgroup load
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int g, c, nchunk;   // kv head, chunk, chunks of the kv head
-    if constexpr (XMODE == 2) {
+    if constexpr (XMODE == 2 || XMODE == 4) {
         // the mapping's arguments are read before anything depends on them,
         // so their scalar loads are in flight together
         asm volatile("" ::"s"(a.n_kv), "s"(a.xm_slots), "s"(a.q), "s"(a.tokpos), "s"(a.xm_xcc));
@@ -169,16 +172,31 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     // FW: this thread's 16 wo codes (row fw_r of the workgroup's wo_rows,
     // 16-byte chunk fw_j of the group's G * HD columns) and their block
     // scale, loaded before anything else (they depend on nothing)
-    constexpr int CPR = GM * HD / 16;   // chunks per wo row (G == GM)
+    constexpr int CPR = GM * HD / 16;   // chunk lanes per wo row (G * HD / 16 in use; all with G == GM)
+    constexpr int RPR = NT / CPR;       // wo rows per round
+    constexpr int FWR = FW1 && CPR >= 32 ? 2 : 1;   // rounds of rows
     const int fw_r = tid / CPR, fw_j = tid % CPR;
     const int fw_row = c * a.wo_rows + fw_r;
     int4 fw_q = make_int4(0, 0, 0, 0);
     uint16_t fw_d = 0;
-    if constexpr (FW) {
+    if constexpr (FW && !FW1) {
         const int rc = min(c * a.wo_rows + min(fw_r, a.wo_rows - 1), a.wo.rows - 1);
         const int col0 = g * G * HD;
         fw_q = *reinterpret_cast<const int4 *>(a.wo.q + (size_t)rc * a.wo.cols + col0 + 16 * fw_j);
         fw_d = a.wo.d[(size_t)rc * (a.wo.cols / QB) + col0 / QB + fw_j / 2];
+    }
+    int4 fw_q4[FWR];      // mode 4: rows fw_r + k RPR of the kv head's own wo_rows
+    uint16_t fw_d4[FWR];
+    if constexpr (FW1) {
+        const int wo_rows = (a.wo.rows + nchunk - 1) / nchunk;
+        const int fw_jc = min(fw_j, G * HD / 16 - 1);
+        const int col0 = g * G * HD;
+#pragma unroll
+        for (int k = 0; k < FWR; k++) {
+            const int rc = min(c * wo_rows + min(fw_r + k * RPR, wo_rows - 1), a.wo.rows - 1);
+            fw_q4[k] = *reinterpret_cast<const int4 *>(a.wo.q + (size_t)rc * a.wo.cols + col0 + 16 * fw_jc);
+            fw_d4[k] = a.wo.d[(size_t)rc * (a.wo.cols / QB) + col0 / QB + fw_jc / 2];
+        }
     }
     // FW: o_g is complete in this XCD's L2: raise the group's flag
     auto raise = [&]() {
@@ -224,7 +242,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     }
     __syncthreads();
     if (!sm_go) return;
-    if (tid < GM * HD / 4) {
+    if (tid < (FW1 ? G : GM) * HD / 4) {
         const float4 x = *reinterpret_cast<const float4 *>(a.out + (size_t)g * G * HD + 4 * tid);
         float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
         m = max8(m);
@@ -238,6 +256,25 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
         if ((tid & 7) == 0) sm_dx[tid >> 3] = h2f(f2h(d));
     }
     __syncthreads();
+    if constexpr (FW1) {
+        const int wo_rows = (a.wo.rows + nchunk - 1) / nchunk, cpr_g = G * HD / 16;
+        const int fw_jc = min(fw_j, cpr_g - 1);
+        const int4 xq = *reinterpret_cast<const int4 *>(&sm_qx[4 * fw_jc]);
+        const float dx = sm_dx[fw_jc >> 1];
+#pragma unroll
+        for (int k = 0; k < FWR; k++) {
+            int isum = sdot4(fw_q4[k].x, xq.x, 0);
+            isum = sdot4(fw_q4[k].y, xq.y, isum);
+            isum = sdot4(fw_q4[k].z, xq.z, isum);
+            isum = sdot4(fw_q4[k].w, xq.w, isum);
+            isum += __builtin_amdgcn_mov_dpp(isum, 0xb1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+            float v = (fw_j & 1) || fw_j >= cpr_g ? 0.0f : ((float)isum * h2f(fw_d4[k])) * dx;
+            v = group_sum<CPR>(v);
+            const int r = fw_r + k * RPR, row = c * wo_rows + r;
+            if (fw_j == 0 && r < wo_rows && row < a.wo.rows) a.wo_part[(size_t)g * a.wo.rows + row] = v;
+        }
+        return;
+    }
     const int4 xq = *reinterpret_cast<const int4 *>(&sm_qx[4 * fw_j]);
     int isum = sdot4(fw_q.x, xq.x, 0);
     isum = sdot4(fw_q.y, xq.y, isum);
@@ -354,6 +391,9 @@ static void dec_launch(hipStream_t st, const AttnArgs &a, dim3 grid) {
         if constexpr (HD != 48 && GM * HD >= 128) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 3>), grid, dim3(NW * 64), 0, st, a);
     }
     else if (grid.y > 1) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 1>), grid, dim3(NW * 64), 0, st, a);
+    else if (a.wo_part) {
+        if constexpr (HD != 48 && GM * HD >= 128) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 4>), grid, dim3(NW * 64), 0, st, a);
+    }
     else hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 2>), grid, dim3(NW * 64), 0, st, a);
 }
 
@@ -387,12 +427,19 @@ int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_
     } else if ((long)a.max_chunks * ATT_DEC_CR < a.ctx) {
         return -1;
     }
-    if (a.wo_part) {   // the folded wo product: the 2-D merge grid, whole groups of 8-64 chunks per row
-        const int G = a.n_heads / a.n_kv, cpr = G * a.hd / 16;
-        if (!a.xm_cnt || a.n_kv % 8 || !a.wo_flag || a.wo.dtype != DT_Q8 || !a.wo.q || !a.wo.d) return -1;
-        if ((G & (G - 1)) || (a.hd != 64 && a.hd != 128) || cpr < 8 || cpr > 64) return -1;
+    if (a.wo_part) {   // the folded wo product: whole 32-weight blocks per kv group, 8-64 chunk lanes per row
+        const int G = a.n_heads / a.n_kv, GM = G <= 1 ? 1 : (G <= 2 ? 2 : (G <= 4 ? 4 : 8));
+        const int cpr = GM * a.hd / 16, rpr = ATT_DEC_NW * 64 / cpr;
+        if (!a.xm_cnt || !a.wo_flag || a.wo.dtype != DT_Q8 || !a.wo.q || !a.wo.d) return -1;
+        if ((a.hd != 64 && a.hd != 128) || (G * a.hd) % QB || cpr < 8 || cpr > 64) return -1;
         if (a.wo.cols != a.n_heads * a.hd || a.wo.rows <= 0 || a.wo_spin < 0) return -1;
-        if (a.wo_rows <= 0 || (long)a.wo_rows * a.max_chunks < a.wo.rows || a.wo_rows * cpr > ATT_DEC_NW * 64) return -1;
+        if (a.n_kv % 8 == 0) {   // mode 3: G == GM, the host's wo_rows in one round
+            if (G != GM || a.wo_rows <= 0 || (long)a.wo_rows * a.max_chunks < a.wo.rows || a.wo_rows > rpr) return -1;
+        } else {                 // mode 4: each kv head's chunk count, up to two rounds of rows
+            if (a.n_kv > 8) return -1;
+            const int nchunk = a.xm_slots, rounds = cpr >= 32 ? 2 : 1;
+            if ((a.wo.rows + nchunk - 1) / nchunk > rounds * rpr) return -1;
+        }
     }
     switch (a.hd) {
         case 48: return f16kv ? dec_pick_g<48, true>(st, a, with_merge) : dec_pick_g<48, false>(st, a, with_merge);

@@ -733,19 +733,27 @@ static int mv(EhipState *s, int pro, int epi, const MatvecArgs &a) {
     return s->ref_order ? launch_matvec_ref(s->st, pro, epi, a) : launch_matvec(s->st, pro, epi, a);
 }
 
-// Whether the decode step folds the wo product into the attention (merge
-// mode 3): the in-kernel merge on the 2-D grid (kv heads a multiple of 8),
-// query heads per kv head a power of two with G * head_dim of 128..1024, and
-// Q8_0 wo (Q8_0 or Q4_0 w1|w3) in every layer.  EHIP_FUSE_WO=0 turns it off.
+// Whether the decode step folds the wo product into the attention: the
+// in-kernel merge on the 2-D grid (kv heads a multiple of 8, merge mode 3:
+// query heads per kv head a power of two, one round of wo rows per
+// workgroup) or on the 1-D grid (at most 8 kv heads, one per XCD, merge mode
+// 4: up to two rounds), with G * head_dim whole 32-weight blocks of 8-64
+// 16-byte chunk lanes per row (the kernel's GM * head_dim / 16), and Q8_0 wo
+// (Q8_0 or Q4_0 w1|w3) in every layer.  EHIP_FUSE_WO=0 turns it off.
 static bool fw_usable(EhipState *s) {
     const EhipModel *m = s->m;
     const EhipConfig &c = m->cfg;
     if (!s->xm_on || s->ref_order || !env_int("EHIP_FUSE_WO", 1)) return false;
-    const int G = c.n_heads / c.n_kv_heads, cpr = G * c.head_dim / 16;
-    if (c.n_kv_heads % 8 || (G & (G - 1)) || (c.head_dim != 64 && c.head_dim != 128) || cpr < 8 || cpr > 64) return false;
-    if (c.n_kv_heads > MATVEC_MAX_PARTS) return false;
-    const int mc = 8 * s->xm_slots / c.n_kv_heads;
-    if ((c.dim + mc - 1) / mc * cpr > ATT_DEC_NW * 64) return false;
+    const int nkv = c.n_kv_heads, G = c.n_heads / nkv, hd = c.head_dim;
+    const int GM = G <= 1 ? 1 : (G <= 2 ? 2 : (G <= 4 ? 4 : 8)), cpr = GM * hd / 16, rpr = ATT_DEC_NW * 64 / cpr;
+    if (G > 8 || (hd != 64 && hd != 128) || (G * hd) % QB || cpr < 8 || cpr > 64) return false;
+    if (nkv > MATVEC_MAX_PARTS) return false;
+    if (nkv % 8 == 0) {
+        const int mc = 8 * s->xm_slots / nkv;
+        if (G != GM || (c.dim + mc - 1) / mc > rpr) return false;
+    } else if ((c.dim + s->xm_slots - 1) / s->xm_slots > (cpr >= 32 ? 2 : 1) * rpr) {
+        return false;
+    }
     for (int l = 0; l < c.n_layers; l++) {
         const DevLayer &y = m->layers[l];
         if (y.wo.dtype != DT_Q8 || (y.w13.dtype != DT_Q8 && y.w13.dtype != DT_Q4)) return false;

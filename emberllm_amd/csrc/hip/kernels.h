@@ -115,11 +115,13 @@ struct AttnArgs {
             uint8_t *kvimg; int kvimg_tiles;
         };
         struct {
-            // decode with xm_cnt on the 2-D grid, optional: the wo product
-            // folded in (Q8_0 wo, every kv group's G * hd columns in whole
-            // 32-weight blocks).  Once kv head g's output is merged into
-            // `out`, its workgroup c computes rows [c wo_rows, (c + 1)
-            // wo_rows) of W_o[:, the group's columns] . o_g into
+            // decode with xm_cnt on the 2-D grid, or on the 1-D grid with at
+            // most 8 kv heads, optional: the wo product folded in (Q8_0 wo,
+            // every kv group's G * hd columns in whole 32-weight blocks).
+            // Once kv head g's output is merged into `out`, its workgroup c
+            // computes rows [c wo_rows, (c + 1) wo_rows) of W_o[:, the
+            // group's columns] . o_g (on the 1-D grid wo_rows is the kernel's
+            // own, from the kv head's chunk count) into
             // wo_part[g][row], with o_g Q8_0-quantized as the decode matvec
             // quantizes its input.  wo_flag[g * XM_CNT_STRIDE] is raised when
             // o_g is complete and must be zero at launch (the next w1|w3

@@ -103,6 +103,36 @@ def test_decode_schedules(schedule, oracle_threads, monkeypatch):
     say(f"{schedule}: " + check_run(res, "qwen3_06b-p16-d32-s11"))
 
 
+@pytest.mark.parametrize("name", ["smollm2_135m", "qwen25_05b"])
+@pytest.mark.parametrize("fold", ["folded-wo", "wo-matvec"])
+def test_decode_fold_1d_grid(name, fold, oracle_threads, monkeypatch):
+    """Shapes whose kv heads are not a multiple of 8 (SmolLM2-135M: 3 kv heads
+    of 3 query heads, Qwen2.5-0.5B: 2 of 7) merge in-kernel on the 1-D grid,
+    one kv head per XCD, and fold the wo product in there (merge mode 4:
+    G * head_dim / 16 of the row's chunk lanes in use, two rounds of rows for
+    Qwen2.5).  With and without the fold (EHIP_FUSE_WO=0) the run must match
+    the oracle past one chunk per workgroup (prompt 300, decode to depth
+    332), and keep its schedule throughout."""
+    if fold == "wo-matvec":
+        monkeypatch.setenv("EHIP_FUSE_WO", "0")
+    want = 3 if fold == "folded-wo" else 1
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    rng = np.random.default_rng(78)
+    ids, toks = rng.integers(0, V, 300), rng.integers(0, V, 32)
+    say(f"{name} {fold} p300 d32")
+    eng = emberllm.Engine(path, ctx=400)
+    assert eng.decode_fusion() == want, f"state chose fusion {eng.decode_fusion()}, expected {want}"
+    orc = oracle.Oracle(path, ctx=400)
+    res = [compare(eng.prefill(ids), orc.prefill(ids))]
+    for i, t in enumerate(toks):
+        res.append(compare(eng.forward(int(t), 300 + i), orc.forward(int(t), 300 + i)))
+    assert eng.decode_fusion() == want, f"the state left fusion {want} during the run"
+    eng.close()
+    orc.close()
+    say(f"{name} {fold}: " + check_run(res, f"{name}-p16-d32-s11"))
+
+
 @pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])
 def test_graph_equals_eager(name):
     """The captured graph replays exactly the eager launch sequence."""
@@ -385,15 +415,17 @@ def test_xcd_check_falls_back_to_the_merge_kernel(name, monkeypatch):
         eng.close()
 
 
-def test_folded_wo_timeout_falls_back(monkeypatch):
+@pytest.mark.parametrize("name", ["qwen3_06b", "smollm2_135m"])
+def test_folded_wo_timeout_falls_back(name, monkeypatch):
     """The folded wo product waits for its kv group's merged output with a
     bounded poll of a flag; on time-out the workgroup raises the error flag
     instead of writing its rows.  EHIP_FW_TEST_SPIN=0 makes every workgroup
     that finds the flag still down time out at once (the kernels otherwise
     run as usual), so the state must switch to the two-kernel schedule for
     good and re-run the work, returning exactly what a state created with
-    that schedule returns, through ember_forward and the device loop."""
-    name = "qwen3_06b"
+    that schedule returns, through ember_forward and the device loop.
+    Qwen3-0.6B folds it on the 2-D grid (merge mode 3), SmolLM2-135M on the
+    1-D grid (mode 4)."""
     path = configs.model_path(name, threads=16)
     V = configs.ALL[name]["vocab_size"]
     ids = np.arange(100) * 89 % V

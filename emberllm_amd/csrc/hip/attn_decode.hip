@@ -134,10 +134,11 @@ template <int HD, bool F16> struct DecLay {
 // its wo_rows rows of the group's wo partial: see AttnArgs::wo); 4 = mode 2
 // with the wo product folded in the same way, each kv head's rows shared
 // over its own chunk count, G * HD / 16 of the CPR lanes per row in use and
-// (CPR >= 32) two rounds of rows per workgroup.
+// (CPR >= 32) two rounds of rows per workgroup; 5 = mode 3 with a Q4_0 wo
+// (one whole 32-weight block per lane: GM * HD / 32 lanes per row).
 template <int HD, int GM, bool F16, int NL, int NW, int XMODE>
 __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
-    constexpr bool XM = XMODE != 0, FW = XMODE >= 3, FW1 = XMODE == 4;
+    constexpr bool XM = XMODE != 0, FW = XMODE >= 3, FW1 = XMODE == 4, FWQ4 = XMODE == 5;
     using L = DecLay<HD, F16>;
     constexpr int PE = L::PE, P = L::P, LPR = L::LPR, RPL = L::RPL;
     constexpr int NT = NW * 64, RPB = NW * RPL;   // threads, rows per workgroup load
@@ -179,11 +180,23 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     const int fw_row = c * a.wo_rows + fw_r;
     int4 fw_q = make_int4(0, 0, 0, 0);
     uint16_t fw_d = 0;
-    if constexpr (FW && !FW1) {
+    if constexpr (FW && !FW1 && !FWQ4) {
         const int rc = min(c * a.wo_rows + min(fw_r, a.wo_rows - 1), a.wo.rows - 1);
         const int col0 = g * G * HD;
         fw_q = *reinterpret_cast<const int4 *>(a.wo.q + (size_t)rc * a.wo.cols + col0 + 16 * fw_j);
         fw_d = a.wo.d[(size_t)rc * (a.wo.cols / QB) + col0 / QB + fw_j / 2];
+    }
+    // mode 5: the lane's Q4_0 block (16 bytes of nibbles) and scale of row
+    // fw_r5 of the workgroup's wo_rows
+    constexpr int CPR5 = GM * HD / 32;
+    const int fw_r5 = tid / CPR5, fw_j5 = tid % CPR5;
+    int4 fw_q5 = make_int4(0, 0, 0, 0);
+    uint16_t fw_d5 = 0;
+    if constexpr (FWQ4) {
+        const int rc = min(c * a.wo_rows + min(fw_r5, a.wo_rows - 1), a.wo.rows - 1);
+        const int blk = g * G * HD / QB + fw_j5;
+        fw_q5 = *reinterpret_cast<const int4 *>(a.wo.q + (size_t)rc * (a.wo.cols / 2) + 16 * blk);
+        fw_d5 = a.wo.d[(size_t)rc * (a.wo.cols / QB) + blk];
     }
     int4 fw_q4[FWR];      // mode 4: rows fw_r + k RPR of the kv head's own wo_rows
     uint16_t fw_d4[FWR];
@@ -227,6 +240,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
     __shared__ int sm_go;
     __shared__ __align__(16) int sm_qx[GM * HD / 4];
     __shared__ float sm_dx[GM * HD / QB];
+    __shared__ int sm_xs[GM * HD / QB];   // mode 5: the blocks' code sums
     if (tid == 0) {
         if (xcc_id() != xcc_want) __hip_atomic_fetch_or(a.xm_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int ok = 1;
@@ -254,8 +268,31 @@ __global__ __launch_bounds__(NW * 64) void k_attn_dec(AttnArgs a) {
         const int q3 = (int)fminf(fmaxf(roundf(x.w * id), -127.0f), 127.0f);
         sm_qx[tid] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
         if ((tid & 7) == 0) sm_dx[tid >> 3] = h2f(f2h(d));
+        if constexpr (FWQ4) {
+            const int xs = sum8(q0 + q1 + q2 + q3);
+            if ((tid & 7) == 0) sm_xs[tid >> 3] = xs;
+        }
     }
     __syncthreads();
+    if constexpr (FWQ4) {   // k_matvec's Q4_0 block: low nibbles x codes 0-15, high x 16-31, minus 8 x code sum
+        const int4 xl = *reinterpret_cast<const int4 *>(&sm_qx[8 * fw_j5]);
+        const int4 xh = *reinterpret_cast<const int4 *>(&sm_qx[8 * fw_j5 + 4]);
+        const int m = 0x0f0f0f0f;
+        int isum = sdot4(fw_q5.x & m, xl.x, 0);
+        isum = sdot4(fw_q5.y & m, xl.y, isum);
+        isum = sdot4(fw_q5.z & m, xl.z, isum);
+        isum = sdot4(fw_q5.w & m, xl.w, isum);
+        isum = sdot4((fw_q5.x >> 4) & m, xh.x, isum);
+        isum = sdot4((fw_q5.y >> 4) & m, xh.y, isum);
+        isum = sdot4((fw_q5.z >> 4) & m, xh.z, isum);
+        isum = sdot4((fw_q5.w >> 4) & m, xh.w, isum);
+        isum -= 8 * sm_xs[fw_j5];
+        float v = ((float)isum * h2f(fw_d5)) * sm_dx[fw_j5];
+        v = group_sum<CPR5>(v);
+        const int row = c * a.wo_rows + fw_r5;
+        if (fw_j5 == 0 && fw_r5 < a.wo_rows && row < a.wo.rows) a.wo_part[(size_t)g * a.wo.rows + row] = v;
+        return;
+    }
     if constexpr (FW1) {
         const int wo_rows = (a.wo.rows + nchunk - 1) / nchunk, cpr_g = G * HD / 16;
         const int fw_jc = min(fw_j, cpr_g - 1);
@@ -387,6 +424,9 @@ template <int HD, bool F16, int GM>
 static void dec_launch(hipStream_t st, const AttnArgs &a, dim3 grid) {
     constexpr int NL = ATT_DEC_NL, NW = ATT_DEC_NW;
     if (!a.xm_cnt) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 0>), grid, dim3(NW * 64), 0, st, a);
+    else if (grid.y > 1 && a.wo_part && a.wo.dtype == DT_Q4) {
+        if constexpr (HD != 48 && GM * HD >= 256) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 5>), grid, dim3(NW * 64), 0, st, a);
+    }
     else if (grid.y > 1 && a.wo_part) {
         if constexpr (HD != 48 && GM * HD >= 128) hipLaunchKernelGGL((k_attn_dec<HD, GM, F16, NL, NW, 3>), grid, dim3(NW * 64), 0, st, a);
     }
@@ -429,8 +469,9 @@ int launch_attn_decode(hipStream_t st, bool f16kv, const AttnArgs &a, bool with_
     }
     if (a.wo_part) {   // the folded wo product: whole 32-weight blocks per kv group, 8-64 chunk lanes per row
         const int G = a.n_heads / a.n_kv, GM = G <= 1 ? 1 : (G <= 2 ? 2 : (G <= 4 ? 4 : 8));
-        const int cpr = GM * a.hd / 16, rpr = ATT_DEC_NW * 64 / cpr;
-        if (!a.xm_cnt || !a.wo_flag || a.wo.dtype != DT_Q8 || !a.wo.q || !a.wo.d) return -1;
+        const bool q4 = a.wo.dtype == DT_Q4;   // mode 5: one block per lane
+        const int cpr = GM * a.hd / (q4 ? 32 : 16), rpr = ATT_DEC_NW * 64 / cpr;
+        if (!a.xm_cnt || !a.wo_flag || (a.wo.dtype != DT_Q8 && !(q4 && a.n_kv % 8 == 0)) || !a.wo.q || !a.wo.d) return -1;
         if ((a.hd != 64 && a.hd != 128) || (G * a.hd) % QB || cpr < 8 || cpr > 64) return -1;
         if (a.wo.cols != a.n_heads * a.hd || a.wo.rows <= 0 || a.wo_spin < 0) return -1;
         if (a.n_kv % 8 == 0) {   // mode 3: G == GM, the host's wo_rows in one round

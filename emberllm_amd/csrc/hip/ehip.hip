@@ -734,18 +734,22 @@ static int mv(EhipState *s, int pro, int epi, const MatvecArgs &a) {
 }
 
 // Whether the decode step folds the wo product into the attention: the
-// in-kernel merge on the 2-D grid (kv heads a multiple of 8, merge mode 3:
-// query heads per kv head a power of two, one round of wo rows per
-// workgroup) or on the 1-D grid (at most 8 kv heads, one per XCD, merge mode
-// 4: up to two rounds), with G * head_dim whole 32-weight blocks of 8-64
-// 16-byte chunk lanes per row (the kernel's GM * head_dim / 16), and Q8_0 wo
-// (Q8_0 or Q4_0 w1|w3) in every layer.  EHIP_FUSE_WO=0 turns it off.
+// in-kernel merge on the 2-D grid (kv heads a multiple of 8, merge mode 3,
+// or 5 with a Q4_0 wo: query heads per kv head a power of two, one round of
+// wo rows per workgroup) or on the 1-D grid (at most 8 kv heads, one per
+// XCD, merge mode 4, Q8_0 wo: up to two rounds), with G * head_dim whole
+// 32-weight blocks of 8-64 chunk lanes per row (the kernel's GM * head_dim
+// / 16 for Q8_0, / 32 for Q4_0), and Q8_0 or Q4_0 w1|w3 in every layer.
+// EHIP_FUSE_WO=0 turns it off.
 static bool fw_usable(EhipState *s) {
     const EhipModel *m = s->m;
     const EhipConfig &c = m->cfg;
     if (!s->xm_on || s->ref_order || !env_int("EHIP_FUSE_WO", 1)) return false;
     const int nkv = c.n_kv_heads, G = c.n_heads / nkv, hd = c.head_dim;
-    const int GM = G <= 1 ? 1 : (G <= 2 ? 2 : (G <= 4 ? 4 : 8)), cpr = GM * hd / 16, rpr = ATT_DEC_NW * 64 / cpr;
+    const int wdt = m->layers[0].wo.dtype;
+    if (wdt != DT_Q8 && !(wdt == DT_Q4 && nkv % 8 == 0)) return false;
+    const int GM = G <= 1 ? 1 : (G <= 2 ? 2 : (G <= 4 ? 4 : 8));
+    const int cpr = GM * hd / (wdt == DT_Q4 ? 32 : 16), rpr = ATT_DEC_NW * 64 / cpr;
     if (G > 8 || (hd != 64 && hd != 128) || (G * hd) % QB || cpr < 8 || cpr > 64) return false;
     if (nkv > MATVEC_MAX_PARTS) return false;
     if (nkv % 8 == 0) {
@@ -756,7 +760,7 @@ static bool fw_usable(EhipState *s) {
     }
     for (int l = 0; l < c.n_layers; l++) {
         const DevLayer &y = m->layers[l];
-        if (y.wo.dtype != DT_Q8 || (y.w13.dtype != DT_Q8 && y.w13.dtype != DT_Q4)) return false;
+        if (y.wo.dtype != wdt || (y.w13.dtype != DT_Q8 && y.w13.dtype != DT_Q4)) return false;
     }
     return true;
 }

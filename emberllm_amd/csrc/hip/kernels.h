@@ -117,7 +117,8 @@ struct AttnArgs {
         struct {
             // decode with xm_cnt on the 2-D grid, or on the 1-D grid with at
             // most 8 kv heads, optional: the wo product folded in (Q8_0 wo,
-            // every kv group's G * hd columns in whole 32-weight blocks).
+            // or Q4_0 on the 2-D grid; every kv group's G * hd columns in
+            // whole 32-weight blocks).
             // Once kv head g's output is merged into `out`, its workgroup c
             // computes rows [c wo_rows, (c + 1) wo_rows) of W_o[:, the
             // group's columns] . o_g (on the 1-D grid wo_rows is the kernel's

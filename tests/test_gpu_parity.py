@@ -103,16 +103,18 @@ def test_decode_schedules(schedule, oracle_threads, monkeypatch):
     say(f"{schedule}: " + check_run(res, "qwen3_06b-p16-d32-s11"))
 
 
-@pytest.mark.parametrize("name", ["smollm2_135m", "qwen25_05b"])
+@pytest.mark.parametrize("name", ["smollm2_135m", "qwen25_05b", "qwen3_06b_q4"])
 @pytest.mark.parametrize("fold", ["folded-wo", "wo-matvec"])
-def test_decode_fold_1d_grid(name, fold, oracle_threads, monkeypatch):
-    """Shapes whose kv heads are not a multiple of 8 (SmolLM2-135M: 3 kv heads
-    of 3 query heads, Qwen2.5-0.5B: 2 of 7) merge in-kernel on the 1-D grid,
-    one kv head per XCD, and fold the wo product in there (merge mode 4:
-    G * head_dim / 16 of the row's chunk lanes in use, two rounds of rows for
-    Qwen2.5).  With and without the fold (EHIP_FUSE_WO=0) the run must match
-    the oracle past one chunk per workgroup (prompt 300, decode to depth
-    332), and keep its schedule throughout."""
+def test_decode_fold(name, fold, oracle_threads, monkeypatch):
+    """The other folds of the wo product.  Shapes whose kv heads are not a
+    multiple of 8 (SmolLM2-135M: 3 kv heads of 3 query heads, Qwen2.5-0.5B: 2
+    of 7) merge in-kernel on the 1-D grid, one kv head per XCD, and fold wo
+    in there (merge mode 4: G * head_dim / 16 of the row's chunk lanes in
+    use, two rounds of rows for Qwen2.5); the Qwen3-0.6B Q4_0 shape folds its
+    Q4_0 wo on the 2-D grid (mode 5: one block per lane).  With and without
+    the fold (EHIP_FUSE_WO=0) the run must match the oracle past one chunk
+    per workgroup (prompt 300, decode to depth 332), and keep its schedule
+    throughout."""
     if fold == "wo-matvec":
         monkeypatch.setenv("EHIP_FUSE_WO", "0")
     want = 3 if fold == "folded-wo" else 1

@@ -413,6 +413,11 @@ struct EhipState {
     // every workgroup that finds the flag still down time out, so the
     // fallback can be exercised while the kernels run as usual)
     int fw_spin;
+    // added to chunk 0's launch token in the in-kernel merge
+    // (EHIP_XMERGE_TEST_TOK, a test hook: 1 makes every merge of a partial
+    // of chunk 0 find a stale token, so the check's fallback can be
+    // exercised while the kernels run as usual)
+    int tok_skew;
     float *part;
     float2 *rope;   // [ctx][hd/2] (cos, sin) of pos * freq_i
     int mc_dec;     // chunks per kv head, two-kernel merge
@@ -589,6 +594,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
     s->m = m; s->ctx = ctx; s->f16kv = kv_fp16 ? 1 : 0; s->esize = kv_fp16 ? 2 : 4;
     s->graph_mode = env_int("EHIP_GRAPH", 1);
     s->fw_spin = env_int("EHIP_FW_TEST_SPIN", ATT_DEC_FW_SPIN);
+    s->tok_skew = env_int("EHIP_XMERGE_TEST_TOK", 0);
     if (hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking) != hipSuccess) {
         set_err("hipStreamCreate failed");
         delete s;
@@ -632,7 +638,7 @@ extern "C" EhipState *ehip_state_create(EhipModel *m, int ctx, int kv_fp16) {
               (s->logits_d = (float *)salloc(s, 4 * ((size_t)c.vocab_size + 4), true)) &&
               (s->xm_cnt = (int *)salloc(s, 4 * (size_t)c.n_layers * c.n_kv_heads * XM_CNT_STRIDE, true)) &&
               (s->xm_xcc = (int *)salloc(s, 4 * (size_t)c.n_kv_heads)) &&
-              (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * std::max(s->mc_dec, s->xm_slots) * (hd + 2))) &&
+              (s->part = (float *)salloc(s, 4 * (size_t)c.n_heads * std::max(s->mc_dec, s->xm_slots) * (hd + 3))) &&
               (s->X = (float *)salloc(s, 4 * pfc * c.dim)) &&
               (s->QKV = (float *)salloc(s, 4 * pfc * (qd + 2 * kvd))) &&
               (s->O = (float *)salloc(s, 4 * pfc * qd)) &&
@@ -780,6 +786,7 @@ static int enq_attn_decode(EhipState *s, int l, bool with_merge = true, bool fw 
         a.xm_cnt = s->xm_cnt + (size_t)l * s->m->cfg.n_kv_heads * XM_CNT_STRIDE;
         a.xm_xcc = s->xm_xcc;
         a.xm_err = s->xm_err;
+        a.tok_skew = s->tok_skew;
         if (fw) {
             const EhipConfig &c = s->m->cfg;
             a.wo = s->m->layers[l].wo;

@@ -77,13 +77,19 @@ struct AttnArgs {
     const int *tokpos;     // fused (decode): device {tok, pos}
     int pos_base;          // unfused (prefill): token b sits at pos_base + b
     int n_tok;
-    float *part;           // decode: chunk partials, o [n_heads][max_chunks][hd] then (m, l) [n_heads][max_chunks]
+    // decode: chunk partials, o [n_heads][max_chunks][hd], then (m, l)
+    // [n_heads][max_chunks], then (with xm_cnt) the launch token of each
+    // chunk's partials, int [n_kv][max_chunks]
+    float *part;
     int max_chunks;
     // decode, optional: merge the chunks of each kv head inside the chunk
     // kernel through the L2 of the one XCD all of them run on.  xm_cnt:
     // arrival counters of this layer, [n_kv] spaced XM_CNT_STRIDE ints apart,
     // zero between launches; xm_xcc: the XCD of each kv head's workgroups;
-    // xm_err: set nonzero by a workgroup that finds itself on another XCD.
+    // xm_err: set nonzero by a workgroup that finds itself on another XCD
+    // (1), by a folded wo product that times out (2) or by a merge that
+    // reads a partial of another launch (4: each carries a token from the
+    // position and tokpos[3]).
     int *xm_cnt; const int *xm_xcc; int *xm_err;
     // with xm_cnt: the grid is 1-D, 8 * xm_slots workgroups (max_chunks =
     // xm_slots); workgroup L takes slot L / 8 of XCD L % 8 (where round-robin
@@ -129,6 +135,9 @@ struct AttnArgs {
             // matvec clears it).  wo_spin bounds the polls of that flag
             // (ATT_DEC_FW_SPIN; a time-out raises the error flag).
             DMat wo; float *wo_part; int *wo_flag; int wo_rows, wo_spin;
+            // decode with xm_cnt (test hook, 0): added to chunk 0's launch
+            // token, so that the merge finds a stale partial
+            int tok_skew;
         };
     };
 };

@@ -187,8 +187,10 @@ int ehip_set_graph_mode(EhipState *s, int mode);
  * merges its chunks itself (no merge kernel), which needs every workgroup of
  * a kv head on one XCD; the state checks that at creation.  Bit 1 = the
  * attention kernel also computes the wo product (no wo matvec launch).  A
- * step whose kernels find a workgroup on another XCD, or whose wo product
- * times out, clears both bits for the rest of the state's life. */
+ * step whose kernels find a workgroup on another XCD, whose wo product
+ * times out, or whose merge reads a chunk's partial of another launch (each
+ * carries a token of its launch), clears both bits for the rest of the
+ * state's life. */
 int ehip_decode_fusion(const EhipState *s);
 /* Time `steps` decode steps at positions pos0.. with HIP events recorded on
  * the state's stream; writes the average step time in ms.  Tokens follow the

@@ -417,6 +417,45 @@ def test_xcd_check_falls_back_to_the_merge_kernel(name, monkeypatch):
         eng.close()
 
 
+@pytest.mark.parametrize("name", ["qwen3_06b", "stories110m", "smollm2_135m"])
+def test_stale_partial_check_falls_back(name, monkeypatch):
+    """Every chunk stores a token of its launch (from the position and the
+    API step's ticket) with its partial, and the in-kernel merge checks each
+    partial it reads carries the current one.  EHIP_XMERGE_TEST_TOK=1 plants a wrong token in
+    chunk 0 (the kernels otherwise run as usual), so the first merge finds a
+    'stale' partial: the state must then switch to the two-kernel schedule
+    for good and re-run the work, returning exactly what a state created with
+    that schedule (EHIP_XMERGE=0) returns, through ember_forward and the
+    device loop.  Qwen3-0.6B merges on the 2-D grid with the folded wo
+    (mode 3), stories110M on the 1-D grid (mode 2), SmolLM2-135M on the 1-D
+    grid with the folded wo (mode 4)."""
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    ids = np.arange(100) * 83 % V   # several chunks per kv head, so the merge (and its check) runs
+    say(f"stale partial check: planted token ({name})")
+    monkeypatch.setenv("EHIP_XMERGE", "0")
+    ref = emberllm.Engine(path, ctx=160)
+    assert ref.decode_fusion() & 3 == 0
+    tok0 = int(np.argmax(ref.prefill(ids)))
+    want_fwd = ref.forward(tok0, len(ids))
+    want_toks, _ = ref.generate_greedy(tok0, len(ids), 9)
+    ref.close()
+    monkeypatch.delenv("EHIP_XMERGE")
+    monkeypatch.setenv("EHIP_XMERGE_TEST_TOK", "1")
+    for path_kind in ("forward", "device loop"):
+        eng = emberllm.Engine(path, ctx=160)
+        if not eng.decode_fusion() & 1:
+            eng.close()
+            pytest.skip("this GPU does not place a kv head's workgroups on one XCD; the merge runs as a second kernel")
+        eng.prefill(ids)
+        if path_kind == "forward":
+            np.testing.assert_array_equal(eng.forward(tok0, len(ids)), want_fwd)
+        got, _ = eng.generate_greedy(tok0, len(ids), 9)
+        np.testing.assert_array_equal(got, want_toks)
+        assert eng.decode_fusion() & 3 == 0, "the state must keep the two-kernel schedule after the check fired"
+        eng.close()
+
+
 @pytest.mark.parametrize("name", ["qwen3_06b", "smollm2_135m"])
 def test_folded_wo_timeout_falls_back(name, monkeypatch):
     """The folded wo product waits for its kv group's merged output with a

@@ -1117,6 +1117,7 @@ static SampleArgs sample_args(EhipState *s, const SampleParams &p, int cap, int 
     a.am_val = s->am_val; a.am_idx = s->am_idx;
     a.tokpos = s->tokpos_d; a.out = s->gen_tok; a.cap = s->ctx;
     a.we = s->smp_we; a.wkeys = s->smp_wk; a.wcum = s->smp_wcum;
+    a.exact = s->ref_order;   // every operation in the reference's order, the softmax sum included
     return a;
 }
 

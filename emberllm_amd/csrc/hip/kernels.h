@@ -306,6 +306,9 @@ struct SampleArgs {
     // top_k = 0 or > SAMPLE_TOPK_MAX: every token's e [n], the sort keys
     // [2][sample_wide_pad(n)] and the running sums of the walk [n]
     float *we; unsigned long long *wkeys; float *wcum;
+    // 1: that whole-vocabulary path for every top_k, so the softmax sum is
+    // the reference's sequential one too (the reference-order mode)
+    int exact;
 };
 int launch_sample(hipStream_t st, const SampleArgs &a);
 // keys sorted per sampler call with any top_k: n rounded up to a power of two

@@ -791,7 +791,7 @@ int launch_sample(hipStream_t st, const SampleArgs &a) {
         hipLaunchKernelGGL(k_samp_greedy_emit, dim3(1), dim3(64), 0, st, a);
         return 0;
     }
-    const bool wide = a.p.top_k < 1 || a.p.top_k > SAMPLE_TOPK_MAX;
+    const bool wide = a.exact || a.p.top_k < 1 || a.p.top_k > SAMPLE_TOPK_MAX;
     SampleArgs b = a;
     if (pen || b.nparts <= 0) {   // per-part maxima of the logits as they now are
         ArgmaxArgs g{};

@@ -95,6 +95,29 @@ def test_device_sampler_matches_host_on_vocab_logits(params):
     eng.close()
 
 
+@pytest.mark.parametrize("top_k", [40, 64, 5])
+def test_reference_order_sampler_takes_the_sequential_path(top_k, monkeypatch):
+    """In the reference-order mode every top_k goes through the
+    whole-vocabulary path, whose softmax sum and running sums are the
+    reference's sequential ones (sample.c:131-133, 149-175): the device draws
+    equal the host sampler's by construction, not only on these rows."""
+    V = 151936
+    monkeypatch.setenv("EHIP_ORDER", "reference")
+    say(f"vocab {V}: reference order, top_k {top_k}")
+    eng = emberllm.Engine(small_model(V))
+    rng = np.random.default_rng(13)
+    a = sampler(0.8, 0.9, top_k, 91)
+    b = sampler(0.8, 0.9, top_k, 91)
+    for step in range(24):
+        lg = rng.normal(0, 3, V).astype(np.float32)
+        lg[rng.integers(0, V, 16)] = lg[int(np.argmax(lg))]      # ties at the top
+        x = lg.copy()
+        host = lib().ember_sample(ctypes.byref(b), x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), V)
+        dev = eng.sample(lg, a)
+        assert dev == host and a.rng_state == b.rng_state, (step, dev, host)
+    eng.close()
+
+
 @pytest.mark.parametrize("top_k", [50, 0], ids=["k50", "k0"])
 @pytest.mark.parametrize("kind", ["flat", "two-level", "quantized", "one-hot", "spread-ties"])
 def test_device_sampler_degenerate_logits(kind, top_k):

@@ -1282,12 +1282,14 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             g3.xf = q.xf; g3.out = s->H; g3.out_stride = 2 * hid;
             GemmArgs g4{};
             g4.W = y.w2; g4.units = c.dim; g4.n = mt; g4.qx = s->qx; g4.dx = s->dxp; g4.xs = s->xsum;
-            // short prompts: the SwiGLU and its quantization in the w1|w3
-            // product's epilogue (the gate | up rows written only for a capture)
+            // the SwiGLU and its quantization in the w1|w3 product's epilogue
+            // (the gate | up rows written only for a capture): the short-prompt
+            // kernel, or the matrix-core tiles (EHIP_PF_SWIGLU=0 keeps those
+            // passes on the product + k_quant_rows)
             GemmArgs gs = g3;
             gs.units = hid; gs.pair_off = hid; gs.oq = s->qx2; gs.odx = s->dxp2; gs.oxs = s->xsum2;
             gs.out = snap ? s->H : nullptr;
-            if (!q.xf && gemm_swiglu_fits(gs)) {
+            if (!q.xf && (gemm_swiglu_fits(gs) || (env_int("EHIP_PF_SWIGLU", 1) && gemm_swiglu_long_fits(gs)))) {
                 rc |= launch_gemm_swiglu(s->st, gs);
                 if (psnap(DBG_H, s->H, 2 * hid, 2 * hid)) return -1;
                 g4.qx = s->qx2; g4.dx = s->dxp2; g4.xs = s->xsum2;

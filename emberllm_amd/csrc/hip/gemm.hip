@@ -276,6 +276,15 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
     const int K = a.W.cols, nb = K / QB, nbh = SP == 1 ? nb : ((nb + 1) / 2 + GM_KB - 1) / GM_KB * GM_KB;
     const int bp0 = pl * nbh, nbp = min(nb, bp0 + nbh) - bp0, nst = (nbh + GM_KB - 1) / GM_KB;
     const int wu = (wave & 1) * 64, wt = (wave >> 1) * (TT / 2);   // this wave's 64 x TT/2 corner
+    // the weight row of tile row r: u0 + r, or with EPI_SWIGLU the (gate, up)
+    // pair of hidden unit c0 + r / 2 (gate rows first in W, up rows at
+    // pair_off), so that a gate and its up product land in neighbouring
+    // accumulators of one lane and a wave's 64 rows are one 32-unit block of h
+    const int c0 = blockIdx.x * (GM_U / 2);
+    auto wrow_of = [&](int r) __attribute__((always_inline)) {
+        if constexpr (EPI == EPI_SWIGLU) return min(c0 + (r >> 1), a.units - 1) + ((r & 1) ? a.pair_off : 0);
+        else return min(u0 + r, a.units - 1);
+    };
 
     // global -> registers for one stage: weights (WROW bytes per row), codes, scales
     constexpr int WLD = GM_U * WROW / 16 / WG, XLD = GM_T * XROW / 16 / WG;
@@ -291,7 +300,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < WLD; i++) {
             const int f = tid + i * WG, row = f / (WROW / 16), c = (f % (WROW / 16)) * 16;
-            const int u = min(u0 + row, a.units - 1), blk = min(b0 + c / WB, nb - 1);
+            const int u = wrow_of(row), blk = min(b0 + c / WB, nb - 1);
             wr[i] = *reinterpret_cast<const i32x4 *>(a.W.q + (size_t)u * (nb * WB) + (size_t)blk * WB + c % WB);
         }
 #pragma unroll
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < NDW; i++) {
             const int f = tid + i * WG, kb = f / GM_U, r = f % GM_U;
-            dwr[i] = a.W.d[(size_t)min(u0 + r, a.units - 1) * nb + min(b0 + kb, nb - 1)];
+            dwr[i] = a.W.d[(size_t)wrow_of(r) * nb + min(b0 + kb, nb - 1)];
         }
 #pragma unroll
         for (int i = 0; i < NDX; i++) {
@@ -408,6 +417,62 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
             for (int y = 0; y < NY; y++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[x][y][r] += xch[((x * NY + y) * 16 + r) * WG + tid];
+    }
+    if constexpr (EPI == EPI_SWIGLU) {
+        // h = silu(gate) * up for the wave's block of 32 hidden units (lane j
+        // holds 16 of them for token column j, lane j + 32 the other 16), then
+        // the Q8_0 codes, fp16-rounded scale and code sum of k_quant_rows'
+        // SwiGLU rows: the same values (the block maximum and the code sum do
+        // not depend on their order)
+        const int hb0 = c0 + wu / 2, nbo = a.units / QB;
+#pragma unroll
+        for (int y = 0; y < NY; y++) {
+            const int t = t0 + wt + 32 * y + j;
+            float v[2][8];
+            float mx = 0.0f;
+#pragma unroll
+            for (int x = 0; x < 2; x++)
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float g = acc[x][y][2 * k], u = acc[x][y][2 * k + 1];
+                    v[x][k] = g / (1.0f + expf(-g)) * u;
+                    mx = fmaxf(mx, fabsf(v[x][k]));
+                }
+            if (a.out && t < a.n)   // the gate | up products themselves, where asked for
+#pragma unroll
+                for (int x = 0; x < 2; x++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int hu = hb0 + (32 * x + mrow(r, h)) / 2;
+                        a.out[(size_t)t * a.out_stride + ((r & 1) ? a.pair_off : 0) + hu] = acc[x][y][r];
+                    }
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float dq = mx / 127.0f;
+            const float id = dq > 0.0f ? 1.0f / dq : 0.0f;
+            int cs = 0;
+            int cq[2][8];
+#pragma unroll
+            for (int x = 0; x < 2; x++)
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    cq[x][k] = (int)fminf(fmaxf(roundf(v[x][k] * id), -127.0f), 127.0f);
+                    cs += cq[x][k];
+                }
+            cs += __shfl_xor(cs, 32);
+            if (t >= a.n) continue;
+            // accumulators 4kk, 4kk + 2 hold hidden units 16x + 2h + 4kk and the next one
+#pragma unroll
+            for (int x = 0; x < 2; x++)
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+                    *reinterpret_cast<uint16_t *>(a.oq + (size_t)t * a.units + hb0 + 16 * x + 2 * h + 4 * kk) =
+                        (uint16_t)(((uint32_t)cq[x][2 * kk] & 0xffu) | (((uint32_t)cq[x][2 * kk + 1] & 0xffu) << 8));
+            if (h == 0) {
+                a.odx[(size_t)t * nbo + hb0 / QB] = h2f(f2h(dq));
+                a.oxs[(size_t)t * nbo + hb0 / QB] = cs;
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int x = 0; x < 2; x++)
@@ -1084,6 +1149,27 @@ constexpr int GS_SPLIT2_MAX_GRID = 1024;
 // take 16-unit tiles instead.
 constexpr int GS_U16_MAX_GRID = 128;
 
+// k_gemm_mfma's tiles for gu 128-row tiles of units and n tokens: 64-token
+// tiles while 128-token tiles give fewer than two workgroups per CU (the
+// epilogue's dependent chains want the waves: Qwen3-0.6B-shape pp1024 6.64
+// -> 6.23 ms; from 512 workgroups on the 128-token tiles are as fast or
+// faster), and when they fill whole rounds of the GPU's workgroup slots where
+// 128-token tiles would not: a 256-CU part holds 3 of those per CU (166
+// VGPRs) and 4 of these (110), so a 4096-token q|k|v product (1,024 or 2,048
+// workgroups) runs two full rounds of 64-token tiles instead of one and a
+// third (pp4096 19.95 -> 19.55 ms).  Products over at least GEMM_SPLIT_MIN_K
+// inputs take the fused block scaling (see k_gemm_mfma), and Q8_0 64-token
+// grids of at most two workgroups per CU split K over two pipelines
+// (Qwen3-0.6B shape: pp512 3.93 -> 3.78 ms, pp1024 5.85 -> 5.78, pp4096
+// 18.81 -> 18.72).
+static void mfma_shape(long gu, int n, int cols, bool *t64, bool *fused, bool *sp2) {
+    const long g128 = gu * ((n + 127) / 128), gt64 = gu * ((n + 63) / 64);
+    auto fill = [](long g, long slots) { return (double)g / (double)(((g + slots - 1) / slots) * slots); };
+    *t64 = g128 < 512 || fill(gt64, 4 * 256) > fill(g128, 3 * 256) + 0.1;
+    *fused = cols >= GEMM_SPLIT_MIN_K;
+    *sp2 = *fused && *t64 && gt64 <= 2 * 256;
+}
+
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
     if (a.W.cols % QB != 0 || a.n <= 0) return -1;
     if (a.W.dtype == DT_Q8 || a.W.dtype == DT_Q4) {
@@ -1127,25 +1213,9 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
 #undef GSL
 #undef GSK
         }
-        // 64-token tiles while 128-token tiles give fewer than two
-        // workgroups per CU (the epilogue's dependent chains want the waves:
-        // Qwen3-0.6B-shape pp1024 6.64 -> 6.23 ms; from 512 workgroups on the
-        // 128-token tiles are as fast or faster), and when they fill whole
-        // rounds of the GPU's workgroup slots where 128-token tiles would not:
-        // a 256-CU part holds 3 of those per CU (166 VGPRs) and 4 of these
-        // (110), so a 4096-token q|k|v product (1,024 or 2,048 workgroups)
-        // runs two full rounds of 64-token tiles instead of one and a third
-        // (pp4096 19.95 -> 19.55 ms)
-        const long g128 = (long)gu * ((a.n + 127) / 128), gt64 = (long)gu * ((a.n + 63) / 64);
-        auto fill = [](long g, long slots) { return (double)g / (double)(((g + slots - 1) / slots) * slots); };
-        const bool t64 = g128 < 512 || fill(gt64, 4 * 256) > fill(g128, 3 * 256) + 0.1;
+        bool t64, fused, sp2;   // (mfma_shape)
+        mfma_shape(gu, a.n, a.W.cols, &t64, &fused, &sp2);
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
-        // products over at least GEMM_SPLIT_MIN_K inputs take the fused block
-        // scaling (see k_gemm_mfma), and Q8_0 64-token grids of at most two
-        // workgroups per CU split K over two pipelines (Qwen3-0.6B shape:
-        // pp512 3.93 -> 3.78 ms, pp1024 5.85 -> 5.78, pp4096 18.81 -> 18.72)
-        const bool fused = a.W.cols >= GEMM_SPLIT_MIN_K;
-        const bool sp2 = fused && t64 && gt64 <= 2 * 256;
 #define GMK(DT, TT, FU, SP)                                                                             \
         if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); \
         else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); \
@@ -1183,7 +1253,29 @@ bool gemm_swiglu_fits(const GemmArgs &a) {
     return ((nb + sp - 1) / sp + GS_KB - 1) / GS_KB <= sw_ring(sp);
 }
 
+// longer passes: k_gemm_mfma's EPI_SWIGLU form over hidden-unit pairs, on the
+// tiles launch_gemm would give the w1|w3 product
+bool gemm_swiglu_long_fits(const GemmArgs &a) {
+    if ((a.W.dtype != DT_Q8 && a.W.dtype != DT_Q4) || a.n <= 0 || a.W.cols % QB != 0) return false;
+    if (!a.oq || !a.odx || !a.oxs || a.pair_off < a.units || a.units % (GM_U / 2) != 0) return false;
+    const long g64 = (long)(2 * a.units / GM_U) * ((a.n + 63) / 64);
+    return !(g64 < 256 || (2 * a.units <= 1024 && g64 < 512));
+}
+
 int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a) {
+    if (gemm_swiglu_long_fits(a)) {
+        const long gu = 2 * a.units / GM_U;
+        bool t64, fused, sp2;
+        mfma_shape(gu, a.n, a.W.cols, &t64, &fused, &sp2);
+        const dim3 g((unsigned)gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
+#define GMS(DT, TT, FU, SP) { hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_SWIGLU, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); return 0; }
+#define GMSF(DT, TT) if (fused) GMS(DT, TT, true, 1) else GMS(DT, TT, false, 1)
+        if (a.W.dtype == DT_Q8 && sp2) GMS(DT_Q8, 64, true, 2)
+        if (a.W.dtype == DT_Q8) { if (t64) { GMSF(DT_Q8, 64) } else { GMSF(DT_Q8, 128) } }
+        if (t64) { GMSF(DT_Q4, 64) } else { GMSF(DT_Q4, 128) }
+#undef GMSF
+#undef GMS
+    }
     if (!gemm_swiglu_fits(a)) return -1;
     const int nb = a.W.cols / QB, sp = nb >= GS_SPLIT_MIN_BLOCKS ? 2 : 1;
     const bool full = nb % (GS_KB * sp) == 0;

@@ -254,6 +254,10 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a);
 // receives the gate | up products (out_stride floats per token).  Returns -1
 // where gemm_swiglu_fits() is false.
 bool gemm_swiglu_fits(const GemmArgs &a);
+// the same for the passes launch_gemm gives the matrix-core tiles: the
+// gate | up rows paired per tile, SwiGLU and quantization in the epilogue
+// (units a multiple of 64)
+bool gemm_swiglu_long_fits(const GemmArgs &a);
 int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a);
 // The q|k|v product of a short prompt with launch_qkpost's work (bias, then
 // QK-norm and RoPE of the q and k heads, q written back into p.qkv, k and v

@@ -135,6 +135,31 @@ def test_decode_fold(name, fold, oracle_threads, monkeypatch):
     say(f"{name} {fold}: " + check_run(res, f"{name}-p16-d32-s11"))
 
 
+@pytest.mark.parametrize("name,n", [("qwen3_06b", 600), ("qwen3_06b", 4096), ("qwen3_06b_q4", 512),
+                                    ("qwen25_05b", 300), ("stories110m", 520)])
+def test_prefill_fused_swiglu_equals_separate(name, n, monkeypatch):
+    """Passes long enough for the matrix-core GEMM tiles quantize the SwiGLU
+    rows in the w1|w3 product's epilogue (k_gemm_mfma's EPI_SWIGLU form: gate
+    and up rows paired in each tile).  Its codes, scales and code sums are
+    the ones k_quant_rows makes from the stored products, so the prefill's
+    logits and KV rows equal those of the separate kernels
+    (EHIP_PF_SWIGLU=0) bit for bit; Q8_0 and Q4_0 weights, 64- and 128-token
+    tiles."""
+    path = configs.model_path(name, threads=16)
+    V, L = configs.ALL[name]["vocab_size"], configs.ALL[name]["n_layers"]
+    ids = np.random.default_rng(n).integers(0, V, n)
+    say(f"{name} pp{n}: fused SwiGLU quantization vs separate kernels")
+    out = []
+    for fused in ("0", "1"):
+        monkeypatch.setenv("EHIP_PF_SWIGLU", fused)
+        eng = emberllm.Engine(path, ctx=n + 8)
+        lg = eng.prefill(ids)
+        out.append((lg, eng.kv_read(0, L - 1, n), eng.kv_read(1, L - 1, n)))
+        eng.close()
+    for a, b in zip(out[0], out[1]):
+        np.testing.assert_array_equal(a, b)
+
+
 @pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])
 def test_graph_equals_eager(name):
     """The captured graph replays exactly the eager launch sequence."""

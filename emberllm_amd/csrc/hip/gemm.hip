@@ -13,7 +13,9 @@
 // block applies the reference's order sum += ((float)isum * dw) * dx
 // (vecdot_q8 / vecdot_q4, kernels.c:151-183), or for products over at least
 // GEMM_SPLIT_MIN_K inputs (FUSED) sum = fma((float)isum, dw * dx, sum): one
-// rounding and one VALU operation fewer per output and block.  Those
+// rounding and one VALU operation fewer per output and block, and with the
+// scale products dw * dx of a tile taken from one fp16 matrix instruction
+// (exact: both are fp16 values) a second VALU operation fewer.  Those
 // products already split their block sums over pipelines elsewhere (the
 // short-prompt and decode products), so the models they belong to run at the
 // reference builds' own noise floor; the others keep the reference's order.
@@ -252,6 +254,8 @@ __global__ __launch_bounds__(WG) void k_gemm(GemmArgs a) {
 // twice the waves per SIMD for grids of at most two workgroups per CU.
 constexpr int GM_U = 128;
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
@@ -265,11 +269,15 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
     static_assert(SP == 1 || (SP == 2 && FUSED && TT == 64 && DT == DT_Q8), "split pipelines: fused Q8_0, 64-token tiles");
     __shared__ __align__(16) uint8_t wsp[SP][2][GM_U * WROW];
     __shared__ __align__(16) int8_t xsp[SP][2][GM_T * XROW];
+    // fp32 scales, or with FUSED the fp16 scale bits (the first half of each
+    // array: [buf][kb][row] packed at the same strides in uint16 units)
     __shared__ float dwp[SP][2][GM_KB][GM_U], dxp[SP][2][GM_KB][GM_T];
     __shared__ int sxp[SP][2][GM_KB][GM_T];
     const int tid = SP == 1 ? (int)threadIdx.x : (int)threadIdx.x % WG, pl = SP == 1 ? 0 : (int)threadIdx.x / WG;
     const int lane = tid & 63, wave = tid >> 6;
     auto &ws = wsp[pl]; auto &xsm = xsp[pl]; auto &dws = dwp[pl]; auto &dxs = dxp[pl]; auto &sxs = sxp[pl];
+    uint16_t (*dwh)[GM_KB][GM_U] = reinterpret_cast<uint16_t (*)[GM_KB][GM_U]>(&dwp[pl][0][0][0]);
+    uint16_t (*dxh)[GM_KB][GM_T] = reinterpret_cast<uint16_t (*)[GM_KB][GM_T]>(&dxp[pl][0][0][0]);
     const int j = lane & 31, h = lane >> 5;
     const int u0 = blockIdx.x * GM_U, t0 = blockIdx.y * GM_T;
     // pipeline pl: blocks [bp0, bp0 + nbp); pipeline 0 has the most stages
@@ -331,13 +339,16 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < NDW; i++) {
             const int f = tid + i * WG;
-            dws[buf][f / GM_U][f % GM_U] = h2f(dwr[i]);
+            if constexpr (FUSED) dwh[buf][f / GM_U][f % GM_U] = dwr[i];
+            else dws[buf][f / GM_U][f % GM_U] = h2f(dwr[i]);
         }
 #pragma unroll
         for (int i = 0; i < NDX; i++) {
             const int f = tid + i * WG;
             if (f < GM_KB * GM_T) {
-                dxs[buf][f / GM_T][f % GM_T] = dxr[i];
+                // activation scales are fp16 values held as fp32: exact both ways
+                if constexpr (FUSED) dxh[buf][f / GM_T][f % GM_T] = f2h(dxr[i]);
+                else dxs[buf][f / GM_T][f % GM_T] = dxr[i];
                 sxs[buf][f / GM_T][f % GM_T] = xsr[i];
             }
         }
@@ -375,20 +386,54 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
             for (int y = 0; y < NY; y++)
                 bf[y] = *reinterpret_cast<const i32x4 *>(xsm[buf] + (size_t)(wt + 32 * y + j) * XROW + kb * 32 + 16 * h);
+            // FUSED: the block's scale products dw * dx of a 32 x 32 tile as
+            // one fp16 matrix instruction, an outer product (weight scales in
+            // element 0 of A's lanes 0..31, activation scales in element 0 of
+            // B's, every other element zero, so no scale meets another
+            // block's).  A product of two fp16 values is exact in fp32, so
+            // these are the bits of the fp32 multiply, and the epilogue keeps
+            // a conversion and an fma per output.
+            f16x4 sa[2], sb[NY];
+            if constexpr (FUSED) {
+#pragma unroll
+                for (int x = 0; x < 2; x++) {
+                    sa[x] = f16x4{};
+                    sa[x][0] = __builtin_bit_cast(_Float16, (uint16_t)(h ? 0 : dwh[buf][kb][wu + 32 * x + j]));
+                }
+#pragma unroll
+                for (int y = 0; y < NY; y++) {
+                    sb[y] = f16x4{};
+                    sb[y][0] = __builtin_bit_cast(_Float16, (uint16_t)(h ? 0 : dxh[buf][kb][wt + 32 * y + j]));
+                }
+            }
 #pragma unroll
             for (int x = 0; x < 2; x++)
 #pragma unroll
                 for (int y = 0; y < NY; y++) {
                     i32x16 d = {};
                     d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[x], bf[y], d, 0, 0, 0);
-                    const float dx = dxs[buf][kb][wt + 32 * y + j];
                     const int xsum = DT == DT_Q4 ? sxs[buf][kb][wt + 32 * y + j] : 0;
+                    if constexpr (FUSED) {
+                        const f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[x], sb[y], f32x16{}, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
-                        const float dw = dws[buf][kb][wu + 32 * x + mrow(r, h)];
-                        if (FUSED) acc[x][y][r] = fmaf((float)isum, dw * dx, acc[x][y][r]);
-                        else acc[x][y][r] += ((float)isum * dw) * dx;
+                        for (int r = 0; r < 16; r++) {
+                            const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
+                            acc[x][y][r] = fmaf((float)isum, sc[r], acc[x][y][r]);
+                        }
+                        // 128-token tiles: each tile's products and epilogue
+                        // stay together (the compiler otherwise hoists the
+                        // scale products: 176 VGPRs, two waves per SIMD
+                        // instead of three; 114.6 -> 102.8 us per 4096-token
+                        // w1|w3 product with the barrier)
+                        if constexpr (TT == 128) __builtin_amdgcn_sched_barrier(0);
+                    } else {
+                        const float dx = dxs[buf][kb][wt + 32 * y + j];
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
+                            const float dw = dws[buf][kb][wu + 32 * x + mrow(r, h)];
+                            acc[x][y][r] += ((float)isum * dw) * dx;
+                        }
                     }
                 }
         }
@@ -560,6 +605,9 @@ void k_gemm_small(GemmArgs a) {
     float (&dwq)[2][GS_KB][U] = dws[q];
     float (&dxq)[2][GS_KB][GS_T] = dxs[q];
     int (&sxq)[2][GS_KB][GS_T] = sxs[q];
+    // SPLIT > 1: the scales as fp16 bits (the first half of each array)
+    uint16_t (&dwhq)[2][GS_KB][U] = *reinterpret_cast<uint16_t (*)[2][GS_KB][U]>(&dws[q][0][0][0]);
+    uint16_t (&dxhq)[2][GS_KB][GS_T] = *reinterpret_cast<uint16_t (*)[2][GS_KB][GS_T]>(&dxs[q][0][0][0]);
 
     // the epilogue's residual (or bias) values: their loads go out first, so
     // the stores at the end do not wait for a round trip (not in the
@@ -640,9 +688,14 @@ void k_gemm_small(GemmArgs a) {
             const int c = tid + i * NTP;
             *reinterpret_cast<i32x4 *>(xsq[buf] + (c / (XROW / 16)) * XP + (c % (XROW / 16)) * 16) = xr[j][i];
         }
-        if (lsw) dwq[buf][skw][srw] = h2f(dwr[j]);
+        if (lsw) {
+            if constexpr (SPLIT > 1) dwhq[buf][skw][srw] = dwr[j];
+            else dwq[buf][skw][srw] = h2f(dwr[j]);
+        }
         if (lsx) {
-            dxq[buf][skx][srx] = dxr[j];
+            // activation scales are fp16 values held as fp32: exact both ways
+            if constexpr (SPLIT > 1) dxhq[buf][skx][srx] = f2h(dxr[j]);
+            else dxq[buf][skx][srx] = dxr[j];
             if (DT == DT_Q4) sxq[buf][skx][srx] = xsr[j];
         }
     };
@@ -661,6 +714,7 @@ void k_gemm_small(GemmArgs a) {
         long af[GS_KB], bf[GS_KB];
         float dx[GS_KB];
         f32x4 dw[GS_KB];
+        f16x4 sa[GS_KB], sb[GS_KB];
         int xsum[GS_KB];
 #pragma unroll
         for (int kb = 0; kb < GS_KB; kb++) {
@@ -672,8 +726,18 @@ void k_gemm_small(GemmArgs a) {
                 af[kb] = (long)((raw >> (4 * (fg >> 1))) & 0x0f0f0f0f0f0f0f0full);
             }
             bf[kb] = *reinterpret_cast<const long *>(xsq[buf] + (wt + fr) * XP + kb * 32 + 8 * fg);
-            dx[kb] = dxq[buf][kb][wt + fr];
-            dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wu + 4 * fg]);
+            if constexpr (SPLIT > 1) {
+                // the scale products as a 16 x 16 x 16 fp16 outer product
+                // (k_gemm_mfma's FUSED form): weight scale of row wu + fr and
+                // token scale of column wt + fr in element 0 of lanes 0..15
+                sa[kb] = f16x4{};
+                sb[kb] = f16x4{};
+                sa[kb][0] = __builtin_bit_cast(_Float16, (uint16_t)(fg ? 0 : dwhq[buf][kb][wu + fr]));
+                sb[kb][0] = __builtin_bit_cast(_Float16, (uint16_t)(fg ? 0 : dxhq[buf][kb][wt + fr]));
+            } else {
+                dx[kb] = dxq[buf][kb][wt + fr];
+                dw[kb] = *reinterpret_cast<const f32x4 *>(&dwq[buf][kb][wu + 4 * fg]);
+            }
             xsum[kb] = DT == DT_Q4 ? sxq[buf][kb][wt + fr] : 0;
         }
         i32x4 d[GS_KB];
@@ -683,11 +747,19 @@ void k_gemm_small(GemmArgs a) {
 #pragma unroll
         for (int kb = 0; kb < GS_KB; kb++) {
             if (kb >= nkb) break;
+            if constexpr (SPLIT > 1) {
+                const f32x4 sc = __builtin_amdgcn_mfma_f32_16x16x16f16(sa[kb], sb[kb], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
-                if (SPLIT > 1) acc[r] = fmaf((float)isum, dw[kb][r] * dx[kb], acc[r]);
-                else acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+                for (int r = 0; r < 4; r++) {
+                    const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
+                    acc[r] = fmaf((float)isum, sc[r], acc[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int isum = DT == DT_Q4 ? d[kb][r] - 8 * xsum[kb] : d[kb][r];
+                    acc[r] += ((float)isum * dw[kb][r]) * dx[kb];
+                }
             }
         }
     };
@@ -1177,11 +1249,14 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         // (a 256-CU part); 64-token tiles then double the grid
         const int gu = (a.units + GM_U - 1) / GM_U;
         // 32 x 32 tiles for short prompts, and for the narrow (<= 1024-output)
-        // wo / w2 products up to twice that grid (at 2048 tokens +2% over the
-        // 64-token tiles below; at 4096 tokens the tiles below are faster:
-        // pp4096 22.9 -> 21.2 ms)
+        // wo / w2 products over fewer than GEMM_SPLIT_MIN_K inputs up to twice
+        // that grid (at 2048 tokens +2% over the 64-token tiles below).  The
+        // longer narrow products take the tiles below from 256 workgroups on:
+        // with the fused block scaling's matrix-core scale products they are
+        // faster there (Qwen3-0.6B shape, 2048 tokens: 55.6 -> 42.1 us per wo
+        // or w2 product; 4096 tokens: pp4096 22.9 -> 21.2 ms)
         const long g64 = (long)gu * ((a.n + 63) / 64);
-        if (g64 < 256 || (a.units <= 1024 && g64 < 512)) {
+        if (g64 < 256 || (a.units <= 1024 && g64 < 512 && a.W.cols < GEMM_SPLIT_MIN_K)) {
             // 16-unit tiles when 32-unit ones would leave half the CUs idle
             const int ty = (a.n + GS_T - 1) / GS_T;
             const bool u16 = (long)((a.units + 31) / 32) * ty <= GS_U16_MAX_GRID;

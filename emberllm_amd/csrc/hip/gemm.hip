@@ -265,10 +265,16 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
     constexpr int GM_T = TT, NY = TT / 64;            // tokens per tile, MFMA tiles per wave along tokens
     constexpr int WB = DT == DT_Q8 ? 32 : 16;          // weight bytes per row and block
     constexpr int WROW = GM_KB * WB, XROW = GM_KB * 32; // stage bytes per row
+    // LDS row pitches: 16 bytes of padding, so the fragment reads (lanes j
+    // at rows j, 16 bytes each) spread over the banks; at the bare 64-byte
+    // (Q4_0 weights: 32-byte) pitch every eight lanes of a read met on the
+    // same banks, and the LDS spent as many cycles stalled on bank conflicts
+    // as serving reads
+    constexpr int WP = WROW + 16, XP = XROW + 16;
     static_assert(TT == 64 || TT == 128, "token tile of 64 or 128");
     static_assert(SP == 1 || (SP == 2 && FUSED && TT == 64 && DT == DT_Q8), "split pipelines: fused Q8_0, 64-token tiles");
-    __shared__ __align__(16) uint8_t wsp[SP][2][GM_U * WROW];
-    __shared__ __align__(16) int8_t xsp[SP][2][GM_T * XROW];
+    __shared__ __align__(16) uint8_t wsp[SP][2][GM_U * WP];
+    __shared__ __align__(16) int8_t xsp[SP][2][GM_T * XP];
     // fp32 scales, or with FUSED the fp16 scale bits (the first half of each
     // array: [buf][kb][row] packed at the same strides in uint16 units)
     __shared__ float dwp[SP][2][GM_KB][GM_U], dxp[SP][2][GM_KB][GM_T];
@@ -333,9 +339,15 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
     };
     auto store = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < WLD; i++) reinterpret_cast<i32x4 *>(ws[buf])[tid + i * WG] = wr[i];
+        for (int i = 0; i < WLD; i++) {
+            const int f = tid + i * WG;
+            *reinterpret_cast<i32x4 *>(ws[buf] + (f / (WROW / 16)) * WP + (f % (WROW / 16)) * 16) = wr[i];
+        }
 #pragma unroll
-        for (int i = 0; i < XLD; i++) reinterpret_cast<i32x4 *>(xsm[buf])[tid + i * WG] = xr[i];
+        for (int i = 0; i < XLD; i++) {
+            const int f = tid + i * WG;
+            *reinterpret_cast<i32x4 *>(xsm[buf] + (f / (XROW / 16)) * XP + (f % (XROW / 16)) * 16) = xr[i];
+        }
 #pragma unroll
         for (int i = 0; i < NDW; i++) {
             const int f = tid + i * WG;
@@ -374,7 +386,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
             i32x4 af[2], bf[NY];
 #pragma unroll
             for (int x = 0; x < 2; x++) {      // weight rows wu + 32x + j, k-half h
-                const uint8_t *src = ws[buf] + (size_t)(wu + 32 * x + j) * WROW + kb * WB;
+                const uint8_t *src = ws[buf] + (size_t)(wu + 32 * x + j) * WP + kb * WB;
                 if (DT == DT_Q8) {
                     af[x] = *reinterpret_cast<const i32x4 *>(src + 16 * h);
                 } else {                       // nibbles: low = weights 0..15, high = 16..31
@@ -385,7 +397,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
             }
 #pragma unroll
             for (int y = 0; y < NY; y++)
-                bf[y] = *reinterpret_cast<const i32x4 *>(xsm[buf] + (size_t)(wt + 32 * y + j) * XROW + kb * 32 + 16 * h);
+                bf[y] = *reinterpret_cast<const i32x4 *>(xsm[buf] + (size_t)(wt + 32 * y + j) * XP + kb * 32 + 16 * h);
             // FUSED: the block's scale products dw * dx of a 32 x 32 tile as
             // one fp16 matrix instruction, an outer product (weight scales in
             // element 0 of A's lanes 0..31, activation scales in element 0 of

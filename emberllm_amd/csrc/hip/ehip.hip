@@ -1242,6 +1242,13 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
                 // short prompts: the QK-norm, RoPE and cache stores in the
                 // product's epilogue (the raw product goes straight to a capture)
                 rc |= launch_gemm_qkv(s->st, s->f16kv, g, p, snap ? s->pdbg[DBG_QKV] : nullptr);
+            } else if (!q.xf && env_int("EHIP_PF_QKPOST", 1) && gemm_qkpost_fits(g, p)) {
+                // longer ones, 128-dim heads: the same in the matrix-core
+                // product's epilogue (EHIP_PF_QKPOST=0 keeps the product and
+                // k_qkpost apart)
+                GemmArgs gq = g;
+                gq.out = snap ? s->pdbg[DBG_QKV] : nullptr;
+                rc |= launch_gemm_qkpost(s->st, s->f16kv, gq, p);
             } else {
                 rc |= launch_gemm(s->st, EPI_STORE, g);
                 if (psnap(DBG_QKV, s->QKV, stride, stride)) return -1;

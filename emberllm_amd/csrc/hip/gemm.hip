@@ -260,7 +260,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
 template <int DT, int EPI, int TT, int KB, bool FUSED, int SP>
-__global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
+__global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p) {
     constexpr int GM_KB = KB;
     constexpr int GM_T = TT, NY = TT / 64;            // tokens per tile, MFMA tiles per wave along tokens
     constexpr int WB = DT == DT_Q8 ? 32 : 16;          // weight bytes per row and block
@@ -298,6 +298,14 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
     auto wrow_of = [&](int r) __attribute__((always_inline)) {
         if constexpr (EPI == EPI_SWIGLU) return min(c0 + (r >> 1), a.units - 1) + ((r & 1) ? a.pair_off : 0);
         else return min(u0 + r, a.units - 1);
+    };
+    // the tile rows of fragment x: wu + 32 x .. + 31, or with EPI_QKPOST (the
+    // tile one 128-dim head vector) 32 (wave & 1) + 64 x .., so that a lane
+    // holds each dimension d < 64 of its rows in fragment 0 and its rotary
+    // partner d + 64 at the same accumulator of fragment 1
+    auto arow = [&](int x) __attribute__((always_inline)) {
+        if constexpr (EPI == EPI_QKPOST) return (wave & 1) * 32 + 64 * x;
+        else return wu + 32 * x;
     };
 
     // global -> registers for one stage: weights (WROW bytes per row), codes, scales
@@ -386,7 +394,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
             i32x4 af[2], bf[NY];
 #pragma unroll
             for (int x = 0; x < 2; x++) {      // weight rows wu + 32x + j, k-half h
-                const uint8_t *src = ws[buf] + (size_t)(wu + 32 * x + j) * WP + kb * WB;
+                const uint8_t *src = ws[buf] + (size_t)(arow(x) + j) * WP + kb * WB;
                 if (DT == DT_Q8) {
                     af[x] = *reinterpret_cast<const i32x4 *>(src + 16 * h);
                 } else {                       // nibbles: low = weights 0..15, high = 16..31
@@ -410,7 +418,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
                 for (int x = 0; x < 2; x++) {
                     sa[x] = f16x4{};
-                    sa[x][0] = __builtin_bit_cast(_Float16, (uint16_t)(h ? 0 : dwh[buf][kb][wu + 32 * x + j]));
+                    sa[x][0] = __builtin_bit_cast(_Float16, (uint16_t)(h ? 0 : dwh[buf][kb][arow(x) + j]));
                 }
 #pragma unroll
                 for (int y = 0; y < NY; y++) {
@@ -443,7 +451,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
                             const int isum = DT == DT_Q4 ? d[r] - 8 * xsum : d[r];
-                            const float dw = dws[buf][kb][wu + 32 * x + mrow(r, h)];
+                            const float dw = dws[buf][kb][arow(x) + mrow(r, h)];
                             acc[x][y][r] += ((float)isum * dw) * dx;
                         }
                     }
@@ -474,6 +482,120 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a) {
             for (int y = 0; y < NY; y++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[x][y][r] += xch[((x * NY + y) * 16 + r) * WG + tid];
+    }
+    if constexpr (EPI == EPI_QKPOST) {
+        // k_qkpost's work on the tile, one 128-dim head vector x TT tokens
+        // (attention.hip; model.c:323-333): the bias (EPI_STORE's order), the
+        // head's RMSNorm for q and k heads (model.c:50-55) in k_qkpost's
+        // order (the squares of dims l and l + 64 added, then wave_sum over
+        // l = 0..63; the pair sums meet in LDS by token), neox RoPE from the
+        // host table (model.c:66-80), then q back into its q|k|v row and k
+        // and v into the cache.  a.out, when set, receives the raw product.
+        // Rounds of 64 tokens (y; two rounds of 32, one per wave pair, where
+        // the pair sums of 64 tokens do not fit the stages): pair sums, one
+        // wave_sum per token, apply.
+        constexpr int PSS = 65;   // pair sums per token, padded
+        constexpr int H2 = (64 * PSS + 64) * 4 <= (int)sizeof(wsp) ? 1 : 2, NTR = 64 / H2;
+        static_assert(GM_U == 128 && SP == 1 && TT == 64 && (NTR * PSS + NTR + 128) * 4 <= (int)sizeof(wsp),
+                      "one head vector x 64 tokens; sums fit the stages");
+        float *pss = reinterpret_cast<float *>(&wsp[0][0][0]), *scl = pss + NTR * PSS, *nws = scl + NTR;
+        const int vh = blockIdx.x, lw = wave & 1;   // lane dims 32 lw + mrow(r, h), and + 64
+        const bool isq = vh < p.n_heads, isk = !isq && vh < p.n_heads + p.n_kv;
+        const int g = isq ? 0 : vh - p.n_heads - (isk ? 0 : p.n_kv);
+        const bool norm = p.q_norm && (isq || isk), rot = isq || isk;
+        const float *nwp = isq ? p.q_norm : p.k_norm;
+        // the head's norm weights, read from LDS after the first barrier
+        if (norm && tid < 128) nws[tid] = nwp[tid];
+#pragma unroll
+        for (int y = 0; y < NY; y++)
+#pragma unroll
+        for (int hh = 0; hh < H2; hh++) {
+            const bool live = H2 == 1 || (wave >> 1) == hh;   // this round's token columns
+            const int lt = (H2 == 1 ? (wave >> 1) * 32 : 0) + j;        // the round's token
+            const int t = t0 + wt + 32 * y + j, tc = min(t, a.n - 1);
+            if (live) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int d = 32 * lw + mrow(r, h);
+                    if (a.bias) {
+                        acc[0][y][r] = acc[0][y][r] + a.bias[u0 + d];
+                        acc[1][y][r] = acc[1][y][r] + a.bias[u0 + d + 64];
+                    }
+                    if (a.out && t < a.n) {
+                        a.out[(size_t)t * a.out_stride + u0 + d] = acc[0][y][r];
+                        a.out[(size_t)t * a.out_stride + u0 + d + 64] = acc[1][y][r];
+                    }
+                    if (norm) pss[lt * PSS + d] = acc[0][y][r] * acc[0][y][r] + acc[1][y][r] * acc[1][y][r];
+                }
+            }
+            if (norm) {
+                __syncthreads();
+#pragma unroll 1
+                for (int k = 0; k < NTR / 4; k++) {   // wave w: the round's tokens NTR / 4 * w ..
+                    const int tk = NTR / 4 * wave + k;
+                    const float ss = wave_sum(pss[tk * PSS + lane]);
+                    if (lane == 0) scl[tk] = 1.0f / sqrtf(ss / 128.0f + p.eps);
+                }
+                __syncthreads();
+            }
+            if (live && t < a.n) {
+                const float sc = norm ? scl[lt] : 1.0f;
+                const int pos = p.pos_base + tc;
+                const size_t kvo = (size_t)pos * p.kv_dim + (size_t)g * 128;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {   // accumulators 4 q4 .. + 3: dims d0 .. d0 + 3
+                    const int d0 = 32 * lw + 4 * h + 8 * q4;
+                    f32x4 y0, y1;
+                    if (rot) {
+                        const f32x4 ca = *reinterpret_cast<const f32x4 *>(p.rope + (size_t)pos * 64 + d0);
+                        const f32x4 cb = *reinterpret_cast<const f32x4 *>(p.rope + (size_t)pos * 64 + d0 + 2);
+                        f32x4 n0 = f32x4{1.0f, 1.0f, 1.0f, 1.0f}, n1 = n0;
+                        if (norm) {
+                            n0 = *reinterpret_cast<const f32x4 *>(nws + d0);
+                            n1 = *reinterpret_cast<const f32x4 *>(nws + d0 + 64);
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            float x0 = acc[0][y][4 * q4 + e], x1 = acc[1][y][4 * q4 + e];
+                            if (norm) {
+                                x0 = x0 * sc * n0[e];
+                                x1 = x1 * sc * n1[e];
+                            }
+                            const float c = e < 2 ? ca[2 * e] : cb[2 * e - 4];
+                            const float sn = e < 2 ? ca[2 * e + 1] : cb[2 * e - 3];
+                            y0[e] = x0 * c - x1 * sn;
+                            y1[e] = x0 * sn + x1 * c;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            y0[e] = acc[0][y][4 * q4 + e];
+                            y1[e] = acc[1][y][4 * q4 + e];
+                        }
+                    }
+                    if (isq) {
+                        float *qo = p.qkv + (size_t)t * p.stride + u0 + d0;
+                        *reinterpret_cast<f32x4 *>(qo) = y0;
+                        *reinterpret_cast<f32x4 *>(qo + 64) = y1;
+                    } else {
+                        void *dst = isk ? p.kc : p.vc;
+                        if (p.kv_f16) {
+                            uint16_t *o = reinterpret_cast<uint16_t *>(dst) + kvo + d0;
+                            *reinterpret_cast<uint2 *>(o) = make_uint2(f2h(y0[0]) | ((uint32_t)f2h(y0[1]) << 16),
+                                                                       f2h(y0[2]) | ((uint32_t)f2h(y0[3]) << 16));
+                            *reinterpret_cast<uint2 *>(o + 64) = make_uint2(f2h(y1[0]) | ((uint32_t)f2h(y1[1]) << 16),
+                                                                            f2h(y1[2]) | ((uint32_t)f2h(y1[3]) << 16));
+                        } else {
+                            float *o = reinterpret_cast<float *>(dst) + kvo + d0;
+                            *reinterpret_cast<f32x4 *>(o) = y0;
+                            *reinterpret_cast<f32x4 *>(o + 64) = y1;
+                        }
+                    }
+                }
+            }
+            if (norm && (y + 1 < NY || hh + 1 < H2)) __syncthreads();   // the next round's sums reuse pss
+        }
+        return;
     }
     if constexpr (EPI == EPI_SWIGLU) {
         // h = silu(gate) * up for the wave's block of 32 hidden units (lane j
@@ -1304,8 +1426,8 @@ int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
         mfma_shape(gu, a.n, a.W.cols, &t64, &fused, &sp2);
         dim3 g(gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
 #define GMK(DT, TT, FU, SP)                                                                             \
-        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); \
-        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); \
+        if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_STORE, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a, QkPostArgs{}); \
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_RESID, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a, QkPostArgs{}); \
         else return -1;                                                                                 \
         return 0;
 #define GMF(DT, TT) if (fused) { GMK(DT, TT, true, 1) } else { GMK(DT, TT, false, 1) }
@@ -1355,7 +1477,7 @@ int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a) {
         bool t64, fused, sp2;
         mfma_shape(gu, a.n, a.W.cols, &t64, &fused, &sp2);
         const dim3 g((unsigned)gu, t64 ? (a.n + 63) / 64 : (a.n + 127) / 128);
-#define GMS(DT, TT, FU, SP) { hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_SWIGLU, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a); return 0; }
+#define GMS(DT, TT, FU, SP) { hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_SWIGLU, TT, 2, FU, SP>), g, dim3(WG * SP), 0, st, a, QkPostArgs{}); return 0; }
 #define GMSF(DT, TT) if (fused) GMS(DT, TT, true, 1) else GMS(DT, TT, false, 1)
         if (a.W.dtype == DT_Q8 && sp2) GMS(DT_Q8, 64, true, 2)
         if (a.W.dtype == DT_Q8) { if (t64) { GMSF(DT_Q8, 64) } else { GMSF(DT_Q8, 128) } }
@@ -1377,6 +1499,34 @@ int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a) {
     return 0;
 }
 
+
+bool gemm_qkpost_fits(const GemmArgs &g, const QkPostArgs &p) {
+    if ((g.W.dtype != DT_Q8 && g.W.dtype != DT_Q4) || g.n <= 0 || g.W.cols % QB != 0 || g.xf) return false;
+    if (p.hd != GM_U || p.rope_style != ROPE_NEOX || g.units != (p.n_heads + 2 * p.n_kv) * p.hd || p.n_tok != g.n)
+        return false;
+    // the shapes whose product launch_gemm gives k_gemm_mfma on 64-token
+    // tiles with one pipeline: the epilogue keeps those at 128 VGPRs (four
+    // waves per SIMD); the two-pipeline and 128-token tiles would lose a wave
+    // per SIMD to it
+    const long g64 = (long)(g.units / GM_U) * ((g.n + 63) / 64);
+    if (g64 < 256 || (g.units <= 1024 && g64 < 512 && g.W.cols < GEMM_SPLIT_MIN_K)) return false;
+    bool t64, fused, sp2;
+    mfma_shape(g.units / GM_U, g.n, g.W.cols, &t64, &fused, &sp2);
+    return t64 && !sp2;
+}
+
+int launch_gemm_qkpost(hipStream_t st, bool f16kv, const GemmArgs &a, const QkPostArgs &p0) {
+    if (!gemm_qkpost_fits(a, p0)) return -1;
+    QkPostArgs p = p0;
+    p.kv_f16 = f16kv ? 1 : 0;
+    const long gu = a.units / GM_U;
+    const bool fused = a.W.cols >= GEMM_SPLIT_MIN_K;   // (mfma_shape)
+    const dim3 g((unsigned)gu, (a.n + 63) / 64);
+#define GMQ(DT, FU) { hipLaunchKernelGGL((k_gemm_mfma<DT, EPI_QKPOST, 64, 2, FU, 1>), g, dim3(WG), 0, st, a, p); return 0; }
+    if (a.W.dtype == DT_Q8) { if (fused) GMQ(DT_Q8, true) else GMQ(DT_Q8, false) }
+    if (fused) GMQ(DT_Q4, true) else GMQ(DT_Q4, false)
+#undef GMQ
+}
 
 bool gemm_qkv_fits(const GemmArgs &g, const QkPostArgs &p) {
     if ((g.W.dtype != DT_Q8 && g.W.dtype != DT_Q4) || g.n <= 0 || g.W.cols % QB != 0) return false;

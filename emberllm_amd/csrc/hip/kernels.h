@@ -18,7 +18,7 @@ namespace ehip {
 //             EPI_RESID   out[r] += W[r].x'
 //             EPI_SWIGLU  out[u] = silu(W[u].x') * W[u+pair_off].x'
 enum { PRO_NORM = 0, PRO_PLAIN = 1, PRO_EMBED_NORM = 2, PRO_NORM_PARTS = 3 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKPOST = 3 };
 
 struct MatvecArgs {
     DMat W;
@@ -217,6 +217,7 @@ struct QkPostArgs {
     float eps; int rope_style;
     void *kc, *vc;
     int kv_dim, hd, n_heads, n_kv, pos_base, n_tok;
+    int kv_f16;                    // (launch_gemm_qkpost) the cache rows are fp16
 };
 int launch_qkpost(hipStream_t st, bool f16kv, const QkPostArgs &a);
 
@@ -266,6 +267,12 @@ int launch_gemm_swiglu(hipStream_t st, const GemmArgs &a);
 // receives the product with its bias ([n][p.stride]).  Returns -1 where
 // gemm_qkv_fits() is false.
 bool gemm_qkv_fits(const GemmArgs &g, const QkPostArgs &p);
+// The q|k|v product of a longer prompt (k_gemm_mfma's shapes) with
+// launch_qkpost's work in the epilogue, for 128-dim heads with neox RoPE;
+// a.out, when set, also receives the raw product.  Returns -1 where
+// gemm_qkpost_fits() is false.
+bool gemm_qkpost_fits(const GemmArgs &g, const QkPostArgs &p);
+int launch_gemm_qkpost(hipStream_t st, bool f16kv, const GemmArgs &a, const QkPostArgs &p);
 int launch_gemm_qkv(hipStream_t st, bool f16kv, const GemmArgs &g, const QkPostArgs &p, float *raw);
 
 // ---------------------------------------------------------------- sample --

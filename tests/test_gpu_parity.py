@@ -160,6 +160,35 @@ def test_prefill_fused_swiglu_equals_separate(name, n, monkeypatch):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("name,n,kv16", [("qwen3_06b", 1100, False), ("qwen3_06b", 2000, True),
+                                         ("qwen3_06b_q4", 2000, False)])
+def test_prefill_fused_qkpost_equals_separate(name, n, kv16, monkeypatch):
+    """Passes whose q|k|v product runs on 64-token matrix-core tiles with one
+    pipeline take k_qkpost's work into its epilogue (k_gemm_mfma's EPI_QKPOST
+    form: bias, the heads' RMSNorm in k_qkpost's summation order, neox RoPE,
+    q into its row, k and v into the cache).  Logits, the last layer's K and
+    V rows and the captured raw product equal those of the separate kernels
+    (EHIP_PF_QKPOST=0) bit for bit: Q8_0 and Q4_0 weights (the latter's
+    smaller stages take the pair sums in two rounds), fp32 and fp16 caches,
+    a partial last token tile (2000 = 31 x 64 + 16)."""
+    path = configs.model_path(name, threads=16)
+    V, L = configs.ALL[name]["vocab_size"], configs.ALL[name]["n_layers"]
+    ids = np.random.default_rng(n).integers(0, V, n)
+    say(f"{name} pp{n} kv16={kv16}: fused QK post-processing vs k_qkpost")
+    out = []
+    for fused in ("0", "1"):
+        monkeypatch.setenv("EHIP_PF_QKPOST", fused)
+        eng = emberllm.Engine(path, ctx=n + 8, kv_fp16=kv16)
+        eng.debug_capture_prefill(L - 1)
+        lg = eng.prefill(ids)
+        raw, p0 = eng.debug_read_prefill(1)
+        assert p0 == 0 and raw.shape[0] == n
+        out.append((lg, eng.kv_read(0, L - 1, n), eng.kv_read(1, L - 1, n), raw))
+        eng.close()
+    for a, b in zip(out[0], out[1]):
+        np.testing.assert_array_equal(a, b)
+
+
 @pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])
 def test_graph_equals_eager(name):
     """The captured graph replays exactly the eager launch sequence."""

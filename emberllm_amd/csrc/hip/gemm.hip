@@ -1504,15 +1504,13 @@ bool gemm_qkpost_fits(const GemmArgs &g, const QkPostArgs &p) {
     if ((g.W.dtype != DT_Q8 && g.W.dtype != DT_Q4) || g.n <= 0 || g.W.cols % QB != 0 || g.xf) return false;
     if (p.hd != GM_U || p.rope_style != ROPE_NEOX || g.units != (p.n_heads + 2 * p.n_kv) * p.hd || p.n_tok != g.n)
         return false;
-    // the shapes whose product launch_gemm gives k_gemm_mfma on 64-token
-    // tiles with one pipeline: the epilogue keeps those at 128 VGPRs (four
-    // waves per SIMD); the two-pipeline and 128-token tiles would lose a wave
-    // per SIMD to it
+    // the shapes whose product launch_gemm gives k_gemm_mfma; they run on
+    // 64-token tiles with one pipeline, where the epilogue keeps the kernel
+    // at 128 VGPRs (four waves per SIMD; the two-pipeline and 128-token tiles
+    // would lose a wave per SIMD to it).  Against those tiles with k_qkpost
+    // (Qwen3-0.6B shape): pp1024 5.05 -> 4.80 ms, pp3072 12.36 -> 11.52.
     const long g64 = (long)(g.units / GM_U) * ((g.n + 63) / 64);
-    if (g64 < 256 || (g.units <= 1024 && g64 < 512 && g.W.cols < GEMM_SPLIT_MIN_K)) return false;
-    bool t64, fused, sp2;
-    mfma_shape(g.units / GM_U, g.n, g.W.cols, &t64, &fused, &sp2);
-    return t64 && !sp2;
+    return !(g64 < 256 || (g.units <= 1024 && g64 < 512 && g.W.cols < GEMM_SPLIT_MIN_K));
 }
 
 int launch_gemm_qkpost(hipStream_t st, bool f16kv, const GemmArgs &a, const QkPostArgs &p0) {

@@ -17,7 +17,7 @@ import pytest
 import oracle
 from cases import CASES, GPU_CASES
 from emberllm_amd import configs, emberllm
-from parity import FLIP_MAX_ABS, FLIP_REL_L2, check_run, compare, near_tie
+from parity import FLIP_MAX_ABS, FLIP_REL_L2, bars, check_run, compare, near_tie
 
 pytestmark = pytest.mark.gpu
 
@@ -160,17 +160,20 @@ def test_prefill_fused_swiglu_equals_separate(name, n, monkeypatch):
         np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("name,n,kv16", [("qwen3_06b", 1100, False), ("qwen3_06b", 2000, True),
-                                         ("qwen3_06b_q4", 2000, False)])
+@pytest.mark.parametrize("name,n,kv16", [("qwen3_06b", 600, False), ("qwen3_06b", 2000, True),
+                                         ("qwen3_06b_q4", 2000, False), ("qwen3_06b", 3072, False)])
 def test_prefill_fused_qkpost_equals_separate(name, n, kv16, monkeypatch):
-    """Passes whose q|k|v product runs on 64-token matrix-core tiles with one
-    pipeline take k_qkpost's work into its epilogue (k_gemm_mfma's EPI_QKPOST
-    form: bias, the heads' RMSNorm in k_qkpost's summation order, neox RoPE,
-    q into its row, k and v into the cache).  Logits, the last layer's K and
-    V rows and the captured raw product equal those of the separate kernels
-    (EHIP_PF_QKPOST=0) bit for bit: Q8_0 and Q4_0 weights (the latter's
-    smaller stages take the pair sums in two rounds), fp32 and fp16 caches,
-    a partial last token tile (2000 = 31 x 64 + 16)."""
+    """Passes long enough for the matrix-core q|k|v product take k_qkpost's
+    work into its epilogue (k_gemm_mfma's EPI_QKPOST form on 64-token tiles
+    with one pipeline: bias, the heads' RMSNorm in k_qkpost's summation
+    order, neox RoPE, q into its row, k and v into the cache).  Logits, the
+    last layer's K and V rows and the captured raw product equal those of the
+    separate kernels on the same tiles (EHIP_PF_QKPOST=0 where the product's
+    shape keeps one pipeline and 64-token tiles: 2000 tokens) bit for bit,
+    and elsewhere (600 tokens: two pipelines, 3072: 128-token tiles) up to
+    the order of the products' block sums; Q8_0 and Q4_0 weights (the
+    latter's smaller stages take the pair sums in two rounds), fp32 and fp16
+    caches, a partial last token tile (2000 = 31 x 64 + 16)."""
     path = configs.model_path(name, threads=16)
     V, L = configs.ALL[name]["vocab_size"], configs.ALL[name]["n_layers"]
     ids = np.random.default_rng(n).integers(0, V, n)
@@ -186,7 +189,17 @@ def test_prefill_fused_qkpost_equals_separate(name, n, kv16, monkeypatch):
         out.append((lg, eng.kv_read(0, L - 1, n), eng.kv_read(1, L - 1, n), raw))
         eng.close()
     for a, b in zip(out[0], out[1]):
-        np.testing.assert_array_equal(a, b)
+        if n == 2000:
+            np.testing.assert_array_equal(a, b)
+            continue
+        # two block-sum orders of the products: within the bar this model's
+        # logits meet against the oracle (set by the reference builds' own
+        # spread at this shape: about 4e-2 max-abs, 1.4e-2 relative L2)
+        b_ = bars("qwen3_06b-p16-d32-s11")
+        if a.dtype == np.uint8:   # cache rows
+            a, b = (x.view(np.float16 if kv16 else np.float32).astype(np.float32) for x in (a, b))
+        r = compare(np.ravel(a), np.ravel(b))
+        assert r["max_abs"] <= b_["abs_max"] and r["rel_l2"] <= b_["rel_max"], (r, b_)
 
 
 @pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])

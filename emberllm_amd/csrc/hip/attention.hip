@@ -28,6 +28,7 @@
 // each as a separately rounded multiply and add like the reference's
 // -ffp-contract=off build.
 #include "kernels.h"
+#include "flimg.h"
 
 namespace ehip {
 
@@ -787,7 +788,6 @@ __global__ __launch_bounds__(64 * QKP_W) void k_qkpost(QkPostArgs a) {
 // Grid (kv heads, row tiles), kv heads varying fastest, so a kv head's
 // workgroups share an XCD and its L2 holds the head's K/V; row tiles in
 // reverse order, so the longest (latest tokens) start first.
-constexpr int FL_BR = 64, FL_BK = 64;
 
 __device__ __forceinline__ float fl_quarter_max(float v) {   // max over lanes i, i^16, i^32, i^48
     auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -986,9 +986,6 @@ __global__ __launch_bounds__(WG) void k_pf_flash(AttnArgs a) {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16-byte image piece (kept in registers)
 
-__device__ __forceinline__ int fl_krow(int k) {
-    return (k & ~31) | ((k & 4) << 2) | ((k & 24) >> 1) | (k & 3);
-}
 // maximum over lanes i, i ^ 8, i ^ 16, ... (the lanes of one key pair)
 __device__ __forceinline__ float fl_pair_max(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false)));   // row_ror:8
@@ -997,31 +994,7 @@ __device__ __forceinline__ float fl_pair_max(float v) {
     r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-// power-of-two exponent that brings a group maximum m into [2^14, 2^15)
-__device__ __forceinline__ int fl_exp(float m) { return 15 - __builtin_amdgcn_frexp_expf(m); }
-__device__ __forceinline__ uint32_t fl_pack(_Float16 a, _Float16 b) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
 
-// geometry of one (kv head, tile) image, in bytes; the LDS copy is the same
-// bytes at the same offsets (K and exponents in one array, V in another)
-template <int HD, bool F16> struct FlImg {
-    static constexpr int NP = F16 ? 1 : 2;                 // planes: hi, and lo for an fp32 cache
-    static constexpr int KRB = 2 * HD;                     // K plane row bytes
-    static constexpr int KRP = HD / 8;                     // 16-byte pieces per K row
-    static constexpr int KBYTES = NP * FL_BK * KRB;        // K planes
-    static constexpr int EBYTES = F16 ? 0 : 2 * FL_BK * 4; // int kex[64], vex[64] (fp32 cache)
-    static constexpr int KE = KBYTES + EBYTES;             // first staging part
-    static constexpr int VBYTES = NP * HD * FL_BK * 2;     // V^T planes, 128-byte rows
-    static constexpr int HBYTES = KE + VBYTES;             // bytes per image
-    static constexpr int SLAB = 1024;                      // one wave's direct-to-LDS load
-    static constexpr int KE_SLABS = (KE + SLAB - 1) / SLAB, V_SLABS = VBYTES / SLAB;
-    static_assert(KE % 16 == 0 && VBYTES % SLAB == 0 && (KRP & (KRP - 1)) == 0, "image geometry");
-    // K row r (plane-major: plane * 64 + row), piece p
-    static __device__ __forceinline__ int k_at(int r, int p) { return r * KRB + 16 * (p ^ (r & (KRP - 1))); }
-    // V^T row d (plane-major: plane * HD + dim), piece p (keys 8p .. 8p + 7)
-    static __device__ __forceinline__ int v_at(int d, int p) { return d * 128 + 16 * (p ^ (d & 7)); }
-};
 
 size_t attn_kvimg_bytes(int hd, bool f16kv, int ctx, int n_kv) {
     const size_t tiles = (size_t)(ctx + FL_BK - 1) / FL_BK * (size_t)n_kv;
@@ -1435,10 +1408,14 @@ int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *q
     if (a.hd == 64 || a.hd == 128) {
         const int nkt = (a.pos_base + a.n_tok + FL_BK - 1) / FL_BK;
         if (!a.kvimg || a.kvimg_tiles < nkt) return -1;
+        if (a.kvimg_fused && (a.hd != 128 || a.pos_base % FL_BK != 0)) return -1;
+        // tiles to convert here: all, or those before the pass (the q|k|v
+        // product wrote the pass's own)
+        const int nks = a.kvimg_fused ? a.pos_base / FL_BK : nkt;
         if (quantized) *quantized = a.qx != nullptr;
-        const dim3 sgrid(a.n_kv, nkt);
+        const dim3 sgrid(a.n_kv, nks);
 #define FL16(H, F)                                                                         \
-    hipLaunchKernelGGL((k_pf_kvsplit<H, F>), sgrid, dim3(WG), 0, st, a);                  \
+    if (nks > 0) hipLaunchKernelGGL((k_pf_kvsplit<H, F>), sgrid, dim3(WG), 0, st, a);     \
     hipLaunchKernelGGL((k_pf_flash16<H, F>), grid, dim3(WG), 0, st, a);
         if (a.hd == 64) {
             if (f16kv) { FL16(64, true) } else { FL16(64, false) }

@@ -1238,6 +1238,11 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             AttnArgs at = attn_args(s, l);
             p.kc = at.kc; p.vc = at.vc; p.kv_dim = kvd; p.hd = hd; p.n_heads = c.n_heads;
             p.n_kv = c.n_kv_heads; p.pos_base = pos0; p.n_tok = mt;
+            bool exact = s->pf_mode == PF_EXACT;
+            if (s->pf_mode == PF_AUTO)
+                exact = s->pf_seq ? pos0 + mt <= PF_EXACT_KEYS
+                                  : pos0 + mt <= PF_FUSE_KEYS && (long)c.n_kv_heads * ((mt + 3) / 4) >= PF_FUSE_MIN_WG;
+            bool img_fused = false;   // the q|k|v product wrote the pass's K/V tile images
             if (!q.xf && gemm_qkv_fits(g, p)) {
                 // short prompts: the QK-norm, RoPE and cache stores in the
                 // product's epilogue (the raw product goes straight to a capture)
@@ -1248,6 +1253,14 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
                 // k_qkpost apart)
                 GemmArgs gq = g;
                 gq.out = snap ? s->pdbg[DBG_QKV] : nullptr;
+                // and, for the matrix-core attention, the pass's own K/V tile
+                // images (EHIP_PF_KVIMG=0 leaves them to k_pf_kvsplit)
+                if (!exact && hd == 128 && s->pf_kvimg && pos0 % 64 == 0 &&
+                    s->pf_kvimg_tiles >= (pos0 + mt + 63) / 64 && env_int("EHIP_PF_KVIMG", 1)) {
+                    p.kvimg = s->pf_kvimg;
+                    p.kvimg_tiles = s->pf_kvimg_tiles;
+                    img_fused = true;
+                }
                 rc |= launch_gemm_qkpost(s->st, s->f16kv, gq, p);
             } else {
                 rc |= launch_gemm(s->st, EPI_STORE, g);
@@ -1259,10 +1272,7 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             at.scores = s->pf_scores; at.tmax = s->pf_tmax; at.rowmax = s->pf_rowmax; at.rowinv = s->pf_rowinv;
             at.kvimg = s->pf_kvimg; at.kvimg_tiles = s->pf_kvimg_tiles;
             at.ldk = attn_prefill_ldk(pos0, mt);
-            bool exact = s->pf_mode == PF_EXACT;
-            if (s->pf_mode == PF_AUTO)
-                exact = s->pf_seq ? pos0 + mt <= PF_EXACT_KEYS
-                                  : pos0 + mt <= PF_FUSE_KEYS && (long)c.n_kv_heads * ((mt + 3) / 4) >= PF_FUSE_MIN_WG;
+            at.kvimg_fused = img_fused ? 1 : 0;
             // the attention can quantize its own output for wo (not for F32
             // weights, whose product reads the fp32 rows)
             bool quantized = false;

@@ -24,6 +24,7 @@
 // k_gemm (F32 weights): a 64 x 64 tile per workgroup, 4 x 4 micro-tiles per
 // thread, dot_f32 order.
 #include "kernels.h"
+#include "flimg.h"
 
 namespace ehip {
 
@@ -258,6 +259,63 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
+
+// One k or v head's 64-key tile image for k_pf_flash16, with k_pf_kvsplit's
+// bytes (flimg.h): the lane (j, h) of wave pair half lw holds key kl's dims
+// 32 lw + mrow(r, h) in v0[r] and the dims 64 above them in v1[r], as stored
+// in the cache.  An fp32 cache's keys take the power-of-two scale of their
+// largest |value| over the 128 dims (the two waves' maxima meet in xmx) and
+// split into hi and lo fp16 planes; an fp16 cache's are copied.  Every wave
+// of the workgroup calls it (a barrier); `live` lanes hold this round's keys.
+template <bool F16>
+__device__ __forceinline__ void qk_image(uint8_t *im, bool isk, const float *v0, const float *v1, int kl, int lw,
+                                         int h, float *xmx, bool live) {
+    using I = FlImg<128, F16>;
+    int ex = 0;
+    if constexpr (!F16) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) mx = fmaxf(mx, fmaxf(fabsf(v0[r]), fabsf(v1[r])));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (live && h == 0) xmx[64 * lw + kl] = mx;
+        __syncthreads();
+        ex = fl_exp(fmaxf(xmx[kl], xmx[64 + kl]));
+        if (live && lw == 0 && h == 0) reinterpret_cast<int *>(im + I::KBYTES)[(isk ? 0 : FL_BK) + kl] = ex;
+    }
+    if (!live) return;
+    const int rk = fl_krow(kl);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float *v = u ? v1 : v0;
+            const int d = 32 * lw + 4 * h + 8 * q4 + 64 * u;   // dims d .. d + 3
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x = F16 ? v[4 * q4 + e] : __builtin_amdgcn_ldexpf(v[4 * q4 + e], ex);
+                hi[e] = (_Float16)x;
+                lo[e] = (_Float16)(x - (float)hi[e]);
+            }
+            if (isk) {   // K planes: 4 dims = half of a 16-byte piece of row rk
+                const int dq = d / 4;
+                *reinterpret_cast<uint2 *>(im + I::k_at(rk, dq >> 1) + 8 * (dq & 1)) =
+                    make_uint2(fl_pack(hi[0], hi[1]), fl_pack(hi[2], hi[3]));
+                if constexpr (!F16)
+                    *reinterpret_cast<uint2 *>(im + I::k_at(FL_BK + rk, dq >> 1) + 8 * (dq & 1)) =
+                        make_uint2(fl_pack(lo[0], lo[1]), fl_pack(lo[2], lo[3]));
+            } else {     // V^T planes: key kl of rows d .. d + 3
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    *reinterpret_cast<uint16_t *>(im + I::KE + I::v_at(d + e, kl >> 3) + 2 * (kl & 7)) =
+                        __builtin_bit_cast(uint16_t, hi[e]);
+                    if constexpr (!F16)
+                        *reinterpret_cast<uint16_t *>(im + I::KE + I::v_at(128 + d + e, kl >> 3) + 2 * (kl & 7)) =
+                            __builtin_bit_cast(uint16_t, lo[e]);
+                }
+            }
+        }
+}
 
 template <int DT, int EPI, int TT, int KB, bool FUSED, int SP>
 __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p) {
@@ -496,7 +554,7 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p)
         // wave_sum per token, apply.
         constexpr int PSS = 65;   // pair sums per token, padded
         constexpr int H2 = (64 * PSS + 64) * 4 <= (int)sizeof(wsp) ? 1 : 2, NTR = 64 / H2;
-        static_assert(GM_U == 128 && SP == 1 && TT == 64 && (NTR * PSS + NTR + 128) * 4 <= (int)sizeof(wsp),
+        static_assert(GM_U == 128 && SP == 1 && TT == 64 && (NTR * PSS + NTR + 128 + 128) * 4 <= (int)sizeof(wsp),
                       "one head vector x 64 tokens; sums fit the stages");
         float *pss = reinterpret_cast<float *>(&wsp[0][0][0]), *scl = pss + NTR * PSS, *nws = scl + NTR;
         const int vh = blockIdx.x, lw = wave & 1;   // lane dims 32 lw + mrow(r, h), and + 64
@@ -506,6 +564,14 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p)
         const float *nwp = isq ? p.q_norm : p.k_norm;
         // the head's norm weights, read from LDS after the first barrier
         if (norm && tid < 128) nws[tid] = nwp[tid];
+        // p.kvimg: the k and v heads also write their 64-key tile's image for
+        // k_pf_flash16 (pos_base a multiple of FL_BK: the tile is the pass's
+        // tokens t0 ..), with the keys' maxima meeting in LDS (xmx)
+        const bool img = p.kvimg && !isq;
+        float *xmx = nws + 128;
+        uint8_t *im = p.kvimg ? p.kvimg + ((size_t)g * p.kvimg_tiles + (p.pos_base + t0) / FL_BK) *
+                                              (p.kv_f16 ? FlImg<128, true>::HBYTES : FlImg<128, false>::HBYTES)
+                              : nullptr;
 #pragma unroll
         for (int y = 0; y < NY; y++)
 #pragma unroll
@@ -538,40 +604,46 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p)
                 }
                 __syncthreads();
             }
-            if (live && t < a.n) {
+            // every column (those past the pass's last token repeat it: the
+            // tile image wants them) in place: normed and rotated q and k,
+            // v as it is
+            const int pos = p.pos_base + tc;
+            if (live && rot) {
                 const float sc = norm ? scl[lt] : 1.0f;
-                const int pos = p.pos_base + tc;
-                const size_t kvo = (size_t)pos * p.kv_dim + (size_t)g * 128;
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {   // accumulators 4 q4 .. + 3: dims d0 .. d0 + 3
                     const int d0 = 32 * lw + 4 * h + 8 * q4;
-                    f32x4 y0, y1;
-                    if (rot) {
-                        const f32x4 ca = *reinterpret_cast<const f32x4 *>(p.rope + (size_t)pos * 64 + d0);
-                        const f32x4 cb = *reinterpret_cast<const f32x4 *>(p.rope + (size_t)pos * 64 + d0 + 2);
-                        f32x4 n0 = f32x4{1.0f, 1.0f, 1.0f, 1.0f}, n1 = n0;
+                    const f32x4 ca = *reinterpret_cast<const f32x4 *>(p.rope + (size_t)pos * 64 + d0);
+                    const f32x4 cb = *reinterpret_cast<const f32x4 *>(p.rope + (size_t)pos * 64 + d0 + 2);
+                    f32x4 n0 = f32x4{1.0f, 1.0f, 1.0f, 1.0f}, n1 = n0;
+                    if (norm) {
+                        n0 = *reinterpret_cast<const f32x4 *>(nws + d0);
+                        n1 = *reinterpret_cast<const f32x4 *>(nws + d0 + 64);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        float x0 = acc[0][y][4 * q4 + e], x1 = acc[1][y][4 * q4 + e];
                         if (norm) {
-                            n0 = *reinterpret_cast<const f32x4 *>(nws + d0);
-                            n1 = *reinterpret_cast<const f32x4 *>(nws + d0 + 64);
+                            x0 = x0 * sc * n0[e];
+                            x1 = x1 * sc * n1[e];
                         }
+                        const float c = e < 2 ? ca[2 * e] : cb[2 * e - 4];
+                        const float sn = e < 2 ? ca[2 * e + 1] : cb[2 * e - 3];
+                        acc[0][y][4 * q4 + e] = x0 * c - x1 * sn;
+                        acc[1][y][4 * q4 + e] = x0 * sn + x1 * c;
+                    }
+                }
+            }
+            if (live && t < a.n) {
+                const size_t kvo = (size_t)pos * p.kv_dim + (size_t)g * 128;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            float x0 = acc[0][y][4 * q4 + e], x1 = acc[1][y][4 * q4 + e];
-                            if (norm) {
-                                x0 = x0 * sc * n0[e];
-                                x1 = x1 * sc * n1[e];
-                            }
-                            const float c = e < 2 ? ca[2 * e] : cb[2 * e - 4];
-                            const float sn = e < 2 ? ca[2 * e + 1] : cb[2 * e - 3];
-                            y0[e] = x0 * c - x1 * sn;
-                            y1[e] = x0 * sn + x1 * c;
-                        }
-                    } else {
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const int d0 = 32 * lw + 4 * h + 8 * q4;
+                    f32x4 y0, y1;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            y0[e] = acc[0][y][4 * q4 + e];
-                            y1[e] = acc[1][y][4 * q4 + e];
-                        }
+                    for (int e = 0; e < 4; e++) {
+                        y0[e] = acc[0][y][4 * q4 + e];
+                        y1[e] = acc[1][y][4 * q4 + e];
                     }
                     if (isq) {
                         float *qo = p.qkv + (size_t)t * p.stride + u0 + d0;
@@ -594,6 +666,13 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p)
                 }
             }
             if (norm && (y + 1 < NY || hh + 1 < H2)) __syncthreads();   // the next round's sums reuse pss
+        }
+        if (img) {   // the pass's tile image of this k or v head (k_pf_kvsplit's bytes)
+            const int kl = (wave >> 1) * 32 + j;   // key within the tile
+            if (p.kv_f16)
+                qk_image<true>(im, isk, acc[0][0], acc[1][0], kl, lw, h, xmx, true);
+            else
+                qk_image<false>(im, isk, acc[0][0], acc[1][0], kl, lw, h, xmx, true);
         }
         return;
     }

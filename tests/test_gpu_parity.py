@@ -202,6 +202,37 @@ def test_prefill_fused_qkpost_equals_separate(name, n, kv16, monkeypatch):
         assert r["max_abs"] <= b_["abs_max"] and r["rel_l2"] <= b_["rel_max"], (r, b_)
 
 
+@pytest.mark.parametrize("name,n,kv16,start", [("qwen3_06b", 600, False, 0), ("qwen3_06b_q4", 700, False, 0),
+                                               ("qwen3_06b", 1100, True, 0), ("qwen3_06b", 600, False, 640),
+                                               ("qwen3_06b", 500, False, 600)])
+def test_prefill_fused_kv_images_equal_kvsplit(name, n, kv16, start, monkeypatch):
+    """The fused q|k|v product of a pass that starts on a 64-key tile also
+    writes the pass's own K/V tile images for the matrix-core attention
+    (k_pf_kvsplit then converts only the earlier tiles).  The images are
+    k_pf_kvsplit's bytes, so logits and the last layer's K/V rows equal those
+    of EHIP_PF_KVIMG=0 bit for bit: Q8_0 and Q4_0 weights, fp32 (hi/lo planes
+    and per-key exponents) and fp16 caches, a continuation pass at position
+    640 (tiles 0..9 converted, 10.. fused) and one at 600 (not on a tile
+    boundary: every tile converted)."""
+    path = configs.model_path(name, threads=16)
+    V, L = configs.ALL[name]["vocab_size"], configs.ALL[name]["n_layers"]
+    rng = np.random.default_rng(n + start)
+    pre = rng.integers(0, V, start)
+    ids = rng.integers(0, V, n)
+    say(f"{name} pp{n} at {start} kv16={kv16}: fused K/V tile images vs k_pf_kvsplit")
+    out = []
+    for fused in ("0", "1"):
+        monkeypatch.setenv("EHIP_PF_KVIMG", fused)
+        eng = emberllm.Engine(path, ctx=start + n + 8, kv_fp16=kv16)
+        if start:
+            eng.prefill(pre)
+        lg = eng.prefill(ids, start)
+        out.append((lg, eng.kv_read(0, L - 1, start + n), eng.kv_read(1, L - 1, start + n)))
+        eng.close()
+    for a, b in zip(out[0], out[1]):
+        np.testing.assert_array_equal(a, b)
+
+
 @pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])
 def test_graph_equals_eager(name):
     """The captured graph replays exactly the eager launch sequence."""

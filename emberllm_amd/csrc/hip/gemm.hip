@@ -266,10 +266,10 @@ __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 *
 // in the cache.  An fp32 cache's keys take the power-of-two scale of their
 // largest |value| over the 128 dims (the two waves' maxima meet in xmx) and
 // split into hi and lo fp16 planes; an fp16 cache's are copied.  Every wave
-// of the workgroup calls it (a barrier); `live` lanes hold this round's keys.
+// of the workgroup calls it (a barrier).
 template <bool F16>
 __device__ __forceinline__ void qk_image(uint8_t *im, bool isk, const float *v0, const float *v1, int kl, int lw,
-                                         int h, float *xmx, bool live) {
+                                         int h, float *xmx) {
     using I = FlImg<128, F16>;
     int ex = 0;
     if constexpr (!F16) {
@@ -277,12 +277,11 @@ __device__ __forceinline__ void qk_image(uint8_t *im, bool isk, const float *v0,
 #pragma unroll
         for (int r = 0; r < 16; r++) mx = fmaxf(mx, fmaxf(fabsf(v0[r]), fabsf(v1[r])));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (live && h == 0) xmx[64 * lw + kl] = mx;
+        if (h == 0) xmx[64 * lw + kl] = mx;
         __syncthreads();
         ex = fl_exp(fmaxf(xmx[kl], xmx[64 + kl]));
-        if (live && lw == 0 && h == 0) reinterpret_cast<int *>(im + I::KBYTES)[(isk ? 0 : FL_BK) + kl] = ex;
+        if (lw == 0 && h == 0) reinterpret_cast<int *>(im + I::KBYTES)[(isk ? 0 : FL_BK) + kl] = ex;
     }
-    if (!live) return;
     const int rk = fl_krow(kl);
 #pragma unroll
     for (int q4 = 0; q4 < 4; q4++)
@@ -670,9 +669,9 @@ __global__ __launch_bounds__(WG * SP) void k_gemm_mfma(GemmArgs a, QkPostArgs p)
         if (img) {   // the pass's tile image of this k or v head (k_pf_kvsplit's bytes)
             const int kl = (wave >> 1) * 32 + j;   // key within the tile
             if (p.kv_f16)
-                qk_image<true>(im, isk, acc[0][0], acc[1][0], kl, lw, h, xmx, true);
+                qk_image<true>(im, isk, acc[0][0], acc[1][0], kl, lw, h, xmx);
             else
-                qk_image<false>(im, isk, acc[0][0], acc[1][0], kl, lw, h, xmx, true);
+                qk_image<false>(im, isk, acc[0][0], acc[1][0], kl, lw, h, xmx);
         }
         return;
     }

@@ -1408,7 +1408,7 @@ int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *q
     if (a.hd == 64 || a.hd == 128) {
         const int nkt = (a.pos_base + a.n_tok + FL_BK - 1) / FL_BK;
         if (!a.kvimg || a.kvimg_tiles < nkt) return -1;
-        if (a.kvimg_fused && (a.hd != 128 || a.pos_base % FL_BK != 0)) return -1;
+        if (a.kvimg_fused && a.pos_base % FL_BK != 0) return -1;
         // tiles to convert here: all, or those before the pass (the q|k|v
         // product wrote the pass's own)
         const int nks = a.kvimg_fused ? a.pos_base / FL_BK : nkt;

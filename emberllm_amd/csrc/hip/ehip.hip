@@ -1243,9 +1243,19 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
                 exact = s->pf_seq ? pos0 + mt <= PF_EXACT_KEYS
                                   : pos0 + mt <= PF_FUSE_KEYS && (long)c.n_kv_heads * ((mt + 3) / 4) >= PF_FUSE_MIN_WG;
             bool img_fused = false;   // the q|k|v product wrote the pass's K/V tile images
+            // the matrix-core attention's K/V tile images of the pass, in the
+            // fused q|k|v epilogues (EHIP_PF_KVIMG=0 leaves them to
+            // k_pf_kvsplit)
+            const bool img_ok = !exact && (hd == 64 || hd == 128) && s->pf_kvimg && pos0 % 64 == 0 &&
+                                s->pf_kvimg_tiles >= (pos0 + mt + 63) / 64 && env_int("EHIP_PF_KVIMG", 1);
             if (!q.xf && gemm_qkv_fits(g, p)) {
                 // short prompts: the QK-norm, RoPE and cache stores in the
                 // product's epilogue (the raw product goes straight to a capture)
+                if (img_ok) {
+                    p.kvimg = s->pf_kvimg;
+                    p.kvimg_tiles = s->pf_kvimg_tiles;
+                    img_fused = true;
+                }
                 rc |= launch_gemm_qkv(s->st, s->f16kv, g, p, snap ? s->pdbg[DBG_QKV] : nullptr);
             } else if (!q.xf && env_int("EHIP_PF_QKPOST", 1) && gemm_qkpost_fits(g, p)) {
                 // longer ones, 128-dim heads: the same in the matrix-core
@@ -1253,10 +1263,7 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
                 // k_qkpost apart)
                 GemmArgs gq = g;
                 gq.out = snap ? s->pdbg[DBG_QKV] : nullptr;
-                // and, for the matrix-core attention, the pass's own K/V tile
-                // images (EHIP_PF_KVIMG=0 leaves them to k_pf_kvsplit)
-                if (!exact && hd == 128 && s->pf_kvimg && pos0 % 64 == 0 &&
-                    s->pf_kvimg_tiles >= (pos0 + mt + 63) / 64 && env_int("EHIP_PF_KVIMG", 1)) {
+                if (img_ok) {
                     p.kvimg = s->pf_kvimg;
                     p.kvimg_tiles = s->pf_kvimg_tiles;
                     img_fused = true;

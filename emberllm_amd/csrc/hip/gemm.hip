@@ -257,6 +257,7 @@ constexpr int GM_U = 128;
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int mrow(int r, int h) { return (r & 3) + 4 * h + 8 * (r >> 2); }
 
@@ -1199,6 +1200,46 @@ __global__ __launch_bounds__(256 * SPLIT, SPLIT == 2 ? 4 : 1) void k_gemm_swq(Ge
     }
 }
 
+// One key's K rows in its 64-key tile image for k_pf_flash16 (k_pf_kvsplit's
+// layout, flimg.h), for k_gemm_qkv's wave-per-token epilogue: lane l holds
+// dims l + 64 k of the key's cache values v[k]; ex is the key's power-of-two
+// scale (fp32 cache: from its largest |value|).
+template <int HD, bool F16>
+__device__ __forceinline__ void qkv_key_image(uint8_t *im, const float *v, int kl, int ex, int lane) {
+    using I = FlImg<HD, F16>;
+    const int rk = fl_krow(kl);
+#pragma unroll
+    for (int k = 0; k < HD / 64; k++) {
+        const int d = lane + 64 * k;
+        const float x = F16 ? v[k] : __builtin_amdgcn_ldexpf(v[k], ex);
+        const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+        *reinterpret_cast<uint16_t *>(im + I::k_at(rk, d >> 3) + 2 * (d & 7)) = __builtin_bit_cast(uint16_t, hi);
+        if constexpr (!F16)
+            *reinterpret_cast<uint16_t *>(im + I::k_at(FL_BK + rk, d >> 3) + 2 * (d & 7)) = __builtin_bit_cast(uint16_t, lo);
+    }
+    if (!F16 && lane == 0) reinterpret_cast<int *>(im + I::KBYTES)[kl] = ex;
+}
+// A k head's key at position pos and, when it is the pass's last, the rest
+// of its tile (k_pf_kvsplit repeats the last key there).
+template <int HD, bool F16>
+__device__ __forceinline__ void qkv_tile_image(const QkPostArgs &p, int g, const float *v, int pos, bool last,
+                                               int lane) {
+    using I = FlImg<HD, F16>;
+    uint8_t *im = p.kvimg + ((size_t)g * p.kvimg_tiles + pos / FL_BK) * I::HBYTES;
+    int ex = 0;
+    if constexpr (!F16) {
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < HD / 64; k++) m = fmaxf(m, fabsf(v[k]));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        ex = fl_exp(m);
+    }
+    qkv_key_image<HD, F16>(im, v, pos % FL_BK, ex, lane);
+    if (last)
+        for (int kp = pos % FL_BK + 1; kp < FL_BK; kp++) qkv_key_image<HD, F16>(im, v, kp, ex, lane);
+}
+
 // k_gemm_qkv: the q|k|v product of a short prompt with k_qkpost's work in
 // the epilogue (replacing that kernel and its launch).  A workgroup takes one
 // head vector (HD units: a q, k or v head) x QV_T = 16 tokens, wave w the
@@ -1207,7 +1248,9 @@ __global__ __launch_bounds__(256 * SPLIT, SPLIT == 2 ? 4 : 1) void k_gemm_swq(Ge
 // per token does what k_qkpost does for it, with the same lane layout (lane
 // l holds elements l, l + 64) and so the same sums: the RMSNorm of q and k
 // heads (model.c:386-389), RoPE from the host table (model.c:66-80), q back
-// into its q|k|v row, k and v into the cache (model.c:39-48).
+// into its q|k|v row, k and v into the cache (model.c:39-48); with
+// p.kvimg also the keys' bytes in the K/V tile images of the matrix-core
+// attention (qkv_tile_image).
 constexpr int QV_T = 16;
 __host__ __device__ constexpr int qv_ring(int split) { return split > 1 ? 4 : 8; }
 template <int DT, int SPLIT, bool FULL, int HD, bool F16>
@@ -1227,6 +1270,7 @@ __global__ __launch_bounds__(64 * (HD / 16) * SPLIT) void k_gemm_qkv(GemmArgs a,
     __shared__ int sxs[SPLIT][2][GS_KB][QV_T];
     __shared__ __align__(16) float red[SPLIT > 1 ? SPLIT - 1 : 1][NWP][64][4];
     __shared__ float hs[QV_T][HD + 1];
+    __shared__ int exs[QV_T];   // (p.kvimg, fp32 cache) the v head's per-key scales
     const int tid = threadIdx.x % NTP, q = threadIdx.x / NTP;
     const int lane = tid & 63, wave = tid >> 6, fr = lane & 15, fg = lane >> 4;
     const int vh = blockIdx.x, u0 = vh * HD, t0 = blockIdx.y * QV_T, wu = wave * 16;
@@ -1366,9 +1410,13 @@ __global__ __launch_bounds__(64 * (HD / 16) * SPLIT) void k_gemm_qkv(GemmArgs a,
         }
     }
     __syncthreads();
-    if (q > 0) return;
+    // a v head writing the tile image keeps every wave for the transposed
+    // V rows at the end (a barrier)
+    const bool vimg = p.kvimg && !isq && !isk;
+    if (q > 0 && !vimg) return;
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
+        if (q > 0) break;
         const int tt = wave * TPW + j, t = t0 + tt;              // uniform over the wave
         if (t >= a.n) break;
         const int pos = p.pos_base + t;
@@ -1381,6 +1429,14 @@ __global__ __launch_bounds__(64 * (HD / 16) * SPLIT) void k_gemm_qkv(GemmArgs a,
             for (int k = 0; k < ND; k++) {
                 if (F16) reinterpret_cast<uint16_t *>(p.vc)[off + lane + 64 * k] = f2h(x[k]);
                 else reinterpret_cast<float *>(p.vc)[off + lane + 64 * k] = x[k];
+            }
+            if (vimg && !F16) {   // the key's scale from its largest |value|
+                float m = 0.0f;
+#pragma unroll
+                for (int k = 0; k < ND; k++) m = fmaxf(m, fabsf(x[k]));
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+                if (lane == 0) exs[tt] = fl_exp(m);
             }
             continue;
         }
@@ -1414,6 +1470,43 @@ __global__ __launch_bounds__(64 * (HD / 16) * SPLIT) void k_gemm_qkv(GemmArgs a,
             for (int k = 0; k < ND; k++) {
                 if (F16) reinterpret_cast<uint16_t *>(p.kc)[off + lane + 64 * k] = f2h(y[k]);
                 else reinterpret_cast<float *>(p.kc)[off + lane + 64 * k] = y[k];
+            }
+            if (p.kvimg) qkv_tile_image<HD, F16>(p, g, y, pos, t == a.n - 1, lane);
+        }
+    }
+    if (vimg) {
+        // V^T rows of the image (k_pf_kvsplit's bytes): 16-byte pieces of 8
+        // keys for every dim, the workgroup's 16 keys and, in the workgroup
+        // of the pass's last token, the rest of its tile (the last key
+        // repeated), from the tile in LDS
+        using I = FlImg<HD, F16>;
+        __syncthreads();   // every key's scale in exs
+        const int n_t = min(QV_T, a.n - t0), kl0 = (p.pos_base + t0) % FL_BK;
+        const int pc0 = kl0 / 8, pc1 = t0 + QV_T >= a.n ? FL_BK / 8 : (kl0 + QV_T) / 8;
+        uint8_t *im = p.kvimg + ((size_t)g * p.kvimg_tiles + (p.pos_base + t0) / FL_BK) * I::HBYTES;
+        for (int w = threadIdx.x; w < HD * (pc1 - pc0); w += NTP * SPLIT) {
+            const int d = w % HD, pc = pc0 + w / HD;
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                _Float16 hi[2], lo[2];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int tt = min(8 * pc + e + u - kl0, n_t - 1);
+                    const float x = F16 ? hs[tt][d] : __builtin_amdgcn_ldexpf(hs[tt][d], exs[tt]);
+                    hi[u] = (_Float16)x;
+                    lo[u] = (_Float16)(x - (float)hi[u]);
+                }
+                hw[e / 2] = fl_pack(hi[0], hi[1]);
+                lw[e / 2] = fl_pack(lo[0], lo[1]);
+            }
+            *reinterpret_cast<u32x4 *>(im + I::KE + I::v_at(d, pc)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            if constexpr (!F16) {
+                *reinterpret_cast<u32x4 *>(im + I::KE + I::v_at(HD + d, pc)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                if (d == 0)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        reinterpret_cast<int *>(im + I::KBYTES)[FL_BK + 8 * pc + e] = exs[min(8 * pc + e - kl0, n_t - 1)];
             }
         }
     }

@@ -120,8 +120,8 @@ struct AttnArgs {
             // kvimg_tiles tiles per head (attn_kvimg_bytes)
             uint8_t *kvimg; int kvimg_tiles;
             // nonzero: the tiles from pos_base / 64 on were written by the
-            // q|k|v product (launch_gemm_qkpost); only the earlier ones are
-            // converted here (pos_base a multiple of 64)
+            // q|k|v product (launch_gemm_qkpost or launch_gemm_qkv); only the
+            // earlier ones are converted here (pos_base a multiple of 64)
             int kvimg_fused;
         };
         struct {
@@ -222,9 +222,9 @@ struct QkPostArgs {
     void *kc, *vc;
     int kv_dim, hd, n_heads, n_kv, pos_base, n_tok;
     int kv_f16;                    // (launch_gemm_qkpost) the cache rows are fp16
-    // (launch_gemm_qkpost, optional) the K/V tile images of the matrix-core
-    // prefill attention (AttnArgs::kvimg): the pass's own tiles are written
-    // too; pos_base a multiple of 64
+    // (launch_gemm_qkpost, launch_gemm_qkv; optional) the K/V tile images of
+    // the matrix-core prefill attention (AttnArgs::kvimg): the pass's own
+    // tiles are written too; pos_base a multiple of 64
     uint8_t *kvimg; int kvimg_tiles;
 };
 int launch_qkpost(hipStream_t st, bool f16kv, const QkPostArgs &a);

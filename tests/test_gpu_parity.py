@@ -204,16 +204,22 @@ def test_prefill_fused_qkpost_equals_separate(name, n, kv16, monkeypatch):
 
 @pytest.mark.parametrize("name,n,kv16,start", [("qwen3_06b", 600, False, 0), ("qwen3_06b_q4", 700, False, 0),
                                                ("qwen3_06b", 1100, True, 0), ("qwen3_06b", 600, False, 640),
-                                               ("qwen3_06b", 500, False, 600)])
+                                               ("qwen3_06b", 500, False, 600), ("qwen3_06b", 320, False, 0),
+                                               ("qwen3_06b_q4", 300, False, 0), ("smollm2_135m", 1000, True, 0),
+                                               ("qwen25_05b", 300, False, 0), ("smollm2_135m", 200, False, 128)])
 def test_prefill_fused_kv_images_equal_kvsplit(name, n, kv16, start, monkeypatch):
-    """The fused q|k|v product of a pass that starts on a 64-key tile also
-    writes the pass's own K/V tile images for the matrix-core attention
-    (k_pf_kvsplit then converts only the earlier tiles).  The images are
-    k_pf_kvsplit's bytes, so logits and the last layer's K/V rows equal those
-    of EHIP_PF_KVIMG=0 bit for bit: Q8_0 and Q4_0 weights, fp32 (hi/lo planes
-    and per-key exponents) and fp16 caches, a continuation pass at position
-    640 (tiles 0..9 converted, 10.. fused) and one at 600 (not on a tile
-    boundary: every tile converted)."""
+    """The fused q|k|v products (k_gemm_mfma's EPI_QKPOST form for longer
+    passes with 128-dim heads, k_gemm_qkv for short prompts and 64-dim heads)
+    of a pass that starts on a 64-key tile also write the pass's own K/V tile
+    images for the matrix-core attention (k_pf_kvsplit then converts only the
+    earlier tiles).  The images are k_pf_kvsplit's bytes, so logits and the
+    last layer's K/V rows equal those of EHIP_PF_KVIMG=0 bit for bit: Q8_0
+    and Q4_0 weights, fp32 (hi/lo planes and per-key exponents) and fp16
+    caches, head dims 128 and 64 (SmolLM2-135M and Qwen2.5-0.5B shapes),
+    passes whose last tile is partial (its rest repeats the last key),
+    continuation passes at positions 640 and 128 (earlier tiles converted,
+    the pass's fused) and one at 600 (not on a tile boundary: every tile
+    converted)."""
     path = configs.model_path(name, threads=16)
     V, L = configs.ALL[name]["vocab_size"], configs.ALL[name]["n_layers"]
     rng = np.random.default_rng(n + start)

@@ -27,6 +27,8 @@
 // Roofline: VALU-bound, 2 * hd multiply-adds per (head, token, key) pair,
 // each as a separately rounded multiply and add like the reference's
 // -ffp-contract=off build.
+#include <cstdlib>
+
 #include "kernels.h"
 #include "flimg.h"
 
@@ -1143,19 +1145,30 @@ __device__ __forceinline__ void fl_load_lds(const uint8_t *src, uint8_t *dst) {
 //   issued into kimg; softmax; wait for this tile's V part; barrier; P.V from
 //   vimg; wait for the next K part; barrier; the next tile's V part issued.
 // Each part's loads land while the other part's products run.
-template <int HD, bool F16>
-__global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
+// KS = 2 (grids of fewer workgroups than CUs: short passes): two groups of
+// RW waves per workgroup take the same 16 RW rows over alternate key tiles
+// (group g tiles g, g + 2, ...), each with its own staging buffers and
+// running softmax, and group 0 merges group 1's state (maximum, sums,
+// accumulators through LDS) before the output; the barriers stay uniform.
+// RW = 2 halves the rows per workgroup, so the grid doubles onto idle CUs.
+template <int HD, bool F16, int KS, int RW>
+__global__ __launch_bounds__(64 * RW * KS) void k_pf_flash16(AttnArgs a) {
     using I = FlImg<HD, F16>;
     constexpr int NQ = HD / 32;         // 32-dim steps of a score product
     constexpr int ND = HD / 16;         // 16-dim output products
-    constexpr int BR = FL_BR;                            // rows per workgroup
-    constexpr int KE_N = (I::KE_SLABS + NWAVE - 1) / NWAVE, KE_MIN = I::KE_SLABS / NWAVE;   // K-part slabs per wave
-    constexpr int V_N = I::V_SLABS / NWAVE;
-    static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64 && I::V_SLABS % NWAVE == 0, "tile shape");
-    __shared__ __align__(16) uint8_t kimg[I::KE_SLABS * I::SLAB];   // K planes, exponents, slab padding
-    __shared__ __align__(16) uint8_t vimg[I::VBYTES];
+    constexpr int GT = 64 * RW;                          // threads per key-tile group
+    constexpr int BR = 16 * RW;                          // rows per workgroup
+    constexpr int KE_N = (I::KE_SLABS + RW - 1) / RW, KE_MIN = I::KE_SLABS / RW;   // K-part slabs per wave
+    constexpr int V_N = I::V_SLABS / RW;
+    static_assert(HD % 32 == 0 && FL_BK == 64 && FL_BR == 64 && I::V_SLABS % RW == 0 && (RW == 4 || KS == 2),
+                  "tile shape");
+    static_assert(KS == 1 || KS == 2, "one or two key-tile groups");
+    __shared__ __align__(16) uint8_t kimgs[KS][I::KE_SLABS * I::SLAB];   // K planes, exponents, slab padding
+    __shared__ __align__(16) uint8_t vimgs[KS][I::VBYTES];
+    const int grp = KS == 1 ? 0 : (int)threadIdx.x / GT;   // key-tile group
+    uint8_t *kimg = kimgs[grp], *vimg = vimgs[grp];
     const int *kex = reinterpret_cast<const int *>(kimg + I::KBYTES), *vex = kex + FL_BK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = KS == 1 ? (int)threadIdx.x : (int)threadIdx.x % GT, lane = tid & 63, wave = tid >> 6;
     const int i = lane & 15, q = lane >> 4;
     const int g = blockIdx.x;
     const int G = a.n_heads / a.n_kv, nrows = a.n_tok * G;
@@ -1205,7 +1218,7 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
         const uint8_t *src = gimg + (size_t)kt * I::HBYTES;
 #pragma unroll
         for (int u = 0; u < KE_N; u++) {
-            const int sl = wave + NWAVE * u;
+            const int sl = wave + RW * u;
             if (u < KE_MIN || sl < I::KE_SLABS)
                 fl_load_lds(src + min(sl * I::SLAB + 16 * lane, I::KE - 16), kimg + sl * I::SLAB);
         }
@@ -1214,24 +1227,29 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
         const uint8_t *src = gimg + (size_t)kt * I::HBYTES + I::KE;
 #pragma unroll
         for (int u = 0; u < V_N; u++) {
-            const int sl = wave + NWAVE * u;
+            const int sl = wave + RW * u;
             fl_load_lds(src + sl * I::SLAB + 16 * lane, vimg + sl * I::SLAB);
         }
     };
-    stage_ke(0);
-    stage_v(0);
+    const int nkt = kend / FL_BK + 1, nit = (nkt + KS - 1) / KS;
+    if (grp < nkt) {
+        stage_ke(grp);
+        stage_v(grp);
+    }
     __builtin_amdgcn_s_waitcnt(fl_vmcnt(0));
     __syncthreads();
 
-    const int nkt = kend / FL_BK + 1;
-    for (int kt = 0; kt < nkt; kt++) {
-        const int k0 = kt * FL_BK;
-        const bool more = kt + 1 < nkt;
-
+    for (int it = 0; it < nit; it++) {
+        // this group's tile kt (act: it has one); `more`: another iteration
+        // follows (uniform: the barriers); gmore: this group has a tile in it
+        const int kt = it * KS + grp, k0 = kt * FL_BK;
+        const bool act = KS == 1 || kt < nkt, more = it + 1 < nit, gmore = KS == 1 ? more : kt + KS < nkt;
         // ---- S'^T: sc[2t + b][r] = S'[row i][key k0 + 32t + 8q + 4b + r]
         f32x4 sc[4];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) sc[kk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        int kx[2][8], vx[2][8];   // the per-key exponents of this lane's 16 keys
+        if (act) {
 #pragma unroll
         for (int s = 0; s < NQ; s++) {
             f16x8 kh[4], kl[4];
@@ -1249,8 +1267,6 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) sc[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[kk], qh[s], sc[kk], 0, 0, 0);
         }
-        // the per-key exponents of this lane's 16 keys
-        int kx[2][8], vx[2][8];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -1265,10 +1281,13 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
                     vx[t][4 * u] = va.x; vx[t][4 * u + 1] = va.y; vx[t][4 * u + 2] = va.z; vx[t][4 * u + 3] = va.w;
                 }
             }
+        }
         if (more) {   // every wave is past its kimg reads: the next tile's K part may land
             fl_sync();
-            stage_ke(kt + 1);
+            if (gmore) stage_ke(kt + KS);
         }
+        f16x8 ph[2], pl[2];
+        if (act) {
         // running softmax of the row (log2 units); keys past the row's position
         // are masked (only in tiles that reach past the workgroup's first row)
         float mx = -INFINITY;
@@ -1293,8 +1312,11 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
         };
         if (k0 + FL_BK - 1 <= kfirst) scores(FlMask<false>{});
         else scores(FlMask<true>{});
-        const float mn = fmaxf(m, fl_quarter_max(mx));   // finite: key 0 is in the first tile
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first tile (m = -inf)
+        // finite: key 0 is in the first tile (KS = 2: group 1's first tile can
+        // hide every key from a row; its maximum stays -inf and mz stands in)
+        const float mn = fmaxf(m, fl_quarter_max(mx));
+        const float mz = KS == 1 || mn != -INFINITY ? mn : 0.0f;
+        const float alpha = __builtin_amdgcn_exp2f(m - mz);   // 0 on the first tile (m = -inf)
         m = mn;
         lsum *= alpha;
         int emin = -(int)fl_quarter_max(-(float)el);
@@ -1303,24 +1325,25 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
         ecur = emin;
 #pragma unroll
         for (int d = 0; d < ND; d++) o[d] *= of;
-        f16x8 ph[2], pl[2];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int t = kk >> 1, jj = 4 * (kk & 1) + r;
-                const float p = __builtin_amdgcn_exp2f(sc[kk][r] - mn);   // masked: 2^-inf = 0
+                const float p = __builtin_amdgcn_exp2f(sc[kk][r] - mz);   // masked: 2^-inf = 0
                 lsum += p;
                 const float x = __builtin_amdgcn_ldexpf(p, 14 + emin - vx[t][jj]);
                 ph[t][jj] = (_Float16)x;
                 pl[t][jj] = (_Float16)(x - (float)ph[t][jj]);
             }
-        if (kt > 0) {   // this tile's V part, issued before the next tile's K part
-            if (more) __builtin_amdgcn_s_waitcnt(fl_vmcnt(KE_MIN));
+        }
+        if (it > 0) {   // this tile's V part, issued before the next tile's K part
+            if (gmore) __builtin_amdgcn_s_waitcnt(fl_vmcnt(KE_MIN));
             else __builtin_amdgcn_s_waitcnt(fl_vmcnt(0));
             fl_sync();
         }
         // ---- O''^T += V'^T . P''^T over keys 32t + 8q + jj
+        if (act)
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             f16x8 vh[ND], vl[ND];
@@ -1341,16 +1364,46 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
         if (more) {   // the next K part has landed and every wave is past its vimg reads
             __builtin_amdgcn_s_waitcnt(fl_vmcnt(0));
             fl_sync();
-            stage_v(kt + 1);
+            if (gmore) stage_v(kt + KS);
         }
     }
     // o[d][r] = 2^(14 + ecur) O^T[dim 16d + 4q + r][row i]
-    const float inv = 1.0f / fl_quarter_sum(lsum);
-    const int un = -(14 + ecur);
+    if constexpr (KS == 2) {
+        // group 1's state into group 0's: with M the larger maximum, each
+        // group's sums and accumulators (unscaled) weighted by 2^(m - M)
+        __syncthreads();   // every wave is past its last image reads
+        float *mo = reinterpret_cast<float *>(&vimgs[0][0]), *ms = reinterpret_cast<float *>(kimgs[1]);
+        static_assert(ND * 4 * GT * 4 <= KS * I::VBYTES && 3 * GT * 4 <= I::KE_SLABS * I::SLAB, "merge fits the images");
+        if (grp == 1) {
 #pragma unroll
-    for (int d = 0; d < ND; d++)
+            for (int d = 0; d < ND; d++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) o[d][r] = __builtin_amdgcn_ldexpf(o[d][r], un) * inv;
+                for (int r = 0; r < 4; r++) mo[(4 * d + r) * GT + tid] = o[d][r];
+            ms[tid] = m;
+            ms[GT + tid] = lsum;
+            ms[2 * GT + tid] = __int_as_float(ecur);
+        }
+        __syncthreads();
+        if (grp == 1) return;
+        const float m1 = ms[tid], l1 = ms[GT + tid];
+        const int e1 = __float_as_int(ms[2 * GT + tid]);
+        const float mm = fmaxf(m, m1);   // finite: group 0 holds key 0
+        const float a0 = __builtin_amdgcn_exp2f(m - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+        const float inv = 1.0f / fl_quarter_sum(lsum * a0 + l1 * a1);
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                o[d][r] = (__builtin_amdgcn_ldexpf(o[d][r], -(14 + ecur)) * a0 +
+                           __builtin_amdgcn_ldexpf(mo[(4 * d + r) * GT + tid], -(14 + e1)) * a1) * inv;
+    } else {
+        const float inv = 1.0f / fl_quarter_sum(lsum);
+        const int un = -(14 + ecur);
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[d][r] = __builtin_amdgcn_ldexpf(o[d][r], un) * inv;
+    }
     const bool live = r0 + wave * 16 + i < nrows;
     const size_t col = (size_t)(g * G + h) * HD + 4 * q;
     const size_t row = (size_t)b * a.n_heads * HD;
@@ -1399,6 +1452,12 @@ __global__ __launch_bounds__(WG) void k_pf_flash16(AttnArgs a) {
     }
 }
 
+// (host) integer environment switch, dflt when unset
+static int env_int_attn(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
 int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *quantized) {
     if (quantized) *quantized = false;
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0 || a.n_tok <= 0 || a.q_stride % 4) return -1;
@@ -1414,9 +1473,22 @@ int launch_attention_mfma(hipStream_t st, bool f16kv, const AttnArgs &a, bool *q
         const int nks = a.kvimg_fused ? a.pos_base / FL_BK : nkt;
         if (quantized) *quantized = a.qx != nullptr;
         const dim3 sgrid(a.n_kv, nks);
+        // grids of up to one 64-row workgroup per CU (two for 64-dim heads,
+        // whose images take half the LDS): 32-row workgroups of two key-tile
+        // groups, twice the grid (Qwen3-0.6B shape pp512 3.17 -> 3.00 ms,
+        // pp1024 4.67 -> 4.52; SmolLM2-135M shape pp1024 2.87 -> 2.63,
+        // pp3072 6.25 -> 5.91; pp1536 with 128-dim heads, 384 workgroups,
+        // 6.63 -> 6.95 ms: there the one-group tiles stay).  Measured and
+        // dropped: 8-wave workgroups of two groups over the same 64 rows
+        // (3.11 ms at pp512: the grid still covered half the CUs).
+        // EHIP_PF_FLASH_KS=1 keeps the one-group kernel.
+        const long gmax = a.hd == 64 ? 512 : 256;
+        const bool ks2 = (long)grid.x * grid.y <= gmax && env_int_attn("EHIP_PF_FLASH_KS", 2) == 2;
+        const dim3 grid2(a.n_kv, (a.n_tok * G + 31) / 32);
 #define FL16(H, F)                                                                         \
     if (nks > 0) hipLaunchKernelGGL((k_pf_kvsplit<H, F>), sgrid, dim3(WG), 0, st, a);     \
-    hipLaunchKernelGGL((k_pf_flash16<H, F>), grid, dim3(WG), 0, st, a);
+    if (ks2) hipLaunchKernelGGL((k_pf_flash16<H, F, 2, 2>), grid2, dim3(WG), 0, st, a);   \
+    else hipLaunchKernelGGL((k_pf_flash16<H, F, 1, 4>), grid, dim3(WG), 0, st, a);
         if (a.hd == 64) {
             if (f16kv) { FL16(64, true) } else { FL16(64, false) }
         } else {

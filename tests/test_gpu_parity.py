@@ -192,14 +192,14 @@ def test_prefill_fused_qkpost_equals_separate(name, n, kv16, monkeypatch):
         if n == 2000:
             np.testing.assert_array_equal(a, b)
             continue
-        # two block-sum orders of the products: within the bar this model's
-        # logits meet against the oracle (set by the reference builds' own
-        # spread at this shape: about 4e-2 max-abs, 1.4e-2 relative L2)
+        # two block-sum orders of the products, each within the bar this
+        # model's logits meet against the oracle (set by the reference
+        # builds' own spread at this shape): so within twice it of each other
         b_ = bars("qwen3_06b-p16-d32-s11")
         if a.dtype == np.uint8:   # cache rows
             a, b = (x.view(np.float16 if kv16 else np.float32).astype(np.float32) for x in (a, b))
         r = compare(np.ravel(a), np.ravel(b))
-        assert r["max_abs"] <= b_["abs_max"] and r["rel_l2"] <= b_["rel_max"], (r, b_)
+        assert r["max_abs"] <= 2 * b_["abs_max"] and r["rel_l2"] <= 2 * b_["rel_max"], (r, b_)
 
 
 @pytest.mark.parametrize("name,n,kv16,start", [("qwen3_06b", 600, False, 0), ("qwen3_06b_q4", 700, False, 0),
@@ -237,6 +237,42 @@ def test_prefill_fused_kv_images_equal_kvsplit(name, n, kv16, start, monkeypatch
         eng.close()
     for a, b in zip(out[0], out[1]):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("name,n,kv16,start", [("qwen3_06b", 512, False, 0), ("qwen3_06b_q4", 300, True, 0),
+                                               ("smollm2_135m", 1000, False, 0), ("qwen25_05b", 256, False, 0),
+                                               ("qwen3_06b", 200, False, 320)])
+def test_prefill_split_attention_matches_one_group(name, n, kv16, start, oracle_threads, monkeypatch):
+    """Passes whose matrix-core attention grid would leave CUs idle run
+    k_pf_flash16 on 32-row workgroups of two key-tile groups (alternate
+    tiles, running softmax states merged at the end).  Its summation order is
+    not the one-group kernel's (EHIP_PF_FLASH_KS=1), so the two agree within
+    the bar the model's logits meet against the oracle, as each of them does
+    against the oracle itself: Q8_0 and Q4_0 weights,
+    fp32 and fp16 caches, 128- and 64-dim heads, 1, 2, 3 and 7 query heads
+    per kv head, a continuation pass at position 320."""
+    path = configs.model_path(name, threads=16)
+    V = configs.ALL[name]["vocab_size"]
+    rng = np.random.default_rng(n + start)
+    pre, ids = rng.integers(0, V, start), rng.integers(0, V, n)
+    say(f"{name} pp{n} at {start} kv16={kv16}: split-group prefill attention")
+    out = []
+    for ks in ("1", "2"):
+        monkeypatch.setenv("EHIP_PF_FLASH_KS", ks)
+        eng = emberllm.Engine(path, ctx=start + n + 8, kv_fp16=kv16)
+        if start:
+            eng.prefill(pre)
+        out.append(eng.prefill(ids, start))
+        eng.close()
+    orc = oracle.Oracle(path, ctx=start + n + 8, kv_fp16=kv16)
+    if start:
+        orc.prefill(pre)
+    ref = orc.prefill(ids, start)
+    orc.close()
+    b = bars(f"{name}-p16-d32-s11")
+    for r, k in ((compare(out[1], ref), 1), (compare(out[0], ref), 1), (compare(out[1], out[0]), 2)):
+        # each path within the bar of the oracle; the two within twice it
+        assert r["finite"] and r["max_abs"] <= k * b["abs_max"] and r["rel_l2"] <= k * b["rel_max"], (r, b)
 
 
 @pytest.mark.parametrize("name", ["t_qwen3", "t_llama"])

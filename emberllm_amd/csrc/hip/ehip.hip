@@ -364,12 +364,13 @@ constexpr size_t PF_SCORES_MAX = (size_t)1 << 30;   // bytes of attention scores
 // deterministic build to rounding: its passes of up to PF_EXACT_KEYS keys
 // use the exact-order kernels.  Wider models split their longer block sums
 // over pipelines (and sum decode products across lanes), so they run at the
-// reference builds' own noise floor in any case: their attention uses the
-// one-kernel exact form where it is the faster (passes of up to
-// PF_FUSE_KEYS keys over at least PF_FUSE_MIN_WG workgroups) and matrix
-// cores otherwise.
+// reference builds' own noise floor in any case: their attention runs on
+// the matrix cores at every length (the one-kernel exact form, once the
+// faster for passes of up to PF_FUSE_KEYS keys over at least 256
+// workgroups, lost to the split key-tile attention: Qwen3-0.6B shape pp128
+// 1.90 -> 1.82 ms, pp256 2.79 -> 2.50, stories110M shape pp128 0.62 ->
+// 0.61; EHIP_PF_ATTN=exact still selects it).
 constexpr int PF_EXACT_KEYS = 512;
-constexpr int PF_FUSE_MIN_WG = 256;
 constexpr int PF_GRAPHS = 8;   // prefill pass graphs kept per state
 enum { PF_AUTO = 0, PF_EXACT = 1, PF_MFMA = 2 };
 
@@ -1240,8 +1241,7 @@ static int enq_prefill_pass(EhipState *s, int pos0, int mt, bool last, int pass)
             p.n_kv = c.n_kv_heads; p.pos_base = pos0; p.n_tok = mt;
             bool exact = s->pf_mode == PF_EXACT;
             if (s->pf_mode == PF_AUTO)
-                exact = s->pf_seq ? pos0 + mt <= PF_EXACT_KEYS
-                                  : pos0 + mt <= PF_FUSE_KEYS && (long)c.n_kv_heads * ((mt + 3) / 4) >= PF_FUSE_MIN_WG;
+                exact = s->pf_seq && pos0 + mt <= PF_EXACT_KEYS;
             bool img_fused = false;   // the q|k|v product wrote the pass's K/V tile images
             // the matrix-core attention's K/V tile images of the pass, in the
             // fused q|k|v epilogues (EHIP_PF_KVIMG=0 leaves them to

@@ -1536,15 +1536,17 @@ constexpr int GS_U16_MAX_GRID = 128;
 // workgroups) runs two full rounds of 64-token tiles instead of one and a
 // third (pp4096 19.95 -> 19.55 ms).  Products over at least GEMM_SPLIT_MIN_K
 // inputs take the fused block scaling (see k_gemm_mfma), and Q8_0 64-token
-// grids of at most two workgroups per CU split K over two pipelines
-// (Qwen3-0.6B shape: pp512 3.93 -> 3.78 ms, pp1024 5.85 -> 5.78, pp4096
-// 18.81 -> 18.72).
+// grids of fewer than two workgroups per CU split K over two pipelines
+// (Qwen3-0.6B shape: pp512 3.93 -> 3.78 ms, pp1024 5.85 -> 5.78; with the
+// matrix-core scale products the 512-workgroup wo and w2 of pp4096 no
+// longer gain from it, 15.68 -> 15.56 ms without, while pp2048's 256 still
+// do, 8.11 -> 7.76 ms).
 static void mfma_shape(long gu, int n, int cols, bool *t64, bool *fused, bool *sp2) {
     const long g128 = gu * ((n + 127) / 128), gt64 = gu * ((n + 63) / 64);
     auto fill = [](long g, long slots) { return (double)g / (double)(((g + slots - 1) / slots) * slots); };
     *t64 = g128 < 512 || fill(gt64, 4 * 256) > fill(g128, 3 * 256) + 0.1;
     *fused = cols >= GEMM_SPLIT_MIN_K;
-    *sp2 = *fused && *t64 && gt64 <= 2 * 256;
+    *sp2 = *fused && *t64 && gt64 < 2 * 256;
 }
 
 int launch_gemm(hipStream_t st, int epi, const GemmArgs &a) {
